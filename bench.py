@@ -1,0 +1,271 @@
+"""Benchmark of the quantized-weight matmul path on one MI355X.
+
+Headline (value): matmulQ4 decode GEMV, M=1, Smith weight [K=4096, N=4096]
+quantized with quantizeQ4, weights resident in HBM.
+A step = one matmulQ4 call (activation prep + MFMA GEMV).  The K timed steps
+rotate over >= 400 MB of distinct weight copies so the 256 MB MALL cannot
+serve them.  value = algorithmic bytes per step / time per step (GB/s);
+roofline.achieved = algorithmic bytes / average duration of the GEMV kernel,
+from HIP events recorded around every GEMV launch on the stream it runs on.
+
+Also measured in the same run (under "configs"): Q4_0 GEMV (GGUF format),
+Q8 GEMV [4096 x 14336] (config 2), the Q4 batched-decode sweep (config 3),
+the Q4 prefill shapes (config 4), and the CPU baseline: the oracle's
+dequantize + f32 matmul (single thread) on a bounded sample of config 1.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 400 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def q4s_bytes(K, N):
+    return (K + 31) // 32 * N * 24
+
+
+def q8_bytes(K, N):
+    return (K + 31) // 32 * N * 34
+
+
+def q40_bytes(K, N):
+    return K // 32 * N * 18
+
+
+def alg_bytes(wbytes, M, K, N):
+    return wbytes + 4 * M * K + 4 * M * N
+
+
+class Weights:
+    """R device copies of one quantized weight (R chosen to exceed the MALL)."""
+
+    def __init__(self, D, buf, nbytes, extra=None):
+        self.nbytes = nbytes
+        reps = max(2, -(-ROTATE_BYTES // nbytes))
+        self.bufs = [buf]
+        self.extra = [extra] if extra is not None else None
+        for _ in range(reps - 1):
+            b = D.alloc(nbytes)
+            D.check(D.lib.smith_copy_d2d(D.ops_ctx(), b, 0, buf, 0, nbytes))
+            self.bufs.append(b)
+            if extra is not None:
+                eb = D.alloc(extra[1])
+                D.check(D.lib.smith_copy_d2d(D.ops_ctx(), eb, 0, extra[0], 0, extra[1]))
+                self.extra.append((eb, extra[1]))
+        D.sync()
+
+
+def time_steps(D, step, steps, warmup):
+    """Returns (ms per step, {kernel-prefix: avg ms}) for `steps` timed calls."""
+    for i in range(warmup):
+        step(i)
+    D.sync()
+    D.timer_start()
+    for i in range(steps):
+        step(i)
+    ms = D.timer_stop()
+    # second pass with per-launch events for the kernel durations
+    D.profile_kernels(True)
+    for i in range(steps):
+        step(i)
+    gemv_ms, gemv_n = D.profile_read("smith_qgemv")
+    prep_ms, prep_n = D.profile_read("smith_qprep")
+    D.profile_kernels(False)
+    D.profile_read("")
+    return ms / steps, {"gemv_ms": gemv_ms / max(gemv_n, 1), "prep_ms": prep_ms / max(prep_n, 1),
+                        "gemv_launches_per_step": gemv_n / steps}
+
+
+_Q4S_CACHE = {}
+
+
+def q4s_weights(D, S, prng, K, N):
+    if (K, N) not in _Q4S_CACHE:
+        q = S.quantizeQ4(prng.randn((K, N), 1, std=0.02))
+        _Q4S_CACHE[(K, N)] = Weights(D, q["buffer"], q["totalBytes"])
+    return _Q4S_CACHE[(K, N)]
+
+
+def bench_q4s(D, S, prng, M, K, N, steps, warmup):
+    W = q4s_weights(D, S, prng, K, N)
+    a = S.tensor(prng.randn((M, K), 0))
+    out = S.create([M, N])
+    ctx = D.ops_ctx()
+    G = (K + 31) // 32
+    bufs = W.bufs
+
+    def step(i):
+        D.lib.smith_matmul_q4(ctx, a.buffer, bufs[i % len(bufs)], out.buffer, M, N, K, G)
+
+    ms, kt = time_steps(D, step, steps, warmup)
+    return ms, kt, alg_bytes(q4s_bytes(K, N), M, K, N)
+
+
+def bench_q8(D, S, prng, M, K, N, steps, warmup):
+    q = S.quantizeQ8(prng.randn((K, N), 1, std=0.02))
+    W = Weights(D, q["buffer"], q["totalBytes"])
+    a = S.tensor(prng.randn((M, K), 0))
+    out = S.create([M, N])
+    ctx = D.ops_ctx()
+    G = (K + 31) // 32
+    bufs = W.bufs
+
+    def step(i):
+        D.lib.smith_matmul_q8(ctx, a.buffer, bufs[i % len(bufs)], out.buffer, M, N, K, G)
+
+    ms, kt = time_steps(D, step, steps, warmup)
+    for b in bufs[1:]:
+        D.release_buffer(b)
+    return ms, kt, alg_bytes(q8_bytes(K, N), M, K, N)
+
+
+def bench_q40(D, S, prng, M, K, N, steps, warmup):
+    ctx = D.ops_ctx()
+    x = S.tensor(prng.randn((N, K), 1, std=0.02))  # GGUF listing [out, in]
+    G = K // 32
+    blocks = D.alloc(N * G * 18)
+    D.check(D.lib.smith_quantize_q4_0(ctx, x.buffer, blocks, N, K))
+    nib = D.alloc(N * G * 16)
+    dsc = D.alloc(N * G * 2)
+    D.check(D.lib.smith_repack_q4_0(ctx, blocks, nib, dsc, N, K))
+    W = Weights(D, nib, N * G * 16, extra=(dsc, N * G * 2))
+    a = S.tensor(prng.randn((M, K), 0))
+    out = S.create([M, N])
+
+    def step(i):
+        j = i % len(W.bufs)
+        D.lib.smith_matmul_q4_0(ctx, a.buffer, W.bufs[j], W.extra[j][0], out.buffer, M, N, K)
+
+    ms, kt = time_steps(D, step, steps, warmup)
+    return ms, kt, alg_bytes(q40_bytes(K, N), M, K, N)
+
+
+def cpu_baseline(K, N, budget_s):
+    """Oracle dequantize + f32 matmul (the reference's CPU semantics), 1 thread."""
+    from oracle import oracle as O
+    from smith_amd import prng
+    w = prng.randn((K, N), 1, std=0.02)
+    a = prng.randn((1, K), 0)
+    q = O.quantize_q4s(w)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.matmul_f32(a, O.dequant_q4s(q, K, N))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and reps >= 2:
+            break
+    per = el / reps
+    return {"value": round(alg_bytes(q4s_bytes(K, N), 1, K, N) / per / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": "%d x [oracle_dequant_q4s + oracle_matmul_f32] on config 1 (M=1, K=N=4096), %.1f s, "
+                      "%.1f ms/call; host has %d cpus" % (reps, el, per * 1e3, os.cpu_count() or 0)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only, no sweep / cpu baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (--gpus %d requested); the sharding design is "
+              "described in DESIGN.md" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import smith_amd as S
+    from smith_amd import device as D
+    from smith_amd import prng
+
+    D.ops_ctx()
+    log("device:", D.device_name())
+    K = N = 4096
+    ms, kt, nbytes = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup)
+    value = nbytes / (ms * 1e-3) / 1e9
+    achieved = nbytes / (kt["gemv_ms"] * 1e-3) / 1e9
+    log("cfg1 q4s M=1: %.2f us/step (%.0f GB/s); gemv kernel %.2f us (%.0f GB/s), prep %.2f us"
+        % (ms * 1e3, value, kt["gemv_ms"] * 1e3, achieved, kt["prep_ms"] * 1e3))
+
+    configs = {}
+    if not args.quick:
+        sub = max(20, args.steps // 4)
+        ms40, kt40, b40 = bench_q40(D, S, prng, 1, K, N, sub, 5)
+        configs["cfg1_q4_0_gemv_M1_4096x4096"] = {
+            "GBps_step": round(b40 / ms40 / 1e6, 1), "GBps_kernel": round(b40 / kt40["gemv_ms"] / 1e6, 1),
+            "us_step": round(ms40 * 1e3, 2), "us_kernel": round(kt40["gemv_ms"] * 1e3, 2)}
+        ms8, kt8, b8 = bench_q8(D, S, prng, 1, 4096, 14336, sub, 5)
+        configs["cfg2_q8_gemv_M1_K4096_N14336"] = {
+            "GBps_step": round(b8 / ms8 / 1e6, 1), "GBps_kernel": round(b8 / kt8["gemv_ms"] / 1e6, 1),
+            "us_step": round(ms8 * 1e3, 2), "us_kernel": round(kt8["gemv_ms"] * 1e3, 2)}
+        log("cfg2:", configs["cfg2_q8_gemv_M1_K4096_N14336"])
+        sweep = {}
+        for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
+            for M in (1, 4, 8, 16, 32):
+                msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, sub, 5)
+                sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = {
+                    "GBps_step": round(bx / msx / 1e6, 1), "GBps_kernel": round(bx / ktx["gemv_ms"] / 1e6, 1),
+                    "us_kernel": round(ktx["gemv_ms"] * 1e3, 2)}
+        configs["cfg3_q4s_batched_decode"] = sweep
+        log("cfg3:", json.dumps(sweep))
+        pre = {}
+        for (Nn, Kk) in [(14336, 4096), (4096, 14336)]:
+            for M in (512, 2048):
+                msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, 3, 1)
+                fl = 2.0 * M * Nn * Kk
+                pre["M%d_N%d_K%d" % (M, Nn, Kk)] = {"TFLOPs_step": round(fl / msx / 1e9, 2),
+                                                   "mfma_util_vs_f16_dense": round(fl / msx / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
+                                                   "ms_step": round(msx, 3),
+                                                   "path": "GEMV in 32-row chunks (MFMA prefill GEMM not built yet)"}
+        configs["cfg4_q4s_prefill"] = pre
+        log("cfg4:", json.dumps(pre))
+
+    cpu = None
+    if not args.quick:
+        cpu = cpu_baseline(K, N, args.cpu_seconds)
+        log("cpu baseline:", cpu)
+
+    line = {
+        "metric": "Q4 GEMV GB/s (% HBM peak) + Q4 decode tokens/sec, 1 MI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (Q4S weights; exact f16 hi/lo MFMA, f32 accumulation)",
+        "data": "synthetic (SplitMix64/Box-Muller seeded: a~N(0,1) seed 0, W~N(0,0.02) seed 1)",
+        "config": {"workload": "config 1: matmulQ4 GEMV M=1, Smith weight [K=4096, N=4096] quantizeQ4 (Q4S, "
+                               "24 B/32 weights); weights rotated over >= 400 MB of copies",
+                   "M": 1, "K": K, "N": N, "format": "Q4S", "algorithmic_bytes_per_step": nbytes},
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "smith_qgemv_q4s_m1", "kernel_us": round(kt["gemv_ms"] * 1e3, 3),
+                     "prep_kernel_us": round(kt["prep_ms"] * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

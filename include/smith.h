@@ -1,0 +1,153 @@
+/*
+ * smith.h -- C ABI of libsmith.so, the MI355X (gfx950) HIP bridge that
+ * replaces SMITH's Objective-C Metal bridge (native/gpu_bridge.h) for the
+ * quantized-weight matmul path.
+ *
+ * Plain C types only: opaque handles are void*, buffers are device pointers
+ * returned by smith_alloc (any device pointer inside such a buffer may be
+ * passed where a buffer is expected), sizes are uint64_t / uint32_t.
+ * One context = one HIP device + one HIP stream (default priority); every
+ * launch is enqueued on that stream in call order.
+ *
+ * Error convention: functions returning a pointer return NULL on failure;
+ * functions returning int return 0 on success and a negative code on
+ * failure.  smith_last_error(ctx) gives the message of the last failure.
+ */
+#ifndef SMITH_H
+#define SMITH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage modes (native/gpu_bridge.h:12-13).  Both allocate device memory
+ * (hipMalloc); SHARED is accepted for API compatibility but is NOT host
+ * visible: use smith_copy_h2d / smith_copy_d2h. */
+#define SMITH_SHARED 0
+#define SMITH_PRIVATE 1
+
+typedef struct SmithEncoder SmithEncoder;
+
+/* Timing of a timed dispatch (native/gpu_bridge.h:113-117).  gpu_start /
+ * gpu_end are seconds on the host's steady clock at submit / completion;
+ * gpu_ms is the HIP-event duration of the encoded work.  Free with
+ * smith_free. */
+typedef struct {
+  double gpu_start;
+  double gpu_end;
+  double gpu_ms;
+} SmithTiming;
+
+/* ---- lifecycle (gpu_bridge.h:18,21) ---- */
+void* smith_init(void);
+void smith_destroy(void* ctx);
+
+/* ---- device info (gpu_bridge.h:26-32) ---- */
+char* smith_device_name(void* ctx);                    /* free with smith_free */
+uint64_t smith_max_threadgroup_memory(void* ctx);      /* LDS bytes per workgroup */
+uint64_t smith_max_threads_per_threadgroup(void* ctx);
+
+/* ---- buffers (gpu_bridge.h:37-52) ---- */
+void* smith_alloc(void* ctx, uint64_t bytes, uint32_t mode);
+void* smith_buffer_contents(void* buffer);  /* always NULL: device memory is not host-mapped */
+uint64_t smith_buffer_length(void* buffer); /* 0 for a pointer not returned by smith_alloc */
+void smith_release_buffer(void* buffer);
+int64_t smith_test_release(void* ctx);
+int64_t smith_test_release_after_use(void* ctx);
+int64_t smith_buffer_retain_count(void* buffer); /* 1 while live, 0 otherwise */
+uint64_t smith_allocated_size(void* ctx);
+
+/* ---- explicit copies (new: replace Metal's shared-memory zero copy) ---- */
+int smith_copy_h2d(void* ctx, void* dst_buffer, uint64_t dst_offset, const void* src, uint64_t bytes);
+int smith_copy_d2h(void* ctx, void* dst, const void* src_buffer, uint64_t src_offset, uint64_t bytes);
+int smith_copy_d2d(void* ctx, void* dst_buffer, uint64_t dst_offset, const void* src_buffer,
+                   uint64_t src_offset, uint64_t bytes);
+int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes); /* enqueued fill kernel */
+int smith_sync(void* ctx);
+void smith_free(void* p); /* strings and SmithTiming returned by this library */
+const char* smith_last_error(void* ctx);
+
+/* ---- code objects (gpu_bridge.h:57-64) ---- */
+/* Load a gfx950 code object (.hsaco) from disk (hipModuleLoad).  The first
+ * library loaded also provides the kernels of the op-level entry points. */
+void* smith_load_library(void* ctx, const char* path);
+/* Compile HIP source for gfx950 with hipRTC and load it. */
+void* smith_compile_source(void* ctx, const char* source, char** error_out);
+void* smith_create_pipeline(void* ctx, void* library, const char* fn_name);
+
+/* ---- encoded dispatch (gpu_bridge.h:72-99) ----
+ * Buffers and inline bytes bind to argument slots by index; at dispatch the
+ * slots are packed in index order into the kernel-argument block (a buffer is
+ * an 8-byte pointer; inline bytes are aligned to 8 if their length is a
+ * multiple of 8, else to 4).  smith_dispatch follows Metal dispatchThreads:
+ * grid_* is the TOTAL thread count per dimension and the launch uses
+ * ceil(grid/group) workgroups, so kernels bound-check their indices. */
+SmithEncoder* smith_begin(void* ctx);
+void smith_set_buffer(SmithEncoder* enc, void* buffer, uint32_t index);
+void smith_set_bytes(SmithEncoder* enc, const void* data, uint32_t length, uint32_t index);
+void smith_set_pipeline(SmithEncoder* enc, void* pipeline);
+void smith_set_threadgroup_memory(SmithEncoder* enc, uint64_t length, uint32_t index);
+void smith_dispatch(SmithEncoder* enc, uint64_t grid_x, uint64_t grid_y, uint64_t grid_z,
+                    uint64_t group_x, uint64_t group_y, uint64_t group_z);
+void smith_end_sync(SmithEncoder* enc);
+void* smith_end_async(SmithEncoder* enc);
+void smith_wait(void* token);
+SmithTiming* smith_end_timed(SmithEncoder* enc);
+void smith_dispatch_sync(void* ctx, void* pipeline, void** buffers, uint32_t* indices, uint32_t buffer_count,
+                         const void* params, uint32_t params_length, uint32_t params_index, uint64_t grid_x,
+                         uint64_t grid_y, uint64_t grid_z, uint64_t group_x, uint64_t group_y,
+                         uint64_t group_z);
+
+/* ---- op-level entry points (new: one FFI call per op) ----
+ * All are enqueued on the context stream and return without waiting.
+ * Buffers are device pointers.  Formats are byte-exact with the reference. */
+
+/* quantizeQ4 (src/ops/quantize.js:14-68) on the GPU: w is f32 [K,N]
+ * row-major; out receives ceil(K/32)*N*24 bytes of Q4S records. */
+int smith_quantize_q4(void* ctx, const float* w, void* out, uint32_t K, uint32_t N);
+
+/* Q8 blocks in the layout matmulQ8 consumes (shaders/matmul_q8.metal:40-52);
+ * the reference has no Q8 quantizer, the rounding is ggml's q8_0 reference.
+ * out receives ceil(K/32)*N*34 bytes. */
+int smith_quantize_q8(void* ctx, const float* w, void* out, uint32_t K, uint32_t N);
+
+/* matmulQ4 (src/ops/quantize.js:71-90): out[M,N] = a[M,K] . deq(wq). */
+int smith_matmul_q4(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
+                    uint32_t K, uint32_t groups);
+
+/* matmulQ8 (src/ops/quantize.js:99-118): out[M,N] = a[M,K] . deq(wq). */
+int smith_matmul_q8(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
+                    uint32_t K, uint32_t groups);
+
+/* GGUF Q4_0 weight (src/gguf.js:187-197), listed [out=N, in=K] in the file
+ * (K % 32 == 0).  smith_repack_q4_0 moves the N*K/32 18-byte blocks into the
+ * planar layout the GEMV reads (nib: N*K/2 bytes, d: N*K/32 f16) without
+ * changing a byte; smith_matmul_q4_0 computes out[M,N] = a[M,K] . W^T, the
+ * product gguf_loader.js:243-253 forms after transposing an [out,in] weight. */
+int smith_repack_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K);
+int smith_matmul_q4_0(void* ctx, const float* a, const void* nib, const void* d, float* out, uint32_t M,
+                      uint32_t N, uint32_t K);
+
+/* GGUF Q4_0 encoder (ggml q4_0 rounding, the reference decoder's interleaved
+ * nibble order) for a row-major f32 [rows, cols] matrix, cols % 32 == 0.
+ * Used to write synthetic GGUF files; out receives rows*cols/32*18 bytes. */
+int smith_quantize_q4_0(void* ctx, const float* x, void* out, uint32_t rows, uint32_t cols);
+
+/* ---- timing on the context stream (HIP events) ---- */
+/* While enabled, every op-level kernel launch is bracketed by a HIP event
+ * pair on the context stream.  smith_profile_read waits for the stream and
+ * returns (then forgets) the summed duration and count of the recorded
+ * launches whose kernel name starts with prefix (all if prefix is NULL/""). */
+int smith_profile_kernels(void* ctx, int enable);
+int smith_profile_read(void* ctx, const char* prefix, double* total_ms, uint64_t* count);
+int smith_timer_start(void* ctx);
+/* Waits for the stream; returns milliseconds since smith_timer_start, <0 on error. */
+double smith_timer_stop(void* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,208 @@
+"""ctypes front end of the CPU oracle (oracle/smith_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.  Each wrapper
+names the reference file:line its C function restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+Q4S_BYTES = 24
+Q8_BYTES = 34
+Q4_0_BYTES = 18
+GGML_Q4_0 = 2
+GGML_Q8_0 = 8
+
+
+def build():
+    subprocess.check_call(["make", "-s", "-C", _HERE])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        I = ctypes.c_int64
+        for name, args, res in [
+            ("oracle_from_f16", [ctypes.c_uint16], ctypes.c_double),
+            ("oracle_to_f16_trunc", [ctypes.c_float], ctypes.c_uint16),
+            ("oracle_f32_to_f16_rne", [ctypes.c_float], ctypes.c_uint16),
+            ("oracle_quantize_q4s", [P, I, I, P], None),
+            ("oracle_dequant_q4s", [P, I, I, P], None),
+            ("oracle_quantize_q8", [P, I, I, P], None),
+            ("oracle_dequant_q8", [P, I, I, P], None),
+            ("oracle_dequant_q4_0_block", [P, P], None),
+            ("oracle_dequant_q8_0_block", [P, P], None),
+            ("oracle_dequantize_tensor", [ctypes.c_int, P, I, P], ctypes.c_int),
+            ("oracle_quantize_rows", [ctypes.c_int, P, I, I, P], ctypes.c_int),
+            ("oracle_matmul_f64acc", [P, P, I, I, I, P], None),
+            ("oracle_matmul_f32", [P, P, I, I, I, P], None),
+            ("oracle_matmul_q4s", [P, P, I, I, I, P], None),
+            ("oracle_matmul_q8", [P, P, I, I, I, P], None),
+            ("oracle_matmul_gguf", [ctypes.c_int, P, P, I, I, I, P], ctypes.c_int),
+        ]:
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def from_f16(h):
+    """fromFloat16, src/gguf.js:398-408."""
+    return lib().oracle_from_f16(int(h))
+
+
+def to_f16_trunc(x):
+    """toFloat16, src/dtype.js:29-58 (truncating)."""
+    return lib().oracle_to_f16_trunc(float(x))
+
+
+def f32_to_f16_rne(x):
+    return lib().oracle_f32_to_f16_rne(float(x))
+
+
+def quantize_q4s(w):
+    """quantizeQ4, src/ops/quantize.js:14-68 -> Q4S bytes."""
+    w = _f32(w)
+    K, N = w.shape
+    groups = (K + 31) // 32
+    out = np.zeros(groups * N * Q4S_BYTES, dtype=np.uint8)
+    lib().oracle_quantize_q4s(_p(w), K, N, _p(out))
+    return out
+
+
+def dequant_q4s(q, K, N):
+    """dequant_q4, shaders/matmul_q4.metal:24-28 -> f32 [K,N]."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    w = np.empty((K, N), dtype=np.float32)
+    lib().oracle_dequant_q4s(_p(q), K, N, _p(w))
+    return w
+
+
+def quantize_q8(w):
+    """Q8 blocks in matmul_q8.metal's layout (ggml q8_0 rounding)."""
+    w = _f32(w)
+    K, N = w.shape
+    groups = (K + 31) // 32
+    out = np.zeros(groups * N * Q8_BYTES, dtype=np.uint8)
+    lib().oracle_quantize_q8(_p(w), K, N, _p(out))
+    return out
+
+
+def dequant_q8(q, K, N):
+    """shaders/matmul_q8.metal:44-52 -> f32 [K,N]."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    w = np.empty((K, N), dtype=np.float32)
+    lib().oracle_dequant_q8(_p(q), K, N, _p(w))
+    return w
+
+
+def dequant_q4_0_block(blk):
+    """dequantQ4_0, src/gguf.js:187-197."""
+    blk = np.ascontiguousarray(blk, dtype=np.uint8)
+    out = np.empty(32, dtype=np.float32)
+    lib().oracle_dequant_q4_0_block(_p(blk), _p(out))
+    return out
+
+
+def dequant_q8_0_block(blk):
+    """dequantQ8_0, src/gguf.js:221-231."""
+    blk = np.ascontiguousarray(blk, dtype=np.uint8)
+    out = np.empty(32, dtype=np.float32)
+    lib().oracle_dequant_q8_0_block(_p(blk), _p(out))
+    return out
+
+
+def dequantize_tensor(ggml_type, data, numel):
+    """dequantizeTensor, src/gguf.js:343-394 (Q4_0 / Q8_0)."""
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(numel, dtype=np.float32)
+    if lib().oracle_dequantize_tensor(ggml_type, _p(data), numel, _p(out)):
+        raise ValueError("unsupported type %d" % ggml_type)
+    return out
+
+
+def quantize_rows(ggml_type, x):
+    """GGUF Q4_0/Q8_0 encoder (ggml reference rounding, interleaved nibbles)."""
+    x = _f32(x)
+    rows, cols = x.shape
+    bpb = Q4_0_BYTES if ggml_type == GGML_Q4_0 else Q8_BYTES
+    out = np.zeros(rows * ((cols + 31) // 32) * bpb, dtype=np.uint8)
+    if lib().oracle_quantize_rows(ggml_type, _p(x), rows, cols, _p(out)):
+        raise ValueError("unsupported type %d" % ggml_type)
+    return out
+
+
+def matmul_f64acc(a, w):
+    a, w = _f32(a), _f32(w)
+    M, K = a.shape
+    N = w.shape[1]
+    c = np.empty((M, N), dtype=np.float32)
+    lib().oracle_matmul_f64acc(_p(a), _p(w), M, N, K, _p(c))
+    return c
+
+
+def matmul_f32(a, w):
+    a, w = _f32(a), _f32(w)
+    M, K = a.shape
+    N = w.shape[1]
+    c = np.empty((M, N), dtype=np.float32)
+    lib().oracle_matmul_f32(_p(a), _p(w), M, N, K, _p(c))
+    return c
+
+
+def matmul_q4s(a, q, K, N):
+    """matmulQ4 reference: dequant (matmul_q4.metal:24-28) then matmul."""
+    a = _f32(a)
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    M = a.shape[0]
+    c = np.empty((M, N), dtype=np.float32)
+    lib().oracle_matmul_q4s(_p(a), _p(q), M, N, K, _p(c))
+    return c
+
+
+def matmul_q8(a, q, K, N):
+    """matmulQ8 reference: dequant (matmul_q8.metal:44-52) then matmul."""
+    a = _f32(a)
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    M = a.shape[0]
+    c = np.empty((M, N), dtype=np.float32)
+    lib().oracle_matmul_q8(_p(a), _p(q), M, N, K, _p(c))
+    return c
+
+
+def matmul_gguf(ggml_type, a, q, K, N):
+    """y = a . W^T for a GGUF weight listed [out=N, in=K]."""
+    a = _f32(a)
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    M = a.shape[0]
+    c = np.empty((M, N), dtype=np.float32)
+    if lib().oracle_matmul_gguf(ggml_type, _p(a), _p(q), M, N, K, _p(c)):
+        raise ValueError("unsupported type %d" % ggml_type)
+    return c
+
+
+def normwise_rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.max(np.abs(ref))
+    return float(np.max(np.abs(y - ref)) / (den if den > 0 else 1.0))

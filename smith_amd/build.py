@@ -1,0 +1,54 @@
+"""Build the gfx950 code object and the C-ABI bridge in-tree.
+
+  smith_amd/lib/smith_kernels.hsaco   hipcc --offload-device-only --offload-arch=gfx950
+  smith_amd/lib/libsmith.so           g++ host code against libamdhip64
+
+Run as `python -m smith_amd.build`; __graft_entry__.build() calls build().
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIBDIR = os.path.join(HERE, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HSACO = os.path.join(LIBDIR, "smith_kernels.hsaco")
+LIBSMITH = os.path.join(LIBDIR, "libsmith.so")
+
+# -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (unreliable on the pool).
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    subprocess.check_call(cmd)
+
+
+def build_kernels():
+    os.makedirs(LIBDIR, exist_ok=True)
+    # a plain gfx950 ELF code object (no offload bundle) for hipModuleLoad
+    _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
+          "-c", os.path.join(CSRC, "smith_kernels.hip"), "-o", HSACO])
+
+
+def build_bridge():
+    os.makedirs(LIBDIR, exist_ok=True)
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
+          "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include"),
+          os.path.join(CSRC, "smith_bridge.cpp"), "-o", LIBSMITH,
+          "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc",
+          "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+
+
+def build():
+    build_kernels()
+    build_bridge()
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

@@ -1,0 +1,831 @@
+// smith_bridge.cpp -- libsmith.so: the C-ABI HIP bridge (include/smith.h).
+//
+// Replaces native/gpu_bridge.m (Objective-C + Metal).  Design differences,
+// all deliberate for MI355X:
+//   * buffers are hipMalloc device memory; the host reaches them with explicit
+//     copies (no unified-memory views);
+//   * kernels come from a gfx950 code object loaded with hipModuleLoad (or
+//     hipRTC for smith_compile_source) and are looked up by name;
+//   * one stream per context; encoders enqueue, end_sync/end_timed wait;
+//   * op-level entry points (smith_matmul_q4, ...) pick the kernel variant
+//     and launch geometry here, so a host language needs one FFI call per op.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/smith.h"
+
+namespace {
+
+struct Library {
+  hipModule_t mod = nullptr;
+  std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+struct Pipeline {
+  hipFunction_t fn;
+  std::string name;
+};
+
+struct Ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  std::string err;
+  std::vector<Library*> libs;
+  Library* ops = nullptr;
+  std::vector<Pipeline*> pipelines;
+  uint64_t allocated = 0;
+  // op scratch: prepared activations, split-K partials, split-K counters
+  void* prep = nullptr;
+  size_t prep_bytes = 0;
+  float* ws = nullptr;
+  size_t ws_bytes = 0;
+  uint32_t* counters = nullptr;
+  size_t counters_n = 0;
+  // per-launch HIP event pairs of op-level kernels while profiling is on
+  bool profile = false;
+  struct Rec {
+    std::string name;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> event_pool;
+};
+
+struct BufInfo {
+  Ctx* ctx;
+  uint64_t bytes;
+};
+
+std::mutex g_mu;
+std::unordered_map<void*, BufInfo> g_bufs;
+
+int fail(Ctx* c, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  return -1;
+}
+
+#define HIPCHK(c, expr)                                                                 \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess) return fail((c), "%s: %s", #expr, hipGetErrorString(e_));     \
+  } while (0)
+
+double now_s() {
+  using namespace std::chrono;
+  return duration<double>(steady_clock::now().time_since_epoch()).count();
+}
+
+int set_device(Ctx* c) {
+  HIPCHK(c, hipSetDevice(c->device));
+  return 0;
+}
+
+int lookup(Ctx* c, Library* lib, const char* name, hipFunction_t* out) {
+  if (!lib) return fail(c, "smith: no code object loaded (call smith_load_library first)");
+  auto it = lib->fns.find(name);
+  if (it != lib->fns.end()) {
+    *out = it->second;
+    return 0;
+  }
+  hipFunction_t f;
+  hipError_t e = hipModuleGetFunction(&f, lib->mod, name);
+  if (e != hipSuccess) return fail(c, "smith: kernel '%s' not found in code object", name);
+  lib->fns[name] = f;
+  *out = f;
+  return 0;
+}
+
+hipEvent_t pooled_event(Ctx* c) {
+  if (!c->event_pool.empty()) {
+    hipEvent_t e = c->event_pool.back();
+    c->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+int launch(Ctx* c, const char* name, dim3 grid, dim3 block, void** args, unsigned shmem = 0) {
+  hipFunction_t f;
+  if (lookup(c, c->ops, name, &f)) return -1;
+  hipEvent_t ea = nullptr, eb = nullptr;
+  if (c->profile) {
+    ea = pooled_event(c);
+    eb = pooled_event(c);
+    if (ea && eb) HIPCHK(c, hipEventRecord(ea, c->stream));
+  }
+  HIPCHK(c, hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, c->stream,
+                                  args, nullptr));
+  if (c->profile && ea && eb) {
+    HIPCHK(c, hipEventRecord(eb, c->stream));
+    c->recs.push_back(Ctx::Rec{name, ea, eb});
+  }
+  return 0;
+}
+
+// Grow-only device scratch owned by the context.  Growing waits for the
+// stream so no enqueued kernel still uses the old allocation.
+int ensure(Ctx* c, void** p, size_t* have, size_t need) {
+  if (need <= *have) return 0;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (*p) HIPCHK(c, hipFree(*p));
+  *p = nullptr;
+  *have = 0;
+  size_t sz = (need + 0xFFFFF) & ~(size_t)0xFFFFF;
+  HIPCHK(c, hipMalloc(p, sz));
+  *have = sz;
+  return 0;
+}
+
+int ensure_counters(Ctx* c, size_t n) {
+  if (n <= c->counters_n) return 0;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (c->counters) HIPCHK(c, hipFree(c->counters));
+  c->counters = nullptr;
+  c->counters_n = 0;
+  size_t cap = std::max<size_t>(n, 4096);
+  HIPCHK(c, hipMalloc((void**)&c->counters, cap * sizeof(uint32_t)));
+  // counters start at zero once; the kernel's last workgroup resets its own
+  HIPCHK(c, hipMemset(c->counters, 0, cap * sizeof(uint32_t)));
+  c->counters_n = cap;
+  return 0;
+}
+
+// ----- GEMV variant table (must match DEF_QGEMV_FMT in smith_kernels.hip) -----
+struct Variant {
+  int mb;      // max rows
+  int rb;      // row blocks (MFMAs per tile)
+  bool hilo;   // hi/lo activation split
+  int ct, gpw, wk;
+  const char* suffix;
+};
+const Variant kVariants[] = {
+    {1, 1, true, 1, 8, 4, "m1"},    {2, 1, true, 1, 8, 4, "m2"},   {4, 1, true, 1, 8, 4, "m4"},
+    {8, 1, true, 1, 8, 4, "m8"},    {16, 1, false, 2, 8, 4, "m16"}, {32, 2, false, 2, 8, 4, "m32"},
+};
+const Variant& pick_variant(uint32_t M) {
+  for (const Variant& v : kVariants)
+    if ((uint32_t)v.mb >= M) return v;
+  return kVariants[5];
+}
+
+enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2 };
+
+// One GEMV chunk of at most 32 rows: prepare activations, then the MFMA GEMV.
+int qgemv_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
+                uint32_t N, uint32_t K, uint32_t G) {
+  const Variant& v = pick_variant(M);
+  const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
+  const char* ptag = fmt == FQ4S ? "q4" : (fmt == FQ8 ? "q8" : "q40");
+  uint32_t RB = (uint32_t)v.rb;
+  size_t frag_bytes = (size_t)RB * G * 64 * 16;
+  size_t cst_bytes = (size_t)RB * G * 16 * 8;
+  if (ensure(c, &c->prep, &c->prep_bytes, frag_bytes + cst_bytes)) return -1;
+  void* frag = c->prep;
+  void* cst = (char*)c->prep + frag_bytes;
+
+  char name[64];
+  snprintf(name, sizeof name, "smith_qprep_%s_%s", ptag, v.hilo ? "hilo" : "plain");
+  uint32_t rpr = v.hilo ? 8 : 16;
+  uint64_t threads = (uint64_t)RB * rpr * G * 4;
+  {
+    const float* pa = a;
+    uint32_t pM = M, pK = K, pG = G, pRB = RB;
+    void* args[] = {&pa, &frag, &cst, &pM, &pK, &pG, &pRB};
+    if (launch(c, name, dim3((unsigned)((threads + 255) / 256)), dim3(256), args)) return -1;
+  }
+
+  uint32_t bc = 16 * (uint32_t)v.ct;
+  uint32_t gx = (N + bc - 1) / bc;
+  uint32_t per_block = (uint32_t)(v.wk * v.gpw);
+  uint32_t ksplit = (G + per_block - 1) / per_block;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  snprintf(name, sizeof name, "smith_qgemv_%s_%s", tag, v.suffix);
+  {
+    const void* pB = B;
+    const void* pD = D;
+    float* pC = out;
+    float* pws = c->ws;
+    uint32_t* pcnt = c->counters;
+    uint32_t pM = M, pN = N, pG = G;
+    void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG};
+    if (launch(c, name, dim3(gx, ksplit), dim3(64 * v.wk), args)) return -1;
+  }
+  return 0;
+}
+
+int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
+            uint32_t N, uint32_t K, uint32_t G) {
+  if (set_device(c)) return -1;
+  if (M == 0 || N == 0) return 0;
+  for (uint32_t m0 = 0; m0 < M; m0 += 32) {
+    uint32_t mc = std::min<uint32_t>(32, M - m0);
+    if (qgemv_chunk(c, fmt, a + (size_t)m0 * K, B, D, out + (size_t)m0 * N, mc, N, K, G)) return -1;
+  }
+  return 0;
+}
+
+struct Slot {
+  bool is_buf = false;
+  void* ptr = nullptr;
+  std::vector<uint8_t> bytes;
+};
+
+}  // namespace
+
+struct SmithEncoder {
+  Ctx* ctx;
+  Pipeline* pipe = nullptr;
+  std::map<uint32_t, Slot> slots;
+  uint64_t shmem = 0;
+  bool timed_started = false;
+  hipEvent_t ev0 = nullptr;
+  double submit_s = 0;
+  bool failed = false;
+};
+
+extern "C" {
+
+// ---------------- lifecycle ----------------
+void* smith_init(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return nullptr;
+  Ctx* c = new Ctx();
+  if (hipSetDevice(0) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess) {
+    delete c;
+    return nullptr;
+  }
+  return c;
+}
+
+void smith_destroy(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return;
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto it = g_bufs.begin(); it != g_bufs.end();) {
+      if (it->second.ctx == c) {
+        hipFree(it->first);
+        it = g_bufs.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
+  if (c->prep) hipFree(c->prep);
+  if (c->ws) hipFree(c->ws);
+  if (c->counters) hipFree(c->counters);
+  for (auto& r : c->recs) {
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+  }
+  for (hipEvent_t e : c->event_pool) hipEventDestroy(e);
+  for (Pipeline* p : c->pipelines) delete p;
+  for (Library* l : c->libs) {
+    hipModuleUnload(l->mod);
+    delete l;
+  }
+  hipEventDestroy(c->t0);
+  hipEventDestroy(c->t1);
+  hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* smith_last_error(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  return c ? c->err.c_str() : "smith: null context";
+}
+
+void smith_free(void* p) { free(p); }
+
+// ---------------- device info ----------------
+char* smith_device_name(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return nullptr;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, c->device) != hipSuccess) return nullptr;
+  std::string s = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  return strdup(s.c_str());
+}
+
+uint64_t smith_max_threadgroup_memory(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  hipDeviceProp_t prop;
+  if (!c || hipGetDeviceProperties(&prop, c->device) != hipSuccess) return 0;
+  return prop.sharedMemPerBlock;
+}
+
+uint64_t smith_max_threads_per_threadgroup(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  hipDeviceProp_t prop;
+  if (!c || hipGetDeviceProperties(&prop, c->device) != hipSuccess) return 0;
+  return prop.maxThreadsPerBlock;
+}
+
+// ---------------- buffers ----------------
+void* smith_alloc(void* ctx, uint64_t bytes, uint32_t mode) {
+  (void)mode;
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return nullptr;
+  if (set_device(c)) return nullptr;
+  // round up and pad so vector loads of a buffer's last record never leave
+  // the allocation
+  uint64_t sz = ((bytes ? bytes : 1) + 255) / 256 * 256 + 256;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, sz);
+  if (e != hipSuccess) {
+    fail(c, "smith: failed to allocate %llu bytes: %s", (unsigned long long)bytes, hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_bufs[p] = BufInfo{c, bytes};
+  c->allocated += bytes;
+  return p;
+}
+
+void* smith_buffer_contents(void* buffer) {
+  (void)buffer;
+  return nullptr;
+}
+
+uint64_t smith_buffer_length(void* buffer) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_bufs.find(buffer);
+  return it == g_bufs.end() ? 0 : it->second.bytes;
+}
+
+int64_t smith_buffer_retain_count(void* buffer) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_bufs.count(buffer) ? 1 : 0;
+}
+
+void smith_release_buffer(void* buffer) {
+  Ctx* c = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_bufs.find(buffer);
+    if (it == g_bufs.end()) return;
+    c = it->second.ctx;
+    c->allocated -= it->second.bytes;
+    g_bufs.erase(it);
+  }
+  // work already enqueued may still read the buffer
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  hipFree(buffer);
+}
+
+uint64_t smith_allocated_size(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  return c ? c->allocated : 0;
+}
+
+int64_t smith_test_release(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  uint64_t before = c->allocated;
+  void* p = smith_alloc(ctx, 1 << 20, SMITH_SHARED);
+  if (!p) return -1;
+  uint64_t mid = c->allocated;
+  smith_release_buffer(p);
+  return (int64_t)(mid - c->allocated) + (int64_t)(c->allocated - before);
+}
+
+int64_t smith_test_release_after_use(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  void* p = smith_alloc(ctx, 1 << 20, SMITH_SHARED);
+  if (!p) return -1;
+  if (hipMemsetAsync(p, 0, 1 << 20, c->stream) != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess) {
+    smith_release_buffer(p);
+    return -1;
+  }
+  uint64_t mid = c->allocated;
+  smith_release_buffer(p);
+  return (int64_t)(mid - c->allocated);
+}
+
+int smith_copy_h2d(void* ctx, void* dst, uint64_t off, const void* src, uint64_t bytes) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (!bytes) return 0;
+  HIPCHK(c, hipMemcpyAsync((char*)dst + off, src, bytes, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+int smith_copy_d2h(void* ctx, void* dst, const void* src, uint64_t off, uint64_t bytes) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (!bytes) return 0;
+  HIPCHK(c, hipMemcpyAsync(dst, (const char*)src + off, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+int smith_copy_d2d(void* ctx, void* dst, uint64_t doff, const void* src, uint64_t soff, uint64_t bytes) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (!bytes) return 0;
+  HIPCHK(c, hipMemcpyAsync((char*)dst + doff, (const char*)src + soff, bytes, hipMemcpyDeviceToDevice, c->stream));
+  return 0;
+}
+
+int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (!bytes) return 0;
+  if (bytes % 4) return fail(c, "smith_fill_zero: byte count %llu is not a multiple of 4", (unsigned long long)bytes);
+  uint64_t n = bytes / 4;
+  void* p = buffer;
+  void* args[] = {&p, &n};
+  uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 65536);
+  return launch(c, "smith_zero_u32", dim3((unsigned)blocks), dim3(256), args);
+}
+
+int smith_sync(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+// ---------------- code objects ----------------
+void* smith_load_library(void* ctx, const char* path) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c || !path) return nullptr;
+  if (set_device(c)) return nullptr;
+  hipModule_t m;
+  hipError_t e = hipModuleLoad(&m, path);
+  if (e != hipSuccess) {
+    fail(c, "smith: failed to load code object at %s: %s", path, hipGetErrorString(e));
+    return nullptr;
+  }
+  Library* lib = new Library();
+  lib->mod = m;
+  c->libs.push_back(lib);
+  if (!c->ops) c->ops = lib;
+  return lib;
+}
+
+void* smith_compile_source(void* ctx, const char* source, char** error_out) {
+  Ctx* c = (Ctx*)ctx;
+  if (error_out) *error_out = nullptr;
+  if (!c || !source) return nullptr;
+  if (set_device(c)) return nullptr;
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, source, "smith_rtc.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+    if (error_out) *error_out = strdup("hiprtcCreateProgram failed");
+    return nullptr;
+  }
+  const char* opts[] = {"--offload-arch=gfx950", "-O3"};
+  hiprtcResult r = hiprtcCompileProgram(prog, 2, opts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n + 1, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    if (error_out) *error_out = strdup(log.c_str());
+    fail(c, "smith: hipRTC compile failed");
+    hiprtcDestroyProgram(&prog);
+    return nullptr;
+  }
+  size_t code_sz = 0;
+  hiprtcGetCodeSize(prog, &code_sz);
+  std::vector<char> code(code_sz);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  hipModule_t m;
+  hipError_t e = hipModuleLoadData(&m, code.data());
+  if (e != hipSuccess) {
+    if (error_out) *error_out = strdup(hipGetErrorString(e));
+    return nullptr;
+  }
+  Library* lib = new Library();
+  lib->mod = m;
+  c->libs.push_back(lib);
+  return lib;
+}
+
+void* smith_create_pipeline(void* ctx, void* library, const char* fn_name) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c || !library || !fn_name) return nullptr;
+  hipFunction_t f;
+  if (lookup(c, (Library*)library, fn_name, &f)) return nullptr;
+  Pipeline* p = new Pipeline{f, fn_name};
+  c->pipelines.push_back(p);
+  return p;
+}
+
+// ---------------- encoded dispatch ----------------
+SmithEncoder* smith_begin(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return nullptr;
+  SmithEncoder* e = new SmithEncoder();
+  e->ctx = c;
+  return e;
+}
+
+void smith_set_buffer(SmithEncoder* enc, void* buffer, uint32_t index) {
+  if (!enc) return;
+  Slot& s = enc->slots[index];
+  s.is_buf = true;
+  s.ptr = buffer;
+  s.bytes.clear();
+}
+
+void smith_set_bytes(SmithEncoder* enc, const void* data, uint32_t length, uint32_t index) {
+  if (!enc) return;
+  Slot& s = enc->slots[index];
+  s.is_buf = false;
+  s.ptr = nullptr;
+  s.bytes.assign((const uint8_t*)data, (const uint8_t*)data + length);
+}
+
+void smith_set_pipeline(SmithEncoder* enc, void* pipeline) {
+  if (enc) enc->pipe = (Pipeline*)pipeline;
+}
+
+void smith_set_threadgroup_memory(SmithEncoder* enc, uint64_t length, uint32_t index) {
+  (void)index;  // HIP has one dynamic LDS block per workgroup: lengths add up
+  if (enc) enc->shmem += length;
+}
+
+void smith_dispatch(SmithEncoder* enc, uint64_t gx, uint64_t gy, uint64_t gz, uint64_t bx, uint64_t by,
+                    uint64_t bz) {
+  if (!enc) return;
+  Ctx* c = enc->ctx;
+  if (!enc->pipe) {
+    fail(c, "smith_dispatch: no pipeline set");
+    enc->failed = true;
+    return;
+  }
+  if (!bx) bx = 1;
+  if (!by) by = 1;
+  if (!bz) bz = 1;
+  if (bx * by * bz > 1024) {
+    fail(c, "smith_dispatch: workgroup of %llu threads exceeds 1024", (unsigned long long)(bx * by * bz));
+    enc->failed = true;
+    return;
+  }
+  if (!gx || !gy || !gz) return;  // empty grid: nothing to run
+  std::vector<uint8_t> blob;
+  for (auto& kv : enc->slots) {
+    const Slot& s = kv.second;
+    size_t align = s.is_buf ? 8 : (s.bytes.size() % 8 == 0 ? 8 : 4);
+    size_t off = (blob.size() + align - 1) / align * align;
+    if (s.is_buf) {
+      blob.resize(off + 8);
+      memcpy(blob.data() + off, &s.ptr, 8);
+    } else {
+      blob.resize(off + s.bytes.size());
+      memcpy(blob.data() + off, s.bytes.data(), s.bytes.size());
+    }
+  }
+  size_t blob_sz = blob.size();
+  void* extra[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, blob.data(), HIP_LAUNCH_PARAM_BUFFER_SIZE, &blob_sz,
+                   HIP_LAUNCH_PARAM_END};
+  if (set_device(c)) {
+    enc->failed = true;
+    return;
+  }
+  if (!enc->timed_started) {
+    enc->timed_started = true;
+    enc->submit_s = now_s();
+    if (hipEventCreate(&enc->ev0) == hipSuccess) hipEventRecord(enc->ev0, c->stream);
+  }
+  hipError_t e = hipModuleLaunchKernel(enc->pipe->fn, (unsigned)((gx + bx - 1) / bx), (unsigned)((gy + by - 1) / by),
+                                       (unsigned)((gz + bz - 1) / bz), (unsigned)bx, (unsigned)by, (unsigned)bz,
+                                       (unsigned)enc->shmem, c->stream, nullptr, extra);
+  if (e != hipSuccess) {
+    fail(c, "smith_dispatch(%s): %s", enc->pipe->name.c_str(), hipGetErrorString(e));
+    enc->failed = true;
+  }
+}
+
+void smith_end_sync(SmithEncoder* enc) {
+  if (!enc) return;
+  hipSetDevice(enc->ctx->device);
+  hipStreamSynchronize(enc->ctx->stream);
+  if (enc->ev0) hipEventDestroy(enc->ev0);
+  delete enc;
+}
+
+void* smith_end_async(SmithEncoder* enc) {
+  if (!enc) return nullptr;
+  hipEvent_t ev;
+  void* token = nullptr;
+  if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
+    hipEventRecord(ev, enc->ctx->stream);
+    token = (void*)ev;
+  }
+  if (enc->ev0) hipEventDestroy(enc->ev0);
+  delete enc;
+  return token;
+}
+
+void smith_wait(void* token) {
+  if (!token) return;
+  hipEvent_t ev = (hipEvent_t)token;
+  hipEventSynchronize(ev);
+  hipEventDestroy(ev);
+}
+
+SmithTiming* smith_end_timed(SmithEncoder* enc) {
+  if (!enc) return nullptr;
+  Ctx* c = enc->ctx;
+  SmithTiming* t = (SmithTiming*)calloc(1, sizeof(SmithTiming));
+  hipSetDevice(c->device);
+  hipEvent_t ev1 = nullptr;
+  if (enc->ev0 && hipEventCreate(&ev1) == hipSuccess) {
+    hipEventRecord(ev1, c->stream);
+    hipEventSynchronize(ev1);
+    float ms = 0.f;
+    hipEventElapsedTime(&ms, enc->ev0, ev1);
+    t->gpu_ms = ms;
+    hipEventDestroy(ev1);
+  } else {
+    hipStreamSynchronize(c->stream);
+  }
+  t->gpu_end = now_s();
+  t->gpu_start = enc->timed_started ? enc->submit_s : t->gpu_end;
+  if (enc->ev0) hipEventDestroy(enc->ev0);
+  delete enc;
+  return t;
+}
+
+void smith_dispatch_sync(void* ctx, void* pipeline, void** buffers, uint32_t* indices, uint32_t count,
+                         const void* params, uint32_t params_length, uint32_t params_index, uint64_t gx,
+                         uint64_t gy, uint64_t gz, uint64_t bx, uint64_t by, uint64_t bz) {
+  SmithEncoder* e = smith_begin(ctx);
+  if (!e) return;
+  smith_set_pipeline(e, pipeline);
+  for (uint32_t i = 0; i < count; i++) smith_set_buffer(e, buffers[i], indices[i]);
+  if (params && params_length) smith_set_bytes(e, params, params_length, params_index);
+  smith_dispatch(e, gx, gy, gz, bx, by, bz);
+  smith_end_sync(e);
+}
+
+// ---------------- op-level entry points ----------------
+int smith_quantize_q4(void* ctx, const float* w, void* out, uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  uint64_t total = (uint64_t)((K + 31) / 32) * N;
+  if (!total) return 0;
+  uint32_t pK = K, pN = N;
+  void* args[] = {&w, &out, &pK, &pN};
+  return launch(c, "smith_quantize_q4s", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_quantize_q8(void* ctx, const float* w, void* out, uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  uint64_t total = (uint64_t)((K + 31) / 32) * N;
+  if (!total) return 0;
+  uint32_t pK = K, pN = N;
+  void* args[] = {&w, &out, &pK, &pN};
+  return launch(c, "smith_quantize_q8", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_quantize_q4_0(void* ctx, const float* x, void* out, uint32_t rows, uint32_t cols) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (cols % 32) return fail(c, "smith_quantize_q4_0: cols %u is not a multiple of 32", cols);
+  if (set_device(c)) return -1;
+  uint64_t total = (uint64_t)rows * (cols / 32);
+  if (!total) return 0;
+  uint32_t pr = rows, pc = cols;
+  void* args[] = {&x, &out, &pr, &pc};
+  return launch(c, "smith_quantize_q4_0_rows", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_repack_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_repack_q4_0: K %u is not a multiple of 32", K);
+  if (set_device(c)) return -1;
+  uint32_t G = K / 32;
+  uint64_t total = (uint64_t)N * G;
+  if (!total) return 0;
+  uint32_t pN = N, pG = G;
+  void* args[] = {&blocks, &nib, &d, &pN, &pG};
+  return launch(c, "smith_repack_q4_0", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_matmul_q4(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
+                    uint32_t groups) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (groups != (K + 31) / 32)
+    return fail(c, "matmulQ4: groups %u does not match ceil(K/32) for K=%u", groups, K);
+  return qmatmul(c, FQ4S, a, wq, nullptr, out, M, N, K, groups);
+}
+
+int smith_matmul_q8(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
+                    uint32_t groups) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (groups != (K + 31) / 32)
+    return fail(c, "matmulQ8: groups %u does not match ceil(K/32) for K=%u", groups, K);
+  return qmatmul(c, FQ8, a, wq, nullptr, out, M, N, K, groups);
+}
+
+int smith_matmul_q4_0(void* ctx, const float* a, const void* nib, const void* d, float* out, uint32_t M,
+                      uint32_t N, uint32_t K) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_matmul_q4_0: K %u is not a multiple of 32", K);
+  return qmatmul(c, FQ40, a, nib, d, out, M, N, K, K / 32);
+}
+
+// ---------------- timing ----------------
+int smith_profile_kernels(void* ctx, int enable) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  c->profile = enable != 0;
+  return 0;
+}
+
+int smith_profile_read(void* ctx, const char* prefix, double* total_ms, uint64_t* count) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  size_t plen = prefix ? strlen(prefix) : 0;
+  double tot = 0.0;
+  uint64_t n = 0;
+  std::vector<Ctx::Rec> keep;
+  for (auto& r : c->recs) {
+    if (plen && r.name.compare(0, plen, prefix) != 0) {
+      keep.push_back(r);
+      continue;
+    }
+    float ms = 0.f;
+    HIPCHK(c, hipEventElapsedTime(&ms, r.a, r.b));
+    tot += ms;
+    n++;
+    c->event_pool.push_back(r.a);
+    c->event_pool.push_back(r.b);
+  }
+  c->recs.swap(keep);
+  if (total_ms) *total_ms = tot;
+  if (count) *count = n;
+  return 0;
+}
+
+int smith_timer_start(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  HIPCHK(c, hipEventRecord(c->t0, c->stream));
+  return 0;
+}
+
+double smith_timer_stop(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (hipEventRecord(c->t1, c->stream) != hipSuccess || hipEventSynchronize(c->t1) != hipSuccess)
+    return fail(c, "smith_timer_stop: event failure");
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, c->t0, c->t1) != hipSuccess) return fail(c, "smith_timer_stop: elapsed failure");
+  return ms;
+}
+
+}  // extern "C"

@@ -1,0 +1,576 @@
+// smith_kernels.hip -- gfx950 (CDNA4) kernels for SMITH's quantized-weight
+// matmul path.  Compiled to a code object (smith_kernels.hsaco) that the
+// bridge loads with hipModuleLoad; every kernel is extern "C" so the bridge
+// and the generic dispatch API can look it up by name.
+//
+// Formats (byte-exact with the reference):
+//   Q4S  -- quantizeQ4 (src/ops/quantize.js:14-68): record (g,n) at
+//           (g*N+n)*24: 16 nibble bytes (element k -> byte k>>1, low nibble
+//           for even k), f32 scale at +16, f32 zero at +20;
+//           w = scale*(nib - zero)                (shaders/matmul_q4.metal:24-28)
+//   Q8   -- matmulQ8 blocks (shaders/matmul_q8.metal:40-52): block (g,n) at
+//           (g*N+n)*34: f16 scale at +0, int8[32] at +2; w = f32(scale)*q
+//   Q4_0 -- GGUF blocks (src/gguf.js:187-197) after the loader splits them
+//           into planes without touching a byte: nibbles nib[(g*N+n)*16..]
+//           and f16 scales d[g*N+n]; w = d*(nib - 8), interleaved nibbles.
+//
+// Decode GEMV (M <= 32) -- the HBM-bound hot path.  One wave computes a
+// 16-column x 32-K "tile" per MFMA (v_mfma_f32_16x16x32_f16):
+//   * B operand = the weights.  Each lane owns one column (lane%16) and one
+//     8-element K slice (lane/16) of a 32-K group, i.e. exactly one dword of
+//     the record's nibble area (Q4) or 8 int8 bytes (Q8).  Nibbles become f16
+//     with one v_and_or_b32 per pair using exponent-bias magic numbers
+//     (0x6400 -> 1024+q for a low nibble, 0x5400 -> 64+q for a high nibble;
+//     int8 bytes -> 1024+(q+128) with v_perm_b32), so B holds exact integers
+//     plus a known per-slot offset.
+//   * A operand = activations, pre-split into f16 hi + f16 lo*2048 rows
+//     ("hi/lo", M <= 8) so the product keeps ~22 bits of each f32
+//     activation, or plain f16 rows (M > 8).  Prepared once per matmul by
+//     qprep_* into a fragment-ready buffer together with two per-row,
+//     per-group constants: C1 = sum(a*offset) (+ folded zero) and S = sum(a).
+//   * Per group the MFMA result P is turned into the exact group
+//     contribution scale*(P - C1 - zero*S) and accumulated in f32.  The
+//     per-group scale/zero therefore never touch the f16 path.
+// Split-K across workgroups is reduced deterministically: partials go to a
+// workspace and the last-arriving workgroup of each column block sums them in
+// fixed order (agent-scope atomic RMWs + counter; the counter self-resets).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define FMT_Q4S 0
+#define FMT_Q8 1
+#define FMT_Q40 2
+
+// ---------------------------------------------------------------------------
+// Reference-semantics kernels (one thread per output element).  They take the
+// exact binding of the reference shaders -- A at slot 0, B at 1, C at 2, the
+// {M,N,K,groups} u32 struct at 3 -- so the reference's quantize.js dispatch
+// (run('matmul_q4', ..., grid {N,M}, group {16,16})) works unchanged through
+// the generic encoder API.  The fast path is the smith_qgemv_* family below.
+// ---------------------------------------------------------------------------
+struct QMatmulParams {
+  uint32_t M, N, K, groups;
+};
+
+extern "C" __global__ void matmul_q4(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                     float* __restrict__ C, QMatmulParams p) {
+  // Same math and accumulation order as shaders/matmul_q4.metal:34-65.
+  uint32_t col = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t row = blockIdx.y * blockDim.y + threadIdx.y;
+  if (row >= p.M || col >= p.N) return;
+  float acc = 0.0f;
+  for (uint32_t g = 0; g < p.groups; g++) {
+    const uint8_t* rec = B + ((size_t)g * p.N + col) * 24;
+    float scale = *(const float*)(rec + 16);
+    float zero = *(const float*)(rec + 20);
+    for (uint32_t k = 0; k < 32 && g * 32 + k < p.K; k++) {
+      uint8_t b = rec[k >> 1];
+      float nib = (float)((k & 1) ? (b >> 4) : (b & 15));
+      acc = __fadd_rn(acc, __fmul_rn(A[(size_t)row * p.K + g * 32 + k], __fmul_rn(scale, __fsub_rn(nib, zero))));
+    }
+  }
+  C[(size_t)row * p.N + col] = acc;
+}
+
+extern "C" __global__ void matmul_q8(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                     float* __restrict__ C, QMatmulParams p) {
+  // Same math and accumulation order as shaders/matmul_q8.metal:20-57.
+  uint32_t col = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t row = blockIdx.y * blockDim.y + threadIdx.y;
+  if (row >= p.M || col >= p.N) return;
+  float acc = 0.0f;
+  for (uint32_t g = 0; g < p.groups; g++) {
+    const uint8_t* blk = B + ((size_t)g * p.N + col) * 34;
+    uint16_t hbits = (uint16_t)(blk[0] | (blk[1] << 8));
+    float scale = (float)__builtin_bit_cast(_Float16, hbits);
+    const int8_t* v = (const int8_t*)(blk + 2);
+    for (uint32_t k = 0; k < 32 && g * 32 + k < p.K; k++)
+      acc = __fadd_rn(acc, __fmul_rn(A[(size_t)row * p.K + g * 32 + k], __fmul_rn(scale, (float)v[k])));
+  }
+  C[(size_t)row * p.N + col] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// quantizeQ4 on the GPU, bit-exact with src/ops/quantize.js:14-68.
+// One thread per (group, column); f64 arithmetic with JavaScript's Math.max /
+// Math.min / Math.round semantics and ToUint8 (NaN -> 0).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double js_max(double a, double b) {
+  if (a != a || b != b) return __builtin_nan("");
+  if (a == 0.0 && b == 0.0) return __builtin_signbit(a) ? b : a;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ double js_min(double a, double b) {
+  if (a != a || b != b) return __builtin_nan("");
+  if (a == 0.0 && b == 0.0) return __builtin_signbit(a) ? a : b;
+  return a < b ? a : b;
+}
+__device__ __forceinline__ uint32_t js_round_u8(double x) {
+  // Math.round (ties toward +inf) followed by the Uint8Array store; x is
+  // NaN or within [0, 15] here.
+  if (x != x) return 0u;
+  double r = __builtin_floor(x);
+  if (__dsub_rn(x, r) >= 0.5) r = r + 1.0;
+  return (uint32_t)(int32_t)r;
+}
+
+extern "C" __global__ void smith_quantize_q4s(const float* __restrict__ w, uint8_t* __restrict__ out,
+                                              uint32_t K, uint32_t N) {
+  uint32_t groups = (K + 31) / 32;
+  size_t total = (size_t)groups * N;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    uint32_t g = (uint32_t)(idx / N), col = (uint32_t)(idx % N);
+    uint32_t k0 = g * 32;
+    uint32_t valid = K - k0 < 32 ? K - k0 : 32;
+    double mn = __builtin_inf(), mx = -__builtin_inf();
+    for (uint32_t k = 0; k < valid; k++) {
+      double v = (double)w[(size_t)(k0 + k) * N + col];
+      if (v < mn) mn = v;
+      if (v > mx) mx = v;
+    }
+    double range = __dsub_rn(mx, mn);
+    double scale = range > 0 ? __ddiv_rn(range, 15.0) : 1.0;
+    double zero = range > 0 ? __ddiv_rn(-mn, scale) : 8.0;
+    uint32_t words[6];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        uint32_t k = d * 8 + j;
+        double v = k < valid ? (double)w[(size_t)(k0 + k) * N + col] : 0.0;
+        double t = __dadd_rn(__ddiv_rn(v, scale), zero);
+        uint32_t q = js_round_u8(js_min(15.0, js_max(0.0, t)));
+        word |= (q & 15u) << (4 * j);
+      }
+      words[d] = word;
+    }
+    words[4] = __float_as_uint(__double2float_rn(scale));
+    words[5] = __float_as_uint(__double2float_rn(zero));
+    uint32_t* rec = (uint32_t*)(out + idx * 24);
+#pragma unroll
+    for (int d = 0; d < 6; d++) rec[d] = words[d];
+  }
+}
+
+// f32 -> f16 bits, IEEE round-to-nearest-even (ggml FP32_TO_FP16).
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Q8 blocks in matmul_q8.metal's layout, ggml q8_0 rounding: d = amax/127,
+// q = roundf(x * (1/d)), scale stored as RNE f16.  Thread per (group, col).
+extern "C" __global__ void smith_quantize_q8(const float* __restrict__ w, uint8_t* __restrict__ out,
+                                             uint32_t K, uint32_t N) {
+  uint32_t groups = (K + 31) / 32;
+  size_t total = (size_t)groups * N;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    uint32_t g = (uint32_t)(idx / N), col = (uint32_t)(idx % N);
+    float x[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+      uint32_t kk = g * 32 + k;
+      x[k] = kk < K ? w[(size_t)kk * N + col] : 0.0f;
+      float a = __builtin_fabsf(x[k]);
+      amax = a > amax ? a : amax;
+    }
+    float d = __fdiv_rn(amax, 127.0f);
+    float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint8_t* blk = out + idx * 34;
+    uint16_t h = f32_to_f16_rne(d);
+    // 34-byte records are only 2-byte aligned: write as 17 u16 halves.
+    uint16_t* hp = (uint16_t*)blk;
+    hp[0] = h;
+#pragma unroll
+    for (int k = 0; k < 32; k += 2) {
+      int8_t q0 = (int8_t)__builtin_roundf(__fmul_rn(x[k], id));
+      int8_t q1 = (int8_t)__builtin_roundf(__fmul_rn(x[k + 1], id));
+      hp[1 + k / 2] = (uint16_t)((uint8_t)q0 | ((uint16_t)(uint8_t)q1 << 8));
+    }
+  }
+}
+
+// GGUF Q4_0 (ggml q4_0 rounding, reference's interleaved nibble order) for a
+// row-major f32 [rows, cols] matrix, cols % 32 == 0.  Thread per block.
+extern "C" __global__ void smith_quantize_q4_0_rows(const float* __restrict__ x, uint8_t* __restrict__ out,
+                                                    uint32_t rows, uint32_t cols) {
+  uint32_t bpr = cols / 32;
+  size_t total = (size_t)rows * bpr;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const float* v = x + idx * 32;  // rows are contiguous, so block idx covers 32 floats
+    float amax = 0.0f, mx = 0.0f;
+    float xv[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      xv[i] = v[i];
+      float a = __builtin_fabsf(xv[i]);
+      if (amax < a) { amax = a; mx = xv[i]; }
+    }
+    float d = __fdiv_rn(mx, -8.0f);
+    float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint16_t* hp = (uint16_t*)(out + idx * 18);
+    hp[0] = f32_to_f16_rne(d);
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+      int q0 = (int)(int8_t)__fadd_rn(__fmul_rn(xv[i], id), 8.5f);
+      int q1 = (int)(int8_t)__fadd_rn(__fmul_rn(xv[i + 1], id), 8.5f);
+      q0 = q0 < 15 ? q0 : 15;
+      q1 = q1 < 15 ? q1 : 15;
+      ((uint8_t*)hp)[2 + i / 2] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+    }
+  }
+}
+
+// Split GGUF Q4_0 blocks of a weight listed [out=N][in=K] (block (n,g) at
+// (n*G+g)*18) into the planar, column-interleaved layout the GEMV reads:
+// nib[(g*N+n)*16 + 0..15] and d[g*N+n].  Bytes are moved, never changed.
+extern "C" __global__ void smith_repack_q4_0(const uint8_t* __restrict__ src, uint8_t* __restrict__ nib,
+                                             uint16_t* __restrict__ dsc, uint32_t N, uint32_t G) {
+  size_t total = (size_t)N * G;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    uint32_t n = (uint32_t)(idx / G), g = (uint32_t)(idx % G);
+    const uint16_t* s = (const uint16_t*)(src + idx * 18);
+    size_t o = (size_t)g * N + n;
+    dsc[o] = s[0];
+    uint16_t* dn = (uint16_t*)(nib + o * 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) dn[i] = s[1 + i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Activation preparation for the MFMA GEMV.
+//   frag[(rb*G + g)*64 + lane]  u32x4 = the 8 f16 A-operand values of `lane`
+//   cst [(rb*G + g)*16 + vrow]  float2 = (C1, S) of virtual row vrow
+// Virtual rows of row block rb: HILO -> vrow r<8 is hi(row rb*8+r), vrow r>=8
+// is lo(row rb*8+r-8)*2048; plain -> vrow r is row rb*16+r.  The f16 slots
+// of a lane follow the B-operand conversion order of the weight format:
+//   Q4 family: elements {0,4,1,5,2,6,3,7} of its 8-K slice, offsets
+//              {1024,1024,64,64,1024,1024,64,64}
+//   Q8:        elements {0,2,1,3,4,6,5,7}, offset 1152 everywhere
+// C1 = sum(a*offset) (+ 8*S folded in for Q4_0, whose zero point is 8).
+// Thread per (real row, group, kslice), kslice fastest.
+// ---------------------------------------------------------------------------
+template <int FMT, bool HILO>
+__device__ __forceinline__ void qprep_body(const float* __restrict__ A, u32x4* __restrict__ frag,
+                                           float2* __restrict__ cst, uint32_t M, uint32_t K, uint32_t G,
+                                           uint32_t RB) {
+  const uint32_t rows_per_rb = HILO ? 8 : 16;
+  uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t kq = tid & 3;
+  uint32_t rest = tid >> 2;
+  uint32_t g = rest % G;
+  uint32_t m = rest / G;  // padded real row, < RB*rows_per_rb
+  bool active = m < RB * rows_per_rb;
+  // slot -> element within the 8-K slice, and slot offsets
+  const int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  const int perm_q8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+  const float off_q4[8] = {1024.f, 1024.f, 64.f, 64.f, 1024.f, 1024.f, 64.f, 64.f};
+  float hi_c1 = 0.f, hi_s = 0.f, lo_c1 = 0.f, lo_s = 0.f;
+  _Float16 hv[8], lv[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    int e = FMT == FMT_Q8 ? perm_q8[j] : perm_q4[j];
+    float off = FMT == FMT_Q8 ? 1152.f : off_q4[j];
+    uint32_t k = g * 32 + kq * 8 + e;
+    float a = (active && m < M && k < K) ? A[(size_t)m * K + k] : 0.0f;
+    _Float16 h = (_Float16)a;
+    hv[j] = h;
+    float hf = (float)h;
+    hi_c1 = __builtin_fmaf(hf, off, hi_c1);
+    hi_s += hf;
+    if (HILO) {
+      _Float16 l = (_Float16)((a - hf) * 2048.0f);
+      lv[j] = l;
+      float lf = (float)l;
+      lo_c1 = __builtin_fmaf(lf, off, lo_c1);
+      lo_s += lf;
+    }
+  }
+  // reduce the four K slices of the group (lanes tid^1, tid^2 are the same
+  // row/group because kq is the fastest index)
+#pragma unroll
+  for (int d = 1; d < 4; d <<= 1) {
+    hi_c1 += __shfl_xor(hi_c1, d);
+    hi_s += __shfl_xor(hi_s, d);
+    if (HILO) {
+      lo_c1 += __shfl_xor(lo_c1, d);
+      lo_s += __shfl_xor(lo_s, d);
+    }
+  }
+  if (!active) return;
+  uint32_t rb = m / rows_per_rb, r = m % rows_per_rb;
+  size_t fbase = ((size_t)rb * G + g) * 64;
+  size_t cbase = ((size_t)rb * G + g) * 16;
+  u32x4 hp;
+  hp.x = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[0], hv[1]});
+  hp.y = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[2], hv[3]});
+  hp.z = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[4], hv[5]});
+  hp.w = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[6], hv[7]});
+  frag[fbase + r + 16 * kq] = hp;
+  float fold = FMT == FMT_Q40 ? 8.0f : 0.0f;
+  if (kq == 0) cst[cbase + r] = make_float2(__builtin_fmaf(fold, hi_s, hi_c1), hi_s);
+  if (HILO) {
+    u32x4 lp;
+    lp.x = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[0], lv[1]});
+    lp.y = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[2], lv[3]});
+    lp.z = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[4], lv[5]});
+    lp.w = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[6], lv[7]});
+    frag[fbase + r + 8 + 16 * kq] = lp;
+    if (kq == 0) cst[cbase + r + 8] = make_float2(__builtin_fmaf(fold, lo_s, lo_c1), lo_s);
+  }
+}
+
+#define DEF_QPREP(NAME, FMT, HILO)                                                                     \
+  extern "C" __global__ __launch_bounds__(256) void NAME(const float* A, u32x4* frag, float2* cst,     \
+                                                         uint32_t M, uint32_t K, uint32_t G,           \
+                                                         uint32_t RB) {                                \
+    qprep_body<FMT, HILO>(A, frag, cst, M, K, G, RB);                                                  \
+  }
+DEF_QPREP(smith_qprep_q4_hilo, FMT_Q4S, true)
+DEF_QPREP(smith_qprep_q4_plain, FMT_Q4S, false)
+DEF_QPREP(smith_qprep_q40_hilo, FMT_Q40, true)
+DEF_QPREP(smith_qprep_q40_plain, FMT_Q40, false)
+DEF_QPREP(smith_qprep_q8_hilo, FMT_Q8, true)
+DEF_QPREP(smith_qprep_q8_plain, FMT_Q8, false)
+
+// ---------------------------------------------------------------------------
+// Weight tile loads and nibble/int8 -> f16 conversion (B operand).
+// ---------------------------------------------------------------------------
+struct WTile {
+  uint32_t q0, q1, q2;  // Q4: q0 = nibble dword; Q8: 3 raw dwords + shift
+  uint32_t sh;
+  float s, z;
+};
+
+// Branch-free: an out-of-range tile (g >= G or n >= N) loads from a clamped,
+// valid record and gets scale 0, so it contributes exactly 0 and the
+// compiler can keep every load of the wave in flight at once.  The Q8 path
+// always reads three dwords; the last one may extend 2 bytes past the final
+// record, which stays inside smith_alloc's 256-byte tail padding.
+template <int FMT>
+__device__ __forceinline__ WTile load_tile(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
+                                           uint32_t N, uint32_t G, uint32_t g, uint32_t n, uint32_t kq) {
+  WTile t;
+  bool ok = g < G && n < N;
+  size_t rec = (size_t)(g < G ? g : G - 1) * N + (n < N ? n : N - 1);
+  t.q1 = t.q2 = 0;
+  t.sh = 0;
+  t.z = 0.f;
+  if (FMT == FMT_Q4S) {
+    const uint8_t* p = B + rec * 24;
+    t.q0 = *(const uint32_t*)(p + 4 * kq);
+    float2 sz = *(const float2*)(p + 16);
+    t.s = sz.x;
+    t.z = sz.y;
+  } else if (FMT == FMT_Q40) {
+    t.q0 = *(const uint32_t*)(B + rec * 16 + 4 * kq);
+    t.s = (float)__builtin_bit_cast(_Float16, D[rec]);
+  } else {
+    const uint8_t* p = B + rec * 34;
+    t.s = (float)__builtin_bit_cast(_Float16, *(const uint16_t*)p);
+    size_t a = (size_t)(p + 2 + 8 * kq);
+    const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
+    t.sh = (uint32_t)(a & 3) * 8;  // 0 or 16 bits
+    t.q0 = w[0];
+    t.q1 = w[1];
+    t.q2 = w[2];
+  }
+  t.s = ok ? t.s : 0.f;
+  t.z = ok ? t.z : 0.f;
+  return t;
+}
+
+template <int FMT>
+__device__ __forceinline__ half8 tile_to_f16(const WTile& t) {
+  u32x4 u;
+  if (FMT == FMT_Q8) {
+    uint32_t x0 = __builtin_amdgcn_alignbyte(t.q1, t.q0, t.sh >> 3) ^ 0x80808080u;
+    uint32_t x1 = __builtin_amdgcn_alignbyte(t.q2, t.q1, t.sh >> 3) ^ 0x80808080u;
+    u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);  // (1024+u0, 1024+u2)
+    u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);  // (1024+u1, 1024+u3)
+    u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);  // (1024+u4, 1024+u6)
+    u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);  // (1024+u5, 1024+u7)
+  } else {
+    uint32_t x = t.q0, y = t.q0 >> 8;
+    u.x = (x & 0x000F000Fu) | 0x64006400u;  // (1024+e0, 1024+e4)
+    u.y = (x & 0x00F000F0u) | 0x54005400u;  // (64+e1, 64+e5)
+    u.z = (y & 0x000F000Fu) | 0x64006400u;  // (1024+e2, 1024+e6)
+    u.w = (y & 0x00F000F0u) | 0x54005400u;  // (64+e3, 64+e7)
+  }
+  return __builtin_bit_cast(half8, u);
+}
+
+// ---------------------------------------------------------------------------
+// The GEMV.  Template parameters:
+//   RB   row blocks (MFMAs per tile); HILO hi/lo activation rows
+//   VPL  accumulator values per lane that carry real rows (<= 4)
+//   CT   16-column tiles per wave; GPW groups per wave; WK waves per block
+// Grid: x = column blocks of 16*CT columns, y = K splits of WK*GPW groups.
+// ---------------------------------------------------------------------------
+template <int FMT, int RB, bool HILO, int VPL, int CT, int GPW, int WK>
+__device__ __forceinline__ void qgemv_body(const u32x4* __restrict__ frag, const float2* __restrict__ cst,
+                                           const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
+                                           float* __restrict__ C, float* __restrict__ ws,
+                                           uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
+                                           uint32_t G) {
+  constexpr int BC = 16 * CT;
+  constexpr int VR = 16;  // virtual rows per row block
+  __shared__ float red[WK][RB][VR][BC];
+  __shared__ int s_last;
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t col = lane & 15, kq = lane >> 4;
+  const uint32_t n0 = blockIdx.x * BC;
+  const uint32_t ksplit = gridDim.y;
+  const uint32_t g0 = (blockIdx.y * WK + wave) * GPW;
+
+  // Issue every load of the wave first (weights, activation fragments,
+  // row constants) so all of them are in flight together, then compute.
+  WTile wt[GPW][CT];
+#pragma unroll
+  for (int j = 0; j < GPW; j++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      uint32_t g = g0 + j, n = n0 + ct * 16 + col;
+      wt[j][ct] = load_tile<FMT>(B, D, N, G, g, n, kq);
+    }
+  u32x4 afr[GPW][RB];
+  float4 cvv[GPW][RB][(VPL + 1) / 2];
+#pragma unroll
+  for (int j = 0; j < GPW; j++) {
+    uint32_t g = g0 + j < G ? g0 + j : G - 1;
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      afr[j][rb] = frag[((size_t)rb * G + g) * 64 + lane];
+      const float4* cp = (const float4*)(cst + ((size_t)rb * G + g) * 16 + kq * 4);
+#pragma unroll
+      for (int h = 0; h < (VPL + 1) / 2; h++) cvv[j][rb][h] = cp[h];
+    }
+  }
+
+  f32x4 acc[CT][RB];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // no early exit: groups past G carry scale 0 (straight-line code keeps the
+  // loads above from being sunk into the loop)
+#pragma unroll
+  for (int j = 0; j < GPW; j++) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      half8 bf = tile_to_f16<FMT>(wt[j][ct]);
+      float s = wt[j][ct].s, z = wt[j][ct].z;
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) {
+        f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, afr[j][rb]), bf,
+                                                         (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < VPL; i++) {
+          float4 c2 = cvv[j][rb][i >> 1];
+          float c1 = (i & 1) ? c2.z : c2.x, sr = (i & 1) ? c2.w : c2.y;
+          float t = p[i] - c1;
+          if (FMT == FMT_Q4S) t = __builtin_fmaf(-z, sr, t);
+          acc[ct][rb][i] = __builtin_fmaf(s, t, acc[ct][rb][i]);
+        }
+      }
+    }
+  }
+
+  // per-wave partials -> LDS: lane holds virtual rows 4*kq+i of column col
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        red[wave][rb][kq * 4 + i][ct * 16 + col] = i < VPL ? acc[ct][rb][i] : 0.f;
+  __syncthreads();
+
+  // combine waves (+ hi/lo) in fixed order; thread -> (row, column)
+  const uint32_t rows_per_rb = HILO ? 8 : 16;
+  const uint32_t nthreads = WK * 64;
+  const uint32_t mrows = M < (uint32_t)(RB * rows_per_rb) ? M : RB * rows_per_rb;
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += nthreads) {
+    uint32_t m = e / BC, c = e % BC;
+    uint32_t rb = m / rows_per_rb, r = m % rows_per_rb;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WK; w++) {
+      if (HILO) v += red[w][rb][r][c] + red[w][rb][r + 8][c] * (1.0f / 2048.0f);
+      else v += red[w][rb][r][c];
+    }
+    uint32_t n = n0 + c;
+    if (n >= N) continue;
+    if (ksplit == 1) {
+      C[(size_t)m * N + n] = v;
+    } else {
+      // Agent-scope atomic RMWs are performed at the device's point of
+      // coherence, so partials written this way are visible to a workgroup
+      // on any XCD without the whole-L2 writeback a release fence costs.
+      __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (ksplit == 1) return;
+
+  __builtin_amdgcn_s_waitcnt(0);  // every exchange of this thread has been performed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == ksplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += nthreads) {
+    uint32_t m = e / BC, c = e % BC;
+    uint32_t n = n0 + c;
+    if (n >= N) continue;
+    float v = 0.f;
+    for (uint32_t s = 0; s < ksplit; s++)
+      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)s * M + m) * N + n, 0u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    C[(size_t)m * N + n] = v;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define DEF_QGEMV(NAME, FMT, RB, HILO, VPL, CT, GPW, WK)                                               \
+  extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                          \
+      const u32x4* frag, const float2* cst, const uint8_t* B, const uint16_t* D, float* C, float* ws,  \
+      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G) {                                        \
+    qgemv_body<FMT, RB, HILO, VPL, CT, GPW, WK>(frag, cst, B, D, C, ws, counters, M, N, G);           \
+  }
+
+// Row buckets: M=1 (hi/lo, 1 value/lane), 2, 4 (hi/lo), 8 (hi/lo, 4 values),
+// 16 (plain, 1 MFMA), 32 (plain, 2 MFMAs).
+#define DEF_QGEMV_FMT(TAG, FMT)                                           \
+  DEF_QGEMV(smith_qgemv_##TAG##_m1, FMT, 1, true, 1, 1, 8, 4)             \
+  DEF_QGEMV(smith_qgemv_##TAG##_m2, FMT, 1, true, 2, 1, 8, 4)             \
+  DEF_QGEMV(smith_qgemv_##TAG##_m4, FMT, 1, true, 4, 1, 8, 4)             \
+  DEF_QGEMV(smith_qgemv_##TAG##_m8, FMT, 1, true, 4, 1, 8, 4)             \
+  DEF_QGEMV(smith_qgemv_##TAG##_m16, FMT, 1, false, 4, 2, 8, 4)           \
+  DEF_QGEMV(smith_qgemv_##TAG##_m32, FMT, 2, false, 4, 2, 8, 4)
+
+DEF_QGEMV_FMT(q4s, FMT_Q4S)
+DEF_QGEMV_FMT(q8, FMT_Q8)
+DEF_QGEMV_FMT(q40, FMT_Q40)
+
+// Zero fill (used instead of hipMemsetAsync so the op stays a plain kernel).
+extern "C" __global__ void smith_zero_u32(uint32_t* __restrict__ p, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}

@@ -1,0 +1,68 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+symbol include/smith.h declares, the code object holds every kernel the
+bridge launches, and host-side errors match the reference's messages."""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "smith.h")
+
+
+def declared_symbols():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(smith_\w+)\s*\(", src)))
+
+
+def test_library_exports_header_symbols():
+    from smith_amd import device
+    names = declared_symbols()
+    assert len(names) >= 40
+    for n in names:
+        assert hasattr(device.lib, n), n
+        assert n in device.SYMBOLS, "ctypes table lacks " + n
+    assert set(device.SYMBOLS) == set(names)
+
+
+def test_reference_bridge_names_all_present():
+    # the 25 functions of native/gpu_bridge.h:15-127, bound at src/device.js:10-50
+    ref = ["smith_init", "smith_destroy", "smith_device_name", "smith_max_threadgroup_memory",
+           "smith_max_threads_per_threadgroup", "smith_alloc", "smith_buffer_contents", "smith_buffer_length",
+           "smith_release_buffer", "smith_load_library", "smith_compile_source", "smith_create_pipeline",
+           "smith_begin", "smith_set_buffer", "smith_set_bytes", "smith_set_threadgroup_memory",
+           "smith_set_pipeline", "smith_dispatch", "smith_end_sync", "smith_end_async", "smith_wait",
+           "smith_end_timed", "smith_allocated_size", "smith_test_release", "smith_test_release_after_use",
+           "smith_buffer_retain_count", "smith_dispatch_sync"]
+    assert set(ref) <= set(declared_symbols())
+
+
+def test_code_object_has_kernels():
+    from smith_amd import device
+    out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.CODE_OBJECT_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    need = ["matmul_q4", "matmul_q8", "smith_quantize_q4s", "smith_quantize_q8", "smith_quantize_q4_0_rows",
+            "smith_repack_q4_0", "smith_zero_u32"]
+    for fmt in ("q4", "q8", "q40"):
+        need += ["smith_qprep_%s_hilo" % fmt, "smith_qprep_%s_plain" % fmt]
+    for fmt in ("q4s", "q8", "q40"):
+        need += ["smith_qgemv_%s_m%d" % (fmt, m) for m in (1, 2, 4, 8, 16, 32)]
+    for k in need:
+        assert re.search(r"\b%s\.kd\b" % k, out), k
+
+
+def test_package_imports_without_gpu_and_errors_match_reference():
+    import smith_amd
+
+    class FakeA:
+        shape = [1, 48]
+        dtype = "f32"
+        buffer = None
+
+    wq = smith_amd.QuantizedWeight(buffer=None, K=64, N=8, groups=2, totalBytes=2 * 8 * 24)
+    with pytest.raises(ValueError, match="matmulQ4: inner dims don't match: 48 vs 64"):
+        smith_amd.matmulQ4(FakeA(), wq)
+    with pytest.raises(ValueError, match="matmulQ8: inner dims don't match: 48 vs 64"):
+        smith_amd.matmulQ8(FakeA(), wq)

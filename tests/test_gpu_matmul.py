@@ -1,0 +1,216 @@
+"""GPU parity: the HIP path (libsmith.so + gfx950 code object) against the CPU
+oracle on the same seeded inputs.
+
+Bars (stated by the path's spec):
+  * packed bytes (quantizeQ4, quantizeQ8, Q4_0 encoder, Q4_0 repack):
+    bit-exact with the oracle;
+  * matmul outputs: normwise max|y - ref| / max|ref| <= 1e-3 against the f32
+    dequantize-then-matmul result (accumulated in f64).  The hi/lo
+    activation split (M <= 8) is additionally held to 2e-5.
+"""
+import numpy as np
+import pytest
+
+import smith_amd as S
+from oracle import oracle as O
+from smith_amd import device, prng
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TOL_HILO = 2e-5
+
+
+def dev_bytes(q):
+    return device.download(q["buffer"], q["totalBytes"], np.uint8)
+
+
+def err(y, ref):
+    return O.normwise_rel_err(y, ref)
+
+
+# ---------------- quantizers: bit-exact ----------------
+
+def edge_weight():
+    K, N = 96, 8
+    w = prng.randn((K, N), 21, std=0.02)
+    w[:32, 0] = np.arange(32) % 16            # identity group, zero = -0
+    w[:, 1] = 0.3                              # constant groups
+    w[:32, 2] = [0, 15, 0.5, 1.5, 2.5, 14.5, 7.5, 3.25] + [0] * 24  # ties
+    w[3, 3] = np.nan                           # NaN element
+    w[32:64, 4] = np.nan                       # all-NaN group
+    w[64, 5] = np.inf                          # infinite element
+    w[65, 6] = -np.inf
+    w[:, 7] = -0.0
+    return w
+
+
+@pytest.mark.parametrize("K,N,seed", [(32, 1, 1), (64, 32, 2), (100, 3, 3), (70, 24, 4), (4096, 256, 5),
+                                      (33, 300, 6)])
+def test_quantize_q4_bit_exact(K, N, seed):
+    w = prng.randn((K, N), seed, std=0.02)
+    q = S.quantizeQ4(S.tensor(w))
+    assert (q.K, q.N, q.groups, q.totalBytes) == (K, N, -(-K // 32), -(-K // 32) * N * 24)
+    assert np.array_equal(dev_bytes(q), O.quantize_q4s(w))
+
+
+def test_quantize_q4_edge_values_bit_exact():
+    w = edge_weight()
+    assert np.array_equal(dev_bytes(S.quantizeQ4(w)), O.quantize_q4s(w))
+
+
+def test_quantize_q4_golden_fixture():
+    g = np.load(__file__.replace("test_gpu_matmul.py", "golden/golden.npz"))
+    assert np.array_equal(dev_bytes(S.quantizeQ4(g["w_q4s"])), g["q4s_bytes"])
+    assert np.array_equal(dev_bytes(S.quantizeQ8(g["w_q8"])), g["q8_bytes"])
+
+
+@pytest.mark.parametrize("K,N,seed", [(32, 2, 1), (100, 17, 2), (4096, 128, 3)])
+def test_quantize_q8_bit_exact(K, N, seed):
+    w = prng.randn((K, N), seed, std=0.02)
+    w[0, 0] = 0.0
+    assert np.array_equal(dev_bytes(S.quantizeQ8(w)), O.quantize_q8(w))
+
+
+def test_quantize_q4_0_rows_bit_exact():
+    rows, cols = 48, 256
+    x = prng.randn((rows, cols), 31, std=0.02)
+    x[0, :32] = np.arange(-8, 24) % 16 - 8
+    xt = S.tensor(x)
+    out = device.alloc(rows * cols // 32 * 18)
+    device.check(device.lib.smith_quantize_q4_0(device.ops_ctx(), xt.buffer, out, rows, cols))
+    got = device.download(out, rows * cols // 32 * 18, np.uint8)
+    assert np.array_equal(got, O.quantize_rows(O.GGML_Q4_0, x))
+
+
+# ---------------- matmul parity ----------------
+
+MS = [1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 70]
+SHAPES = [(32, 1), (100, 17), (256, 64), (1024, 300)]
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_matmul_q4_parity(K, N):
+    w = prng.randn((K, N), 41, std=0.02)
+    q = S.quantizeQ4(w)
+    qb = dev_bytes(q)
+    dq = O.dequant_q4s(qb, K, N).astype(np.float64)
+    for M in MS:
+        a = prng.randn((M, K), 100 + M)
+        y = S.matmulQ4(S.tensor(a), q).data
+        assert y.shape == (M, N)
+        ref = a.astype(np.float64) @ dq
+        e = err(y, ref)
+        assert e <= (TOL_HILO if M <= 8 else TOL), (M, K, N, e)
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_matmul_q8_parity(K, N):
+    w = prng.randn((K, N), 42, std=0.02)
+    q = S.quantizeQ8(w)
+    dq = O.dequant_q8(dev_bytes(q), K, N).astype(np.float64)
+    for M in MS:
+        a = prng.randn((M, K), 200 + M)
+        y = S.matmulQ8(S.tensor(a), q).data
+        ref = a.astype(np.float64) @ dq
+        e = err(y, ref)
+        assert e <= (TOL_HILO if M <= 8 else TOL), (M, K, N, e)
+
+
+def test_matmul_q4_oracle_matmul_small():
+    # the oracle's own quantize -> dequant -> matmul chain end to end
+    K, N, M = 100, 24, 3
+    w = prng.randn((K, N), 43, std=0.02)
+    a = prng.randn((M, K), 44)
+    y = S.matmulQ4(S.tensor(a), S.quantizeQ4(w)).data
+    assert err(y, O.matmul_q4s(a, O.quantize_q4s(w), K, N)) <= TOL_HILO
+
+
+def test_reference_dispatch_kernels():
+    """matmul_q4 / matmul_q8 bound exactly as src/ops/quantize.js:82-87 binds them."""
+    from smith_amd.quantize import matmul_reference_dispatch
+    K, N, M = 100, 40, 5
+    w = prng.randn((K, N), 45, std=0.02)
+    a = prng.randn((M, K), 46)
+    at = S.tensor(a)
+    q4, q8 = S.quantizeQ4(w), S.quantizeQ8(w)
+    y4 = matmul_reference_dispatch("matmul_q4", at, q4).data
+    y8 = matmul_reference_dispatch("matmul_q8", at, q8).data
+    assert err(y4, O.matmul_q4s(a, O.quantize_q4s(w), K, N)) <= 1e-6
+    assert err(y8, O.matmul_q8(a, O.quantize_q8(w), K, N)) <= 1e-6
+
+
+def test_matmul_deterministic_and_k_mismatch():
+    K, N = 4096, 512
+    q = S.quantizeQ4(prng.randn((K, N), 47, std=0.02))
+    a = S.tensor(prng.randn((1, K), 48))
+    y1 = S.matmulQ4(a, q).data
+    y2 = S.matmulQ4(a, q).data
+    assert np.array_equal(y1, y2)  # split-K reduction order is fixed
+    with pytest.raises(ValueError, match="inner dims don't match: 100 vs 4096"):
+        S.matmulQ4(S.tensor(np.zeros((1, 100), np.float32)), q)
+
+
+# ---------------- GGUF Q4_0 ----------------
+
+@pytest.mark.parametrize("N,K", [(16, 32), (40, 96), (300, 1024)])
+def test_q4_0_repack_and_matmul(N, K):
+    w = prng.randn((N, K), 51, std=0.02)  # GGUF listing [out, in]
+    blocks = O.quantize_rows(O.GGML_Q4_0, w)
+    G = K // 32
+    src = device.alloc(blocks.size)
+    device.upload(src, blocks)
+    nib = device.alloc(N * G * 16)
+    dsc = device.alloc(N * G * 2)
+    ctx = device.ops_ctx()
+    device.check(device.lib.smith_repack_q4_0(ctx, src, nib, dsc, N, K))
+    got_nib = device.download(nib, N * G * 16, np.uint8).reshape(G, N, 16)
+    got_d = device.download(dsc, N * G * 2, np.uint8).reshape(G, N, 2)
+    b = blocks.reshape(N, G, 18)
+    assert np.array_equal(got_nib, b[:, :, 2:].transpose(1, 0, 2))
+    assert np.array_equal(got_d, b[:, :, :2].transpose(1, 0, 2))
+    wd = O.dequantize_tensor(O.GGML_Q4_0, blocks, N * K).reshape(N, K).astype(np.float64)
+    for M in MS:
+        a = prng.randn((M, K), 300 + M)
+        at = S.tensor(a)
+        out = S.create([M, N])
+        device.check(device.lib.smith_matmul_q4_0(ctx, at.buffer, nib, dsc, out.buffer, M, N, K))
+        e = err(out.data, a.astype(np.float64) @ wd.T)
+        assert e <= (TOL_HILO if M <= 8 else TOL), (M, N, K, e)
+
+
+# ---------------- BASELINE configs at full size ----------------
+
+def test_config1_q4_gemv_4096():
+    K = N = 4096
+    w = prng.randn((K, N), 1, std=0.02)
+    a = prng.randn((1, K), 0)
+    q = S.quantizeQ4(w)
+    qb = dev_bytes(q)
+    assert np.array_equal(qb, O.quantize_q4s(w))
+    y = S.matmulQ4(S.tensor(a), q).data
+    ref = O.matmul_q4s(a, qb, K, N)
+    assert err(y, ref) <= TOL_HILO
+
+
+def test_config2_q8_gemv_14336():
+    K, N = 4096, 14336
+    w = prng.randn((K, N), 1, std=0.02)
+    a = prng.randn((1, K), 0)
+    q = S.quantizeQ8(w)
+    qb = dev_bytes(q)
+    assert np.array_equal(qb, O.quantize_q8(w))
+    y = S.matmulQ8(S.tensor(a), q).data
+    assert err(y, O.matmul_q8(a, qb, K, N)) <= TOL_HILO
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+def test_config3_batched_decode_sweep(N, K):
+    w = prng.randn((K, N), 2, std=0.02)  # Smith weight [K, N]
+    q = S.quantizeQ4(w)
+    dq = O.dequant_q4s(dev_bytes(q), K, N).astype(np.float64)
+    for M in (1, 4, 8, 16, 32):
+        a = prng.randn((M, K), 10 + M)
+        y = S.matmulQ4(S.tensor(a), q).data
+        e = err(y, a.astype(np.float64) @ dq)
+        assert e <= (TOL_HILO if M <= 8 else TOL), (M, N, K, e)
