@@ -175,12 +175,12 @@ struct Variant {
   int mb;      // max rows
   int rb;      // row blocks (MFMAs per tile)
   bool hilo;   // hi/lo activation split
-  int ct, gpw, wk;
+  int ct, gpw, wk, wn;
   const char* suffix;
 };
 const Variant kVariants[] = {
-    {1, 1, true, 1, 8, 4, "m1"},    {2, 1, true, 1, 8, 4, "m2"},   {4, 1, true, 1, 8, 4, "m4"},
-    {8, 1, true, 1, 8, 4, "m8"},    {16, 1, false, 2, 8, 4, "m16"}, {32, 2, false, 2, 8, 4, "m32"},
+    {1, 1, true, 1, 8, 4, 1, "m1"},     {2, 1, true, 1, 8, 4, 1, "m2"},    {4, 1, true, 1, 8, 4, 1, "m4"},
+    {8, 1, true, 1, 8, 4, 1, "m8"},     {16, 1, false, 2, 8, 4, 1, "m16"}, {32, 2, false, 2, 8, 4, 1, "m32"},
 };
 const Variant& pick_variant(uint32_t M) {
   for (const Variant& v : kVariants)
@@ -214,7 +214,7 @@ int qgemv_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, f
     if (launch(c, name, dim3((unsigned)((threads + 255) / 256)), dim3(256), args)) return -1;
   }
 
-  uint32_t bc = 16 * (uint32_t)v.ct;
+  uint32_t bc = 16 * (uint32_t)(v.ct * v.wn);
   uint32_t gx = (N + bc - 1) / bc;
   uint32_t per_block = (uint32_t)(v.wk * v.gpw);
   uint32_t ksplit = (G + per_block - 1) / per_block;
@@ -231,9 +231,37 @@ int qgemv_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, f
     uint32_t* pcnt = c->counters;
     uint32_t pM = M, pN = N, pG = G;
     void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG};
-    if (launch(c, name, dim3(gx, ksplit), dim3(64 * v.wk), args)) return -1;
+    if (launch(c, name, dim3(gx, ksplit), dim3(64 * v.wk * v.wn), args)) return -1;
   }
   return 0;
+}
+
+// M <= 2: the fused kernel (activation prep in LDS, whole records per lane,
+// K split across the waves of a block; a cross-block split only when one
+// block's 64/128 groups do not cover K).
+int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
+                 uint32_t N, uint32_t K, uint32_t G) {
+  const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
+  bool small = G <= 64;
+  uint32_t kb = small ? 64 : 128;
+  uint32_t threads = small ? 256 : 512;
+  uint32_t gx = (N + 15) / 16;
+  uint32_t ksplit = (G + kb - 1) / kb;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u", tag, M, kb);
+  const float* pa = a;
+  const void* pB = B;
+  const void* pD = D;
+  float* pC = out;
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pM = M, pN = N, pK = K, pG = G;
+  void* args[] = {&pa, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pK, &pG};
+  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
 }
 
 int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
@@ -242,7 +270,10 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
   if (M == 0 || N == 0) return 0;
   for (uint32_t m0 = 0; m0 < M; m0 += 32) {
     uint32_t mc = std::min<uint32_t>(32, M - m0);
-    if (qgemv_chunk(c, fmt, a + (size_t)m0 * K, B, D, out + (size_t)m0 * N, mc, N, K, G)) return -1;
+    const float* am = a + (size_t)m0 * K;
+    float* om = out + (size_t)m0 * N;
+    int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G) : qgemv_chunk(c, fmt, am, B, D, om, mc, N, K, G);
+    if (rc) return -1;
   }
   return 0;
 }

@@ -414,26 +414,30 @@ __device__ __forceinline__ half8 tile_to_f16(const WTile& t) {
 // The GEMV.  Template parameters:
 //   RB   row blocks (MFMAs per tile); HILO hi/lo activation rows
 //   VPL  accumulator values per lane that carry real rows (<= 4)
-//   CT   16-column tiles per wave; GPW groups per wave; WK waves per block
-// Grid: x = column blocks of 16*CT columns, y = K splits of WK*GPW groups.
+//   CT   16-column tiles per wave; GPW groups per wave
+//   WK x WN waves per block: WK waves split the block's groups (reduced in
+//   LDS), WN waves sit side by side along N (longer contiguous weight runs)
+// Grid: x = column blocks of 16*CT*WN columns, y = K splits of WK*GPW groups.
 // ---------------------------------------------------------------------------
-template <int FMT, int RB, bool HILO, int VPL, int CT, int GPW, int WK>
+template <int FMT, int RB, bool HILO, int VPL, int CT, int GPW, int WK, int WN>
 __device__ __forceinline__ void qgemv_body(const u32x4* __restrict__ frag, const float2* __restrict__ cst,
                                            const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
                                            float* __restrict__ C, float* __restrict__ ws,
                                            uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
                                            uint32_t G) {
-  constexpr int BC = 16 * CT;
+  constexpr int BC = 16 * CT * WN;
   constexpr int VR = 16;  // virtual rows per row block
   __shared__ float red[WK][RB][VR][BC];
   __shared__ int s_last;
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wk = wave / WN, wn = wave % WN;
   const uint32_t col = lane & 15, kq = lane >> 4;
   const uint32_t n0 = blockIdx.x * BC;
+  const uint32_t nw = n0 + wn * (16 * CT);  // first column of this wave
   const uint32_t ksplit = gridDim.y;
-  const uint32_t g0 = (blockIdx.y * WK + wave) * GPW;
+  const uint32_t g0 = (blockIdx.y * WK + wk) * GPW;
 
   // Issue every load of the wave first (weights, activation fragments,
   // row constants) so all of them are in flight together, then compute.
@@ -442,7 +446,7 @@ __device__ __forceinline__ void qgemv_body(const u32x4* __restrict__ frag, const
   for (int j = 0; j < GPW; j++)
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
-      uint32_t g = g0 + j, n = n0 + ct * 16 + col;
+      uint32_t g = g0 + j, n = nw + ct * 16 + col;
       wt[j][ct] = load_tile<FMT>(B, D, N, G, g, n, kq);
     }
   u32x4 afr[GPW][RB];
@@ -496,12 +500,12 @@ __device__ __forceinline__ void qgemv_body(const u32x4* __restrict__ frag, const
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
       for (int i = 0; i < 4; i++)
-        red[wave][rb][kq * 4 + i][ct * 16 + col] = i < VPL ? acc[ct][rb][i] : 0.f;
+        red[wk][rb][kq * 4 + i][wn * 16 * CT + ct * 16 + col] = i < VPL ? acc[ct][rb][i] : 0.f;
   __syncthreads();
 
   // combine waves (+ hi/lo) in fixed order; thread -> (row, column)
   const uint32_t rows_per_rb = HILO ? 8 : 16;
-  const uint32_t nthreads = WK * 64;
+  const uint32_t nthreads = WK * WN * 64;
   const uint32_t mrows = M < (uint32_t)(RB * rows_per_rb) ? M : RB * rows_per_rb;
   for (uint32_t e = threadIdx.x; e < mrows * BC; e += nthreads) {
     uint32_t m = e / BC, c = e % BC;
@@ -548,26 +552,318 @@ __device__ __forceinline__ void qgemv_body(const u32x4* __restrict__ frag, const
     __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-#define DEF_QGEMV(NAME, FMT, RB, HILO, VPL, CT, GPW, WK)                                               \
-  extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                          \
+#define DEF_QGEMV(NAME, FMT, RB, HILO, VPL, CT, GPW, WK, WN)                                           \
+  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                     \
       const u32x4* frag, const float2* cst, const uint8_t* B, const uint16_t* D, float* C, float* ws,  \
       uint32_t* counters, uint32_t M, uint32_t N, uint32_t G) {                                        \
-    qgemv_body<FMT, RB, HILO, VPL, CT, GPW, WK>(frag, cst, B, D, C, ws, counters, M, N, G);           \
+    qgemv_body<FMT, RB, HILO, VPL, CT, GPW, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G);       \
   }
 
 // Row buckets: M=1 (hi/lo, 1 value/lane), 2, 4 (hi/lo), 8 (hi/lo, 4 values),
 // 16 (plain, 1 MFMA), 32 (plain, 2 MFMAs).
 #define DEF_QGEMV_FMT(TAG, FMT)                                           \
-  DEF_QGEMV(smith_qgemv_##TAG##_m1, FMT, 1, true, 1, 1, 8, 4)             \
-  DEF_QGEMV(smith_qgemv_##TAG##_m2, FMT, 1, true, 2, 1, 8, 4)             \
-  DEF_QGEMV(smith_qgemv_##TAG##_m4, FMT, 1, true, 4, 1, 8, 4)             \
-  DEF_QGEMV(smith_qgemv_##TAG##_m8, FMT, 1, true, 4, 1, 8, 4)             \
-  DEF_QGEMV(smith_qgemv_##TAG##_m16, FMT, 1, false, 4, 2, 8, 4)           \
-  DEF_QGEMV(smith_qgemv_##TAG##_m32, FMT, 2, false, 4, 2, 8, 4)
+  DEF_QGEMV(smith_qgemv_##TAG##_m1, FMT, 1, true, 1, 1, 8, 4, 1)          \
+  DEF_QGEMV(smith_qgemv_##TAG##_m2, FMT, 1, true, 2, 1, 8, 4, 1)          \
+  DEF_QGEMV(smith_qgemv_##TAG##_m4, FMT, 1, true, 4, 1, 8, 4, 1)          \
+  DEF_QGEMV(smith_qgemv_##TAG##_m8, FMT, 1, true, 4, 1, 8, 4, 1)          \
+  DEF_QGEMV(smith_qgemv_##TAG##_m16, FMT, 1, false, 4, 2, 8, 4, 1)        \
+  DEF_QGEMV(smith_qgemv_##TAG##_m32, FMT, 2, false, 4, 2, 8, 4, 1)
 
+// ---------------------------------------------------------------------------
+// Decode GEMV for M <= 2 with the activation prep fused (no prep launch).
+//
+// Lane (c = lane%16, j = lane/16) loads the WHOLE weight record of column
+// n0+c in group g0+4s+j with 128-bit loads, so the 16 lanes of a lane group
+// read 16 consecutive records (one contiguous run).  Step s covers 4 groups
+// (one per lane group) x 16 columns with 4 MFMAs: MFMA i consumes nibble
+// dword i (K elements 8i..8i+7) of every lane.  The A operand is arranged so
+// that MFMA row 4j+u only sees K slice j (lane group j), i.e. row 4j+u of P
+// is the dot product of group g0+4s+j alone, and it lands in lane group j of
+// the accumulator layout -- the lanes that hold that group's scale and zero.
+// Rows u: 0 = hi(row 0), 1 = lo(row 0)*2048, 2 = hi(row 1), 3 = lo(row 1).
+//
+// The block loads its K range of the activations, issues all of its weight
+// loads, and converts the activations into those f16 fragments in LDS (plus
+// per-group C1 and S) while the weights are in flight.  WK waves split the
+// block's groups (reduced through LDS), WN waves sit side by side along N.
+// Grid: x = column blocks of 16*CT*WN, y = K splits of 4*S*WK groups.
+// ---------------------------------------------------------------------------
+template <int FMT>
+struct Rec {
+  u32x4 q;        // 32 nibbles (Q4) or int8 0..15 (Q8)
+  u32x4 q8b;      // Q8: int8 16..31 (+ one spare dword for the 2-byte shift)
+  uint32_t q8c;
+  uint32_t sh;
+  float s, z;
+};
+
+template <int FMT>
+__device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
+                                             uint32_t N, uint32_t G, uint32_t g, uint32_t n) {
+  Rec<FMT> r;
+  bool ok = g < G && n < N;
+  size_t rec = (size_t)(g < G ? g : G - 1) * N + (n < N ? n : N - 1);
+  r.z = 0.f;
+  r.sh = 0;
+  if (FMT == FMT_Q4S) {
+    const uint8_t* p = B + rec * 24;
+    r.q = *(const u32x4*)p;
+    float2 sz = *(const float2*)(p + 16);
+    r.s = sz.x;
+    r.z = sz.y;
+  } else if (FMT == FMT_Q40) {
+    r.q = *(const u32x4*)(B + rec * 16);
+    r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
+  } else {
+    const uint8_t* p = B + rec * 34;
+    r.s = (float)__builtin_bit_cast(_Float16, *(const uint16_t*)p);
+    size_t a = (size_t)(p + 2);
+    const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
+    r.sh = (uint32_t)(a & 3);  // bytes: 0 or 2
+    r.q = (u32x4){w[0], w[1], w[2], w[3]};
+    r.q8b = (u32x4){w[4], w[5], w[6], w[7]};
+    r.q8c = w[8];
+  }
+  r.s = ok ? r.s : 0.f;
+  r.z = ok ? r.z : 0.f;
+  return r;
+}
+
+// B operand of MFMA i (K elements 8i..8i+7 of the record).
+template <int FMT>
+__device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
+  u32x4 u;
+  if (FMT == FMT_Q8) {
+    uint32_t d[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
+    uint32_t x0 = __builtin_amdgcn_alignbyte(d[2 * i + 1], d[2 * i], r.sh) ^ 0x80808080u;
+    uint32_t x1 = __builtin_amdgcn_alignbyte(d[2 * i + 2], d[2 * i + 1], r.sh) ^ 0x80808080u;
+    u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);
+    u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);
+    u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);
+    u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);
+  } else {
+    uint32_t x = i == 0 ? r.q.x : (i == 1 ? r.q.y : (i == 2 ? r.q.z : r.q.w));
+    uint32_t y = x >> 8;
+    u.x = (x & 0x000F000Fu) | 0x64006400u;
+    u.y = (x & 0x00F000F0u) | 0x54005400u;
+    u.z = (y & 0x000F000Fu) | 0x64006400u;
+    u.w = (y & 0x00F000F0u) | 0x54005400u;
+  }
+  return __builtin_bit_cast(half8, u);
+}
+
+template <int FMT, int MR, int CT, int WK, int WN, int S>
+__device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                            const uint16_t* __restrict__ D, float* __restrict__ C,
+                                            float* __restrict__ ws, uint32_t* __restrict__ counters,
+                                            uint32_t M, uint32_t N, uint32_t K, uint32_t G) {
+  constexpr int GPW = 4 * S;           // groups per wave (S steps of 4)
+  constexpr int KB = GPW * WK;         // groups per block
+  constexpr int BC = 16 * CT * WN;     // block columns
+  constexpr int NT = 64 * WK * WN;     // threads
+  constexpr int NCH = KB * MR * 4;     // prep chunks: (group, row, mfma slice)
+  constexpr int CPT = (NCH + NT - 1) / NT;
+  __shared__ u32x4 fragL[KB][2 * MR][4];  // [group][row u][mfma i]
+  __shared__ float2 cL[KB][MR];           // (C1, S) with hi + lo/2048 folded
+  __shared__ float red[WK][MR][BC];
+  __shared__ int s_last;
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wk = wave / WN, wn = wave % WN;
+  const uint32_t c = lane & 15, j = lane >> 4;
+  const uint32_t n0 = blockIdx.x * BC + wn * 16 * CT;
+  const uint32_t gb = blockIdx.y * KB;
+  const uint32_t gw = gb + wk * GPW;
+  const uint32_t ksplit = gridDim.y;
+
+  // 1. activation loads first (small, cache resident): the in-order load
+  //    counter then lets the conversion below run while weights are in flight
+  const int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  const int perm_q8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+  const float off_q4[8] = {1024.f, 1024.f, 64.f, 64.f, 1024.f, 1024.f, 64.f, 64.f};
+  float av[CPT][8];
+#pragma unroll
+  for (int cc = 0; cc < CPT; cc++) {
+    uint32_t ch = threadIdx.x + cc * NT;
+    uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
+    uint32_t k0 = (gb + gl) * 32 + 8 * i;
+    bool ok = ch < (uint32_t)NCH && m < M && k0 + 8 <= K;
+    if (ok) {
+      const float4* ap = (const float4*)(A + (size_t)m * K + k0);
+      float4 x0 = ap[0], x1 = ap[1];
+      av[cc][0] = x0.x; av[cc][1] = x0.y; av[cc][2] = x0.z; av[cc][3] = x0.w;
+      av[cc][4] = x1.x; av[cc][5] = x1.y; av[cc][6] = x1.z; av[cc][7] = x1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        uint32_t k = k0 + e;
+        av[cc][e] = (ch < (uint32_t)NCH && m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
+      }
+    }
+  }
+
+  // 2. weights: every record of this wave, all loads in flight
+  Rec<FMT> wr[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+
+  // 3. activations -> f16 hi/lo fragments + (C1, S) in LDS
+#pragma unroll
+  for (int cc = 0; cc < CPT; cc++) {
+    uint32_t ch = threadIdx.x + cc * NT;
+    uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
+    float c1h = 0.f, sh_ = 0.f, c1l = 0.f, sl = 0.f;
+    _Float16 hv[8], lv[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      int el = FMT == FMT_Q8 ? perm_q8[e] : perm_q4[e];
+      float off = FMT == FMT_Q8 ? 1152.f : off_q4[e];
+      float a = av[cc][el];
+      _Float16 h = (_Float16)a;
+      float hf = (float)h;
+      _Float16 l = (_Float16)((a - hf) * 2048.0f);
+      float lf = (float)l;
+      hv[e] = h;
+      lv[e] = l;
+      c1h = __builtin_fmaf(hf, off, c1h);
+      sh_ += hf;
+      c1l = __builtin_fmaf(lf, off, c1l);
+      sl += lf;
+    }
+    float c1 = __builtin_fmaf(c1l, 1.0f / 2048.0f, c1h);
+    float sm = __builtin_fmaf(sl, 1.0f / 2048.0f, sh_);
+    // the four mfma slices of (group, row) are adjacent threads
+    c1 += __shfl_xor(c1, 1);
+    sm += __shfl_xor(sm, 1);
+    c1 += __shfl_xor(c1, 2);
+    sm += __shfl_xor(sm, 2);
+    if (FMT == FMT_Q40) c1 = __builtin_fmaf(8.0f, sm, c1);
+    if (ch < (uint32_t)NCH) {
+      u32x4 hp, lp;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        hp[q] = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[2 * q], hv[2 * q + 1]});
+        lp[q] = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[2 * q], lv[2 * q + 1]});
+      }
+      fragL[gl][2 * m][i] = hp;
+      fragL[gl][2 * m + 1][i] = lp;
+      if (i == 0) cL[gl][m] = make_float2(c1, sm);
+    }
+  }
+  __syncthreads();
+
+  // 4. MFMAs: lane (r = lane%16, j) feeds A row r from K slice j only
+  const uint32_t r = lane & 15;
+  const bool a_active = (r >> 2) == j && (r & 3) < 2 * MR;
+  const uint32_t ru = a_active ? (r & 3) : 0;
+  float acc[CT][MR];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[ct][m] = 0.f;
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const uint32_t gl = wk * GPW + 4 * st + j;
+    half8 af[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      u32x4 v = fragL[gl][ru][i];
+      af[i] = __builtin_bit_cast(half8, a_active ? v : (u32x4){0u, 0u, 0u, 0u});
+    }
+    float2 cv[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) cv[m] = cL[gl][m];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], rec_to_f16<FMT>(wr[st][ct], i), p, 0, 0, 0);
+      float s = wr[st][ct].s, z = wr[st][ct].z;
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        float t = __builtin_fmaf(p[2 * m + 1], 1.0f / 2048.0f, p[2 * m]) - cv[m].x;
+        if (FMT == FMT_Q4S) t = __builtin_fmaf(-z, cv[m].y, t);
+        acc[ct][m] = __builtin_fmaf(s, t, acc[ct][m]);
+      }
+    }
+  }
+
+  // 5. sum the four lane groups (different K groups, same column), then the
+  //    WK waves of the block in fixed order
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float v = acc[ct][m];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (j == 0) red[wk][m][wn * 16 * CT + ct * 16 + c] = v;
+    }
+  __syncthreads();
+  const uint32_t nb = blockIdx.x * BC;
+  const uint32_t mrows = M < (uint32_t)MR ? M : MR;
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+    uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WK; w++) v += red[w][m][cc];
+    if (n >= N) continue;
+    if (ksplit == 1)
+      C[(size_t)m * N + n] = v;
+    else
+      __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (ksplit == 1) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == ksplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+    uint32_t m = e / BC, n = nb + e % BC;
+    if (n >= N) continue;
+    float v = 0.f;
+    for (uint32_t sp = 0; sp < ksplit; sp++)
+      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    C[(size_t)m * N + n] = v;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define DEF_QGEMV1(NAME, FMT, MR, CT, WK, WN, S)                                                        \
+  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(const float* A, const uint8_t* B,     \
+                                                                  const uint16_t* D, float* C, float* ws, \
+                                                                  uint32_t* counters, uint32_t M,       \
+                                                                  uint32_t N, uint32_t K, uint32_t G) { \
+    qgemv1_body<FMT, MR, CT, WK, WN, S>(A, B, D, C, ws, counters, M, N, K, G);                           \
+  }
+
+// Fused M <= 2 variants: "k128" = 8 waves x 4 steps (128 groups per block),
+// "k64" = 4 waves x 4 steps (64 groups per block).
+#define DEF_QGEMV1_FMT(TAG, FMT)                                          \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k128, FMT, 2, 1, 8, 1, 4)            \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)
+
+#ifndef SMITH_NO_INSTANCES
 DEF_QGEMV_FMT(q4s, FMT_Q4S)
 DEF_QGEMV_FMT(q8, FMT_Q8)
 DEF_QGEMV_FMT(q40, FMT_Q40)
+DEF_QGEMV1_FMT(q4s, FMT_Q4S)
+DEF_QGEMV1_FMT(q8, FMT_Q8)
+DEF_QGEMV1_FMT(q40, FMT_Q40)
+#endif
 
 // Zero fill (used instead of hipMemsetAsync so the op stays a plain kernel).
 extern "C" __global__ void smith_zero_u32(uint32_t* __restrict__ p, uint64_t n) {
