@@ -170,70 +170,47 @@ int ensure_counters(Ctx* c, size_t n) {
   return 0;
 }
 
-// ----- GEMV variant table (must match DEF_QGEMV_FMT in smith_kernels.hip) -----
-struct Variant {
-  int mb;      // max rows
-  int rb;      // row blocks (MFMAs per tile)
-  bool hilo;   // hi/lo activation split
-  int ct, gpw, wk, wn;
-  const char* suffix;
-};
-const Variant kVariants[] = {
-    {1, 1, true, 1, 8, 4, 1, "m1"},     {2, 1, true, 1, 8, 4, 1, "m2"},    {4, 1, true, 1, 8, 4, 1, "m4"},
-    {8, 1, true, 1, 8, 4, 1, "m8"},     {16, 1, false, 2, 8, 4, 1, "m16"}, {32, 2, false, 2, 8, 4, 1, "m32"},
-};
-const Variant& pick_variant(uint32_t M) {
-  for (const Variant& v : kVariants)
-    if ((uint32_t)v.mb >= M) return v;
-  return kVariants[5];
-}
-
 enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2 };
 
-// One GEMV chunk of at most 32 rows: prepare activations, then the MFMA GEMV.
-int qgemv_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
-                uint32_t N, uint32_t K, uint32_t G) {
-  const Variant& v = pick_variant(M);
+// M > 2: prepare the activations once (smith_qprep_*), then the 16-row
+// MFMA GEMV (smith_qgemv3_*).  Buckets must match DEF_QGEMV3_FMT.
+int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
+                 uint32_t N, uint32_t K, uint32_t G) {
   const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
   const char* ptag = fmt == FQ4S ? "q4" : (fmt == FQ8 ? "q8" : "q40");
-  uint32_t RB = (uint32_t)v.rb;
+  uint32_t bucket = M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
+  bool hilo = bucket <= 8;
+  uint32_t RB = bucket == 32 ? 2 : 1;
   size_t frag_bytes = (size_t)RB * G * 64 * 16;
   size_t cst_bytes = (size_t)RB * G * 16 * 8;
   if (ensure(c, &c->prep, &c->prep_bytes, frag_bytes + cst_bytes)) return -1;
   void* frag = c->prep;
   void* cst = (char*)c->prep + frag_bytes;
-
   char name[64];
-  snprintf(name, sizeof name, "smith_qprep_%s_%s", ptag, v.hilo ? "hilo" : "plain");
-  uint32_t rpr = v.hilo ? 8 : 16;
-  uint64_t threads = (uint64_t)RB * rpr * G * 4;
+  snprintf(name, sizeof name, "smith_qprep_%s_%s", ptag, hilo ? "hilo" : "plain");
+  uint64_t threads = (uint64_t)RB * (hilo ? 8 : 16) * G * 4;
   {
     const float* pa = a;
     uint32_t pM = M, pK = K, pG = G, pRB = RB;
     void* args[] = {&pa, &frag, &cst, &pM, &pK, &pG, &pRB};
     if (launch(c, name, dim3((unsigned)((threads + 255) / 256)), dim3(256), args)) return -1;
   }
-
-  uint32_t bc = 16 * (uint32_t)(v.ct * v.wn);
+  const uint32_t bc = 32, kb = 32, nthreads = 512;  // CT=2, S=1, WK=8
   uint32_t gx = (N + bc - 1) / bc;
-  uint32_t per_block = (uint32_t)(v.wk * v.gpw);
-  uint32_t ksplit = (G + per_block - 1) / per_block;
+  uint32_t ksplit = (G + kb - 1) / kb;
   if (ksplit > 1) {
     if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
     if (ensure_counters(c, gx)) return -1;
   }
-  snprintf(name, sizeof name, "smith_qgemv_%s_%s", tag, v.suffix);
-  {
-    const void* pB = B;
-    const void* pD = D;
-    float* pC = out;
-    float* pws = c->ws;
-    uint32_t* pcnt = c->counters;
-    uint32_t pM = M, pN = N, pG = G;
-    void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG};
-    if (launch(c, name, dim3(gx, ksplit), dim3(64 * v.wk * v.wn), args)) return -1;
-  }
-  return 0;
+  snprintf(name, sizeof name, "smith_qgemv3_%s_m%u", tag, bucket);
+  const void* pB = B;
+  const void* pD = D;
+  float* pC = out;
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pM = M, pN = N, pG = G;
+  void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG};
+  return launch(c, name, dim3(gx, ksplit), dim3(nthreads), args);
 }
 
 // M <= 2: the fused kernel (activation prep in LDS, whole records per lane,
@@ -272,7 +249,7 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
     uint32_t mc = std::min<uint32_t>(32, M - m0);
     const float* am = a + (size_t)m0 * K;
     float* om = out + (size_t)m0 * N;
-    int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G) : qgemv_chunk(c, fmt, am, B, D, om, mc, N, K, G);
+    int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G) : qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G);
     if (rc) return -1;
   }
   return 0;

@@ -14,26 +14,22 @@
 //           into planes without touching a byte: nibbles nib[(g*N+n)*16..]
 //           and f16 scales d[g*N+n]; w = d*(nib - 8), interleaved nibbles.
 //
-// Decode GEMV (M <= 32) -- the HBM-bound hot path.  One wave computes a
-// 16-column x 32-K "tile" per MFMA (v_mfma_f32_16x16x32_f16):
-//   * B operand = the weights.  Each lane owns one column (lane%16) and one
-//     8-element K slice (lane/16) of a 32-K group, i.e. exactly one dword of
-//     the record's nibble area (Q4) or 8 int8 bytes (Q8).  Nibbles become f16
-//     with one v_and_or_b32 per pair using exponent-bias magic numbers
-//     (0x6400 -> 1024+q for a low nibble, 0x5400 -> 64+q for a high nibble;
-//     int8 bytes -> 1024+(q+128) with v_perm_b32), so B holds exact integers
-//     plus a known per-slot offset.
-//   * A operand = activations, pre-split into f16 hi + f16 lo*2048 rows
-//     ("hi/lo", M <= 8) so the product keeps ~22 bits of each f32
-//     activation, or plain f16 rows (M > 8).  Prepared once per matmul by
-//     qprep_* into a fragment-ready buffer together with two per-row,
-//     per-group constants: C1 = sum(a*offset) (+ folded zero) and S = sum(a).
-//   * Per group the MFMA result P is turned into the exact group
-//     contribution scale*(P - C1 - zero*S) and accumulated in f32.  The
-//     per-group scale/zero therefore never touch the f16 path.
-// Split-K across workgroups is reduced deterministically: partials go to a
-// workspace and the last-arriving workgroup of each column block sums them in
-// fixed order (agent-scope atomic RMWs + counter; the counter self-resets).
+// Decode GEMV (M <= 32) -- the HBM-bound hot path -- on
+// v_mfma_f32_16x16x32_f16 with EXACT weights: nibbles / int8 become f16
+// integers plus a known per-slot offset with one v_and_or_b32 (or v_perm_b32)
+// per pair, using exponent-bias magic numbers (0x6400 -> 1024+q for a low
+// nibble, 0x5400 -> 64+q for a high nibble, 1024+(q+128) for int8).
+// Activations are split into f16 hi + f16 lo*2048 ("hi/lo", M <= 8) so the
+// products keep ~22 bits of each f32 activation, or plain f16 (M > 8).  Per
+// 32-K group and activation row the MFMA result P becomes the exact group
+// contribution scale * (P - C1 - zero * S), with C1 = sum(a * offset) and
+// S = sum(a), accumulated in f32; scale and zero never touch the f16 path.
+//   smith_qgemv1_*  M <= 2: activation prep fused (LDS), one kernel per call
+//   smith_qgemv3_*  M >  2: activations prepared once by smith_qprep_*
+// Split-K across workgroups (only when a block does not cover K) is reduced
+// deterministically: partials go to a workspace through agent-scope atomic
+// RMWs and the last-arriving workgroup of each column block sums them in
+// fixed order (the counter self-resets).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -344,232 +340,6 @@ DEF_QPREP(smith_qprep_q8_hilo, FMT_Q8, true)
 DEF_QPREP(smith_qprep_q8_plain, FMT_Q8, false)
 
 // ---------------------------------------------------------------------------
-// Weight tile loads and nibble/int8 -> f16 conversion (B operand).
-// ---------------------------------------------------------------------------
-struct WTile {
-  uint32_t q0, q1, q2;  // Q4: q0 = nibble dword; Q8: 3 raw dwords + shift
-  uint32_t sh;
-  float s, z;
-};
-
-// Branch-free: an out-of-range tile (g >= G or n >= N) loads from a clamped,
-// valid record and gets scale 0, so it contributes exactly 0 and the
-// compiler can keep every load of the wave in flight at once.  The Q8 path
-// always reads three dwords; the last one may extend 2 bytes past the final
-// record, which stays inside smith_alloc's 256-byte tail padding.
-template <int FMT>
-__device__ __forceinline__ WTile load_tile(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
-                                           uint32_t N, uint32_t G, uint32_t g, uint32_t n, uint32_t kq) {
-  WTile t;
-  bool ok = g < G && n < N;
-  size_t rec = (size_t)(g < G ? g : G - 1) * N + (n < N ? n : N - 1);
-  t.q1 = t.q2 = 0;
-  t.sh = 0;
-  t.z = 0.f;
-  if (FMT == FMT_Q4S) {
-    const uint8_t* p = B + rec * 24;
-    t.q0 = *(const uint32_t*)(p + 4 * kq);
-    float2 sz = *(const float2*)(p + 16);
-    t.s = sz.x;
-    t.z = sz.y;
-  } else if (FMT == FMT_Q40) {
-    t.q0 = *(const uint32_t*)(B + rec * 16 + 4 * kq);
-    t.s = (float)__builtin_bit_cast(_Float16, D[rec]);
-  } else {
-    const uint8_t* p = B + rec * 34;
-    t.s = (float)__builtin_bit_cast(_Float16, *(const uint16_t*)p);
-    size_t a = (size_t)(p + 2 + 8 * kq);
-    const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
-    t.sh = (uint32_t)(a & 3) * 8;  // 0 or 16 bits
-    t.q0 = w[0];
-    t.q1 = w[1];
-    t.q2 = w[2];
-  }
-  t.s = ok ? t.s : 0.f;
-  t.z = ok ? t.z : 0.f;
-  return t;
-}
-
-template <int FMT>
-__device__ __forceinline__ half8 tile_to_f16(const WTile& t) {
-  u32x4 u;
-  if (FMT == FMT_Q8) {
-    uint32_t x0 = __builtin_amdgcn_alignbyte(t.q1, t.q0, t.sh >> 3) ^ 0x80808080u;
-    uint32_t x1 = __builtin_amdgcn_alignbyte(t.q2, t.q1, t.sh >> 3) ^ 0x80808080u;
-    u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);  // (1024+u0, 1024+u2)
-    u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);  // (1024+u1, 1024+u3)
-    u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);  // (1024+u4, 1024+u6)
-    u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);  // (1024+u5, 1024+u7)
-  } else {
-    uint32_t x = t.q0, y = t.q0 >> 8;
-    u.x = (x & 0x000F000Fu) | 0x64006400u;  // (1024+e0, 1024+e4)
-    u.y = (x & 0x00F000F0u) | 0x54005400u;  // (64+e1, 64+e5)
-    u.z = (y & 0x000F000Fu) | 0x64006400u;  // (1024+e2, 1024+e6)
-    u.w = (y & 0x00F000F0u) | 0x54005400u;  // (64+e3, 64+e7)
-  }
-  return __builtin_bit_cast(half8, u);
-}
-
-// ---------------------------------------------------------------------------
-// The GEMV.  Template parameters:
-//   RB   row blocks (MFMAs per tile); HILO hi/lo activation rows
-//   VPL  accumulator values per lane that carry real rows (<= 4)
-//   CT   16-column tiles per wave; GPW groups per wave
-//   WK x WN waves per block: WK waves split the block's groups (reduced in
-//   LDS), WN waves sit side by side along N (longer contiguous weight runs)
-// Grid: x = column blocks of 16*CT*WN columns, y = K splits of WK*GPW groups.
-// ---------------------------------------------------------------------------
-template <int FMT, int RB, bool HILO, int VPL, int CT, int GPW, int WK, int WN>
-__device__ __forceinline__ void qgemv_body(const u32x4* __restrict__ frag, const float2* __restrict__ cst,
-                                           const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
-                                           float* __restrict__ C, float* __restrict__ ws,
-                                           uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
-                                           uint32_t G) {
-  constexpr int BC = 16 * CT * WN;
-  constexpr int VR = 16;  // virtual rows per row block
-  __shared__ float red[WK][RB][VR][BC];
-  __shared__ int s_last;
-
-  const uint32_t lane = threadIdx.x & 63;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t wk = wave / WN, wn = wave % WN;
-  const uint32_t col = lane & 15, kq = lane >> 4;
-  const uint32_t n0 = blockIdx.x * BC;
-  const uint32_t nw = n0 + wn * (16 * CT);  // first column of this wave
-  const uint32_t ksplit = gridDim.y;
-  const uint32_t g0 = (blockIdx.y * WK + wk) * GPW;
-
-  // Issue every load of the wave first (weights, activation fragments,
-  // row constants) so all of them are in flight together, then compute.
-  WTile wt[GPW][CT];
-#pragma unroll
-  for (int j = 0; j < GPW; j++)
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
-      uint32_t g = g0 + j, n = nw + ct * 16 + col;
-      wt[j][ct] = load_tile<FMT>(B, D, N, G, g, n, kq);
-    }
-  u32x4 afr[GPW][RB];
-  float4 cvv[GPW][RB][(VPL + 1) / 2];
-#pragma unroll
-  for (int j = 0; j < GPW; j++) {
-    uint32_t g = g0 + j < G ? g0 + j : G - 1;
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-      afr[j][rb] = frag[((size_t)rb * G + g) * 64 + lane];
-      const float4* cp = (const float4*)(cst + ((size_t)rb * G + g) * 16 + kq * 4);
-#pragma unroll
-      for (int h = 0; h < (VPL + 1) / 2; h++) cvv[j][rb][h] = cp[h];
-    }
-  }
-
-  f32x4 acc[CT][RB];
-#pragma unroll
-  for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  // no early exit: groups past G carry scale 0 (straight-line code keeps the
-  // loads above from being sunk into the loop)
-#pragma unroll
-  for (int j = 0; j < GPW; j++) {
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++) {
-      half8 bf = tile_to_f16<FMT>(wt[j][ct]);
-      float s = wt[j][ct].s, z = wt[j][ct].z;
-#pragma unroll
-      for (int rb = 0; rb < RB; rb++) {
-        f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, afr[j][rb]), bf,
-                                                         (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < VPL; i++) {
-          float4 c2 = cvv[j][rb][i >> 1];
-          float c1 = (i & 1) ? c2.z : c2.x, sr = (i & 1) ? c2.w : c2.y;
-          float t = p[i] - c1;
-          if (FMT == FMT_Q4S) t = __builtin_fmaf(-z, sr, t);
-          acc[ct][rb][i] = __builtin_fmaf(s, t, acc[ct][rb][i]);
-        }
-      }
-    }
-  }
-
-  // per-wave partials -> LDS: lane holds virtual rows 4*kq+i of column col
-#pragma unroll
-  for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        red[wk][rb][kq * 4 + i][wn * 16 * CT + ct * 16 + col] = i < VPL ? acc[ct][rb][i] : 0.f;
-  __syncthreads();
-
-  // combine waves (+ hi/lo) in fixed order; thread -> (row, column)
-  const uint32_t rows_per_rb = HILO ? 8 : 16;
-  const uint32_t nthreads = WK * WN * 64;
-  const uint32_t mrows = M < (uint32_t)(RB * rows_per_rb) ? M : RB * rows_per_rb;
-  for (uint32_t e = threadIdx.x; e < mrows * BC; e += nthreads) {
-    uint32_t m = e / BC, c = e % BC;
-    uint32_t rb = m / rows_per_rb, r = m % rows_per_rb;
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < WK; w++) {
-      if (HILO) v += red[w][rb][r][c] + red[w][rb][r + 8][c] * (1.0f / 2048.0f);
-      else v += red[w][rb][r][c];
-    }
-    uint32_t n = n0 + c;
-    if (n >= N) continue;
-    if (ksplit == 1) {
-      C[(size_t)m * N + n] = v;
-    } else {
-      // Agent-scope atomic RMWs are performed at the device's point of
-      // coherence, so partials written this way are visible to a workgroup
-      // on any XCD without the whole-L2 writeback a release fence costs.
-      __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
-                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (ksplit == 1) return;
-
-  __builtin_amdgcn_s_waitcnt(0);  // every exchange of this thread has been performed
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == ksplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for (uint32_t e = threadIdx.x; e < mrows * BC; e += nthreads) {
-    uint32_t m = e / BC, c = e % BC;
-    uint32_t n = n0 + c;
-    if (n >= N) continue;
-    float v = 0.f;
-    for (uint32_t s = 0; s < ksplit; s++)
-      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)s * M + m) * N + n, 0u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    C[(size_t)m * N + n] = v;
-  }
-  if (threadIdx.x == 0)
-    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-#define DEF_QGEMV(NAME, FMT, RB, HILO, VPL, CT, GPW, WK, WN)                                           \
-  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                     \
-      const u32x4* frag, const float2* cst, const uint8_t* B, const uint16_t* D, float* C, float* ws,  \
-      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G) {                                        \
-    qgemv_body<FMT, RB, HILO, VPL, CT, GPW, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G);       \
-  }
-
-// Row buckets: M=1 (hi/lo, 1 value/lane), 2, 4 (hi/lo), 8 (hi/lo, 4 values),
-// 16 (plain, 1 MFMA), 32 (plain, 2 MFMAs).
-#define DEF_QGEMV_FMT(TAG, FMT)                                           \
-  DEF_QGEMV(smith_qgemv_##TAG##_m1, FMT, 1, true, 1, 1, 8, 4, 1)          \
-  DEF_QGEMV(smith_qgemv_##TAG##_m2, FMT, 1, true, 2, 1, 8, 4, 1)          \
-  DEF_QGEMV(smith_qgemv_##TAG##_m4, FMT, 1, true, 4, 1, 8, 4, 1)          \
-  DEF_QGEMV(smith_qgemv_##TAG##_m8, FMT, 1, true, 4, 1, 8, 4, 1)          \
-  DEF_QGEMV(smith_qgemv_##TAG##_m16, FMT, 1, false, 4, 2, 8, 4, 1)        \
-  DEF_QGEMV(smith_qgemv_##TAG##_m32, FMT, 2, false, 4, 2, 8, 4, 1)
-
-// ---------------------------------------------------------------------------
 // Decode GEMV for M <= 2 with the activation prep fused (no prep launch).
 //
 // Lane (c = lane%16, j = lane/16) loads the WHOLE weight record of column
@@ -848,6 +618,196 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     qgemv1_body<FMT, MR, CT, WK, WN, S>(A, B, D, C, ws, counters, M, N, K, G);                           \
   }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV for 2 < M <= 32 (16-row MFMA layout, prepared activations).
+//
+// Loads are as in the fused kernel (lane (c, j) fetches the whole record of
+// column c in group g+j with 128-bit loads); a 4x4 transpose of dwords across
+// the four lane groups (v_permlane32_swap + v_permlane16_swap) then gives
+// every lane (c, kq) dword kq of each of the four records, i.e. the
+// K-slice layout of v_mfma_f32_16x16x32_f16 in which all 16 MFMA rows carry
+// activation rows (8 hi/lo rows, or 16 plain rows, per row block).  The
+// activation fragments and (C1, S) come from smith_qprep_* (one pass over A
+// shared by every workgroup).  Scale / zero of group g+t reach all lanes of a
+// column with ds_bpermute from lane group t.
+// Grid: x = column blocks of 16*CT*WN, y = K splits of 4*S*WK groups.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void xpose4(uint32_t& x0, uint32_t& x1, uint32_t& x2, uint32_t& x3) {
+  // in: lane group j holds X[j][0..3] in (x0..x3); out: lane group i holds X[0..3][i]
+  // in (x0..x3), i.e. register t of lane group i = X[t][i].
+  auto a = __builtin_amdgcn_permlane32_swap(x0, x2, false, false);
+  auto b = __builtin_amdgcn_permlane32_swap(x1, x3, false, false);
+  auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  x0 = c[0];
+  x1 = c[1];
+  x2 = d[0];
+  x3 = d[1];
+}
+
+template <int FMT, int RB, bool HILO, int VPL, int CT, int S, int WK, int WN>
+__device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, const float2* __restrict__ cst,
+                                            const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
+                                            float* __restrict__ C, float* __restrict__ ws,
+                                            uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
+                                            uint32_t G) {
+  constexpr int GPW = 4 * S;
+  constexpr int BC = 16 * CT * WN;
+  constexpr int NT = 64 * WK * WN;
+  __shared__ float red[WK][RB][16][BC];
+  __shared__ int s_last;
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wk = wave / WN, wn = wave % WN;
+  const uint32_t c = lane & 15, j = lane >> 4;
+  const uint32_t n0 = blockIdx.x * BC + wn * 16 * CT;
+  const uint32_t ksplit = gridDim.y;
+  const uint32_t g0 = (blockIdx.y * WK + wk) * GPW;
+
+  Rec<FMT> wr[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, g0 + 4 * st + j, n0 + ct * 16 + c);
+  u32x4 afr[S][4][RB];
+  float4 cvv[S][4][RB][(VPL + 1) / 2];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      uint32_t g = g0 + 4 * st + t;
+      g = g < G ? g : G - 1;
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) {
+        afr[st][t][rb] = frag[((size_t)rb * G + g) * 64 + lane];
+        const float4* cp = (const float4*)(cst + ((size_t)rb * G + g) * 16 + j * 4);
+#pragma unroll
+        for (int h = 0; h < (VPL + 1) / 2; h++) cvv[st][t][rb][h] = cp[h];
+      }
+    }
+
+  f32x4 acc[CT][RB];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      const Rec<FMT>& rr = wr[st][ct];
+      // K-slice operands of the four records after the transpose
+      half8 bf[4];
+      if (FMT == FMT_Q8) {
+        uint32_t d[9] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w, rr.q8b.x, rr.q8b.y, rr.q8b.z, rr.q8b.w, rr.q8c};
+        uint32_t e[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) e[q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], rr.sh);
+        xpose4(e[0], e[2], e[4], e[6]);
+        xpose4(e[1], e[3], e[5], e[7]);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          uint32_t x0 = e[2 * t] ^ 0x80808080u, x1 = e[2 * t + 1] ^ 0x80808080u;
+          u32x4 u;
+          u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);
+          u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);
+          u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);
+          u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);
+          bf[t] = __builtin_bit_cast(half8, u);
+        }
+      } else {
+        uint32_t x[4] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w};
+        xpose4(x[0], x[1], x[2], x[3]);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          uint32_t y = x[t] >> 8;
+          u32x4 u;
+          u.x = (x[t] & 0x000F000Fu) | 0x64006400u;
+          u.y = (x[t] & 0x00F000F0u) | 0x54005400u;
+          u.z = (y & 0x000F000Fu) | 0x64006400u;
+          u.w = (y & 0x00F000F0u) | 0x54005400u;
+          bf[t] = __builtin_bit_cast(half8, u);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        float s = __shfl(rr.s, (int)(c + 16 * t));
+        float z = FMT == FMT_Q4S ? __shfl(rr.z, (int)(c + 16 * t)) : 0.f;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+          f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, afr[st][t][rb]), bf[t],
+                                                           (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < VPL; i++) {
+            float4 c2 = cvv[st][t][rb][i >> 1];
+            float c1 = (i & 1) ? c2.z : c2.x, sr = (i & 1) ? c2.w : c2.y;
+            float tt = p[i] - c1;
+            if (FMT == FMT_Q4S) tt = __builtin_fmaf(-z, sr, tt);
+            acc[ct][rb][i] = __builtin_fmaf(s, tt, acc[ct][rb][i]);
+          }
+        }
+      }
+    }
+
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        red[wk][rb][j * 4 + i][wn * 16 * CT + ct * 16 + c] = i < VPL ? acc[ct][rb][i] : 0.f;
+  __syncthreads();
+  const uint32_t rows_per_rb = HILO ? 8 : 16;
+  const uint32_t mrows = M < (uint32_t)(RB * rows_per_rb) ? M : RB * rows_per_rb;
+  const uint32_t nb = blockIdx.x * BC;
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+    uint32_t m = e / BC, cc = e % BC;
+    uint32_t rb = m / rows_per_rb, rr = m % rows_per_rb;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WK; w++) {
+      if (HILO) v += red[w][rb][rr][cc] + red[w][rb][rr + 8][cc] * (1.0f / 2048.0f);
+      else v += red[w][rb][rr][cc];
+    }
+    uint32_t n = nb + cc;
+    if (n >= N) continue;
+    if (ksplit == 1)
+      C[(size_t)m * N + n] = v;
+    else
+      __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (ksplit == 1) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == ksplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+    uint32_t m = e / BC, n = nb + e % BC;
+    if (n >= N) continue;
+    float v = 0.f;
+    for (uint32_t sp = 0; sp < ksplit; sp++)
+      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    C[(size_t)m * N + n] = v;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define DEF_QGEMV3(NAME, FMT, RB, HILO, VPL, CT, S, WK, WN)                                             \
+  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                       \
+      const u32x4* frag, const float2* cst, const uint8_t* B, const uint16_t* D, float* C, float* ws,    \
+      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G) {                                          \
+    qgemv3_body<FMT, RB, HILO, VPL, CT, S, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G);           \
+  }
+
 // Fused M <= 2 variants: "k128" = 8 waves x 4 steps (128 groups per block),
 // "k64" = 4 waves x 4 steps (64 groups per block).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
@@ -856,10 +816,18 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k128, FMT, 2, 1, 8, 1, 4)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)
 
+// M > 2 row buckets (RB, HILO, VPL): m4 / m8 hi/lo, m16 / m32 plain f16;
+// 2 column tiles x 1 step per wave, 8 waves split the block's 32 groups.
+#define DEF_QGEMV3_FMT(TAG, FMT)                                          \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m4, FMT, 1, true, 4, 2, 1, 8, 1)        \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m8, FMT, 1, true, 4, 2, 1, 8, 1)        \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m16, FMT, 1, false, 4, 2, 1, 8, 1)      \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m32, FMT, 2, false, 4, 2, 1, 8, 1)
+
 #ifndef SMITH_NO_INSTANCES
-DEF_QGEMV_FMT(q4s, FMT_Q4S)
-DEF_QGEMV_FMT(q8, FMT_Q8)
-DEF_QGEMV_FMT(q40, FMT_Q40)
+DEF_QGEMV3_FMT(q4s, FMT_Q4S)
+DEF_QGEMV3_FMT(q8, FMT_Q8)
+DEF_QGEMV3_FMT(q40, FMT_Q40)
 DEF_QGEMV1_FMT(q4s, FMT_Q4S)
 DEF_QGEMV1_FMT(q8, FMT_Q8)
 DEF_QGEMV1_FMT(q40, FMT_Q40)
