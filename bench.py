@@ -29,6 +29,10 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 400 << 20
+# HBM bytes per config-1 GEMV launch from two rocprofv3 --pmc passes
+# (profiles/qgemv1_q4s_m1_cfg1_hbm_traffic.md): FETCH_SIZE 6251.5 KiB x 1.996
+# (factor from a 12,582,912 B device copy) + WRITE_SIZE 16.0 KiB x 1.0.
+TRAFFIC_CFG1 = 12793900
 
 
 def log(*a):
@@ -173,6 +177,43 @@ def cpu_baseline(K, N, budget_s):
                       "%.1f ms/call; host has %d cpus" % (reps, el, per * 1e3, os.cpu_count() or 0)}
 
 
+def calibrate(D, steps):
+    """Platform floor: per-launch duration of an empty kernel and of a plain
+    128-bit streaming read of the config-1/3 weight sizes (HIP events over
+    back-to-back launches, buffers rotated over >= 800 MB)."""
+    import struct
+    res = {}
+    out = D.alloc(4096)
+    for name in ("smith_calib_empty", "smith_calib_stream_read"):
+        p = D.pipeline(name)
+        for size in (12582912, 44040192, 201326592):
+            reps = max(2, -(-(800 << 20) // size))
+            bufs = [D.alloc(size) for _ in range(reps)]
+            for b in bufs:
+                D.check(D.lib.smith_fill_zero(D.ctx(), b, size))
+
+            def launch(i):
+                enc = D.lib.smith_begin(D.ctx())
+                D.lib.smith_set_pipeline(enc, p)
+                D.lib.smith_set_buffer(enc, bufs[i % reps], 0)
+                prm = struct.pack("<Q", size // 16)
+                D.lib.smith_set_bytes(enc, prm, 8, 1)
+                D.lib.smith_set_buffer(enc, out, 2)
+                D.lib.smith_dispatch(enc, 1024 * 256, 1, 1, 256, 1, 1)
+                D.lib.smith_wait(D.lib.smith_end_async(enc))
+
+            for i in range(5):
+                launch(i)
+            D.timer_start()
+            for i in range(steps):
+                launch(i)
+            us = D.timer_stop() * 1e3 / steps
+            res["%s_%dB" % (name, size)] = {"us": round(us, 2), "GBps": round(size / us / 1e3, 1)}
+            for b in bufs:
+                D.release_buffer(b)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -180,6 +221,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no sweep / cpu baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate", action="store_true", help="print the platform floor (empty kernel, streaming read)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (--gpus %d requested); the sharding design is "
@@ -192,6 +234,9 @@ def main():
 
     D.ops_ctx()
     log("device:", D.device_name())
+    if args.calibrate:
+        print(json.dumps({"calibration": calibrate(D, args.steps)}), flush=True)
+        return
     K = N = 4096
     ms, kt, nbytes = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup)
     assert kt["launches_per_step"] == 1, kt  # the M=1 path is one fused kernel
@@ -256,7 +301,7 @@ def main():
                    "M": 1, "K": K, "N": N, "format": "Q4S", "algorithmic_bytes_per_step": nbytes},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1,
                      "kernel": "smith_qgemv1_q4s_m1_k128", "kernel_us": round(ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "configs": configs,

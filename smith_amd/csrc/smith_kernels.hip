@@ -838,3 +838,27 @@ extern "C" __global__ void smith_zero_u32(uint32_t* __restrict__ p, uint64_t n) 
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = 0u;
 }
+
+// Platform calibration (bench.py --calibrate): a plain 128-bit streaming read
+// with U loads in flight per thread, and an empty kernel.  They bound what
+// any kernel reading the same bytes can achieve on this GPU.
+extern "C" __global__ void smith_calib_stream_read(const uint4* __restrict__ p, uint64_t n16, uint32_t* out) {
+  constexpr int U = 4;
+  uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0;
+  for (uint64_t base = tid; base < n16; base += stride * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      uint64_t i = base + u * stride;
+      v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads alive
+}
+
+extern "C" __global__ void smith_calib_empty(const uint4* p, uint64_t n16, uint32_t* out) {
+  if (n16 == 0x12345u) out[0] = (uint32_t)(size_t)p;
+}
