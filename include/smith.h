@@ -136,6 +136,59 @@ int smith_matmul_q4_0(void* ctx, const float* a, const void* nib, const void* d,
  * Used to write synthetic GGUF files; out receives rows*cols/32*18 bytes. */
 int smith_quantize_q4_0(void* ctx, const float* x, void* out, uint32_t rows, uint32_t cols);
 
+/* ---- GGUF Llama decode path (loadGGUF(...).generate) ----
+ * Weights listed [out=N, in=K] in the file.  The *_into repacks place column
+ * n of a weight at column n_off + n*n_stride of a shared N_total-column
+ * buffer (q|k|v concatenated; gate/up interleaved for the SwiGLU epilogue),
+ * moving blocks without changing a byte (gguf_loader.js:216-273 keeps
+ * nothing quantized; this is the wiring SURVEY.md f1 calls for). */
+int smith_repack_q4_0_into(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K,
+                           uint32_t n_off, uint32_t n_stride, uint32_t N_total);
+int smith_repack_q8_0_into(void* ctx, const void* blocks, void* dst, uint32_t N, uint32_t K, uint32_t n_off,
+                           uint32_t n_stride, uint32_t N_total);
+/* linear (nn.js:22-25) on a repacked Q4_0 / Q8 weight with optional fusions:
+ * norm_gamma != NULL: RMSNorm of each x row first (rmsnorm.metal:15-47);
+ * epilogue 0: out = y; 1: out = resid + y (gguf_cache.js:159,171);
+ * 2: columns are (gate, up) pairs, out[M, N/2] = silu(gate) * up
+ * (swiglu.metal:12-21). */
+int smith_linear_q4_0(void* ctx, const float* x, const void* nib, const void* d, float* out, uint32_t M, uint32_t N,
+                      uint32_t K, const float* norm_gamma, float eps, const float* resid, uint32_t epilogue);
+int smith_linear_q8(void* ctx, const float* x, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
+                    const float* norm_gamma, float eps, const float* resid, uint32_t epilogue);
+/* rmsnormForward (ops/rmsnorm.js:19-37) over rows. */
+int smith_rmsnorm(void* ctx, const float* x, const float* gamma, float* out, uint32_t rows, uint32_t cols, float eps);
+/* embedding gather (autograd.js:308-334): out[r] = E[tokens[r]]. */
+int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, uint32_t rows, uint32_t dim);
+/* RoPE (whole-row indexing of rope.metal:18-37 as gguf_cache.js applies it)
+ * + KV-cache append + GQA softmax attention for S rows at positions
+ * *pos_ptr .. *pos_ptr+S-1 (gguf_cache.js:128-157, 212-231).  qkv rows are
+ * [q | k | v] with stride ld; caches are [n_kv_heads, max_seq, head_dim]. */
+int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
+                    uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
+                    float* kcache, float* vcache, uint32_t max_seq, float* out);
+/* LM head on a Q4_0 output.weight read as lmHead[K=dim][N=vocab] (blocks run
+ * along the vocab axis, gguf_loader.js:240-259), optional fused final RMSNorm. */
+int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,
+                         uint32_t K, uint32_t N);
+/* f32 GEMV, W [K][N] (w_is_nk = 0) or [N][K] (weight tying, 1). */
+int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,
+                   uint32_t K, uint32_t N, int w_is_nk);
+/* greedy step on device: token = argmax(logits) (generate.js:70-76),
+ * tokens[*count] = token, x = E[token], ++*count, ++*pos. */
+int smith_argmax_embed(void* ctx, const float* logits, uint32_t N, const float* E, uint32_t dim, float* x,
+                       int32_t* tokens, int32_t* count, int32_t* pos);
+int smith_set_i32(void* ctx, int32_t* p, int32_t v);
+/* seeded N(mean, std) f32 stream (SplitMix64 + Box-Muller), offset even. */
+int smith_randn(void* ctx, float* out, uint64_t n, uint64_t seed, uint64_t offset, float stdv, float mean);
+
+/* ---- HIP graphs: capture the context stream, replay it ----
+ * Ops enqueued between begin and end are recorded, not run; their scratch
+ * must already be allocated (run the same ops once before capturing). */
+int smith_graph_begin(void* ctx);
+void* smith_graph_end(void* ctx);
+int smith_graph_launch(void* ctx, void* graph);
+void smith_graph_destroy(void* graph);
+
 /* ---- timing on the context stream (HIP events) ---- */
 /* While enabled, every op-level kernel launch is bracketed by a HIP event
  * pair on the context stream.  smith_profile_read waits for the stream and

@@ -54,6 +54,9 @@ struct Ctx {
   size_t ws_bytes = 0;
   uint32_t* counters = nullptr;
   size_t counters_n = 0;
+  void* normbuf = nullptr;
+  size_t normbuf_bytes = 0;
+  bool capturing = false;
   // per-launch HIP event pairs of op-level kernels while profiling is on
   bool profile = false;
   struct Rec {
@@ -124,9 +127,29 @@ hipEvent_t pooled_event(Ctx* c) {
   return e;
 }
 
+// Op kernels may live in any loaded code object (smith_kernels.hsaco,
+// smith_llama.hsaco, ...): first match in load order wins.
+int find_kernel(Ctx* c, const char* name, hipFunction_t* out) {
+  if (c->libs.empty()) return fail(c, "smith: no code object loaded (call smith_load_library first)");
+  for (Library* lib : c->libs) {
+    auto it = lib->fns.find(name);
+    if (it != lib->fns.end()) {
+      *out = it->second;
+      return 0;
+    }
+    hipFunction_t f;
+    if (hipModuleGetFunction(&f, lib->mod, name) == hipSuccess) {
+      lib->fns[name] = f;
+      *out = f;
+      return 0;
+    }
+  }
+  return fail(c, "smith: kernel '%s' not found in any loaded code object", name);
+}
+
 int launch(Ctx* c, const char* name, dim3 grid, dim3 block, void** args, unsigned shmem = 0) {
   hipFunction_t f;
-  if (lookup(c, c->ops, name, &f)) return -1;
+  if (find_kernel(c, name, &f)) return -1;
   hipEvent_t ea = nullptr, eb = nullptr;
   if (c->profile) {
     ea = pooled_event(c);
@@ -146,6 +169,9 @@ int launch(Ctx* c, const char* name, dim3 grid, dim3 block, void** args, unsigne
 // stream so no enqueued kernel still uses the old allocation.
 int ensure(Ctx* c, void** p, size_t* have, size_t need) {
   if (need <= *have) return 0;
+  if (c->capturing)
+    return fail(c, "smith: scratch of %zu bytes needed while capturing a graph; run the op once before capture",
+                need);
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (*p) HIPCHK(c, hipFree(*p));
   *p = nullptr;
@@ -158,6 +184,7 @@ int ensure(Ctx* c, void** p, size_t* have, size_t need) {
 
 int ensure_counters(Ctx* c, size_t n) {
   if (n <= c->counters_n) return 0;
+  if (c->capturing) return fail(c, "smith: split-K counters needed while capturing a graph; run the op once first");
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (c->counters) HIPCHK(c, hipFree(c->counters));
   c->counters = nullptr;
@@ -174,8 +201,15 @@ enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2 };
 
 // M > 2: prepare the activations once (smith_qprep_*), then the 16-row
 // MFMA GEMV (smith_qgemv3_*).  Buckets must match DEF_QGEMV3_FMT.
+struct Epi {
+  const float* gamma = nullptr;  // RMSNorm of the activation rows first
+  float eps = 0.f;
+  const float* resid = nullptr;  // out = resid + y
+  uint32_t mode = 0;             // 0 store, 1 residual, 2 SwiGLU on (gate, up) column pairs
+};
+
 int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
-                 uint32_t N, uint32_t K, uint32_t G) {
+                 uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
   const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
   const char* ptag = fmt == FQ4S ? "q4" : (fmt == FQ8 ? "q8" : "q40");
   uint32_t bucket = M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
@@ -186,6 +220,18 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   if (ensure(c, &c->prep, &c->prep_bytes, frag_bytes + cst_bytes)) return -1;
   void* frag = c->prep;
   void* cst = (char*)c->prep + frag_bytes;
+  if (ep.gamma) {
+    // RMSNorm rows into a context buffer, then GEMV on the normalized rows
+    if (ensure(c, &c->normbuf, &c->normbuf_bytes, (size_t)M * K * sizeof(float))) return -1;
+    const float* pa = a;
+    const float* pg = ep.gamma;
+    void* py = c->normbuf;
+    uint32_t pr = M, pc = K;
+    float pe = ep.eps;
+    void* nargs[] = {&pa, &pg, &py, &pr, &pc, &pe};
+    if (launch(c, "smith_rmsnorm_rows", dim3(M), dim3(256), nargs)) return -1;
+    a = (const float*)c->normbuf;
+  }
   char name[64];
   snprintf(name, sizeof name, "smith_qprep_%s_%s", ptag, hilo ? "hilo" : "plain");
   uint64_t threads = (uint64_t)RB * (hilo ? 8 : 16) * G * 4;
@@ -209,7 +255,9 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   float* pws = c->ws;
   uint32_t* pcnt = c->counters;
   uint32_t pM = M, pN = N, pG = G;
-  void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG};
+  const float* pR = ep.resid;
+  uint32_t pepi = ep.mode;
+  void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG, &pR, &pepi};
   return launch(c, name, dim3(gx, ksplit), dim3(nthreads), args);
 }
 
@@ -217,7 +265,7 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
 // K split across the waves of a block; a cross-block split only when one
 // block's 64/128 groups do not cover K).
 int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
-                 uint32_t N, uint32_t K, uint32_t G) {
+                 uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
   const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
   bool small = G <= 64;
   uint32_t kb = small ? 64 : 128;
@@ -237,19 +285,28 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   float* pws = c->ws;
   uint32_t* pcnt = c->counters;
   uint32_t pM = M, pN = N, pK = K, pG = G;
-  void* args[] = {&pa, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pK, &pG};
+  const float* pg = ep.gamma;
+  float pe = ep.eps;
+  const float* pR = ep.resid;
+  uint32_t pepi = ep.mode;
+  void* args[] = {&pa, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pK, &pG, &pg, &pe, &pR, &pepi};
   return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
 }
 
 int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
-            uint32_t N, uint32_t K, uint32_t G) {
+            uint32_t N, uint32_t K, uint32_t G, const Epi& ep = Epi()) {
   if (set_device(c)) return -1;
   if (M == 0 || N == 0) return 0;
+  if (ep.mode == 2 && N % 2) return fail(c, "smith: SwiGLU epilogue needs an even column count (got %u)", N);
+  const uint32_t nout = ep.mode == 2 ? N / 2 : N;
   for (uint32_t m0 = 0; m0 < M; m0 += 32) {
     uint32_t mc = std::min<uint32_t>(32, M - m0);
     const float* am = a + (size_t)m0 * K;
-    float* om = out + (size_t)m0 * N;
-    int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G) : qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G);
+    float* om = out + (size_t)m0 * nout;
+    Epi e = ep;
+    if (e.resid) e.resid += (size_t)m0 * N;
+    int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
+                     : qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G, e);
     if (rc) return -1;
   }
   return 0;
@@ -306,6 +363,7 @@ void smith_destroy(void* ctx) {
     }
   }
   if (c->prep) hipFree(c->prep);
+  if (c->normbuf) hipFree(c->normbuf);
   if (c->ws) hipFree(c->ws);
   if (c->counters) hipFree(c->counters);
   for (auto& r : c->recs) {
@@ -750,9 +808,9 @@ int smith_repack_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_
   uint32_t G = K / 32;
   uint64_t total = (uint64_t)N * G;
   if (!total) return 0;
-  uint32_t pN = N, pG = G;
-  void* args[] = {&blocks, &nib, &d, &pN, &pG};
-  return launch(c, "smith_repack_q4_0", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+  uint32_t pN = N, pG = G, po = 0, ps = 1, pt = N;
+  void* args[] = {&blocks, &nib, &d, &pN, &pG, &po, &ps, &pt};
+  return launch(c, "smith_repack_q4_0_cols", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
                 dim3(256), args);
 }
 
@@ -780,6 +838,208 @@ int smith_matmul_q4_0(void* ctx, const float* a, const void* nib, const void* d,
   if (!c) return -1;
   if (K % 32) return fail(c, "smith_matmul_q4_0: K %u is not a multiple of 32", K);
   return qmatmul(c, FQ40, a, nib, d, out, M, N, K, K / 32);
+}
+
+
+// ---------------- GGUF decode path ----------------
+int smith_repack_q4_0_into(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K, uint32_t n_off,
+                           uint32_t n_stride, uint32_t N_total) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_repack_q4_0_into: K %u is not a multiple of 32", K);
+  if ((uint64_t)n_off + (uint64_t)(N ? N - 1 : 0) * n_stride >= N_total && N)
+    return fail(c, "smith_repack_q4_0_into: columns exceed N_total=%u", N_total);
+  if (set_device(c)) return -1;
+  uint32_t G = K / 32;
+  uint64_t total = (uint64_t)N * G;
+  if (!total) return 0;
+  uint32_t pN = N, pG = G, po = n_off, ps = n_stride, pt = N_total;
+  void* args[] = {&blocks, &nib, &d, &pN, &pG, &po, &ps, &pt};
+  return launch(c, "smith_repack_q4_0_cols", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_repack_q8_0_into(void* ctx, const void* blocks, void* dst, uint32_t N, uint32_t K, uint32_t n_off,
+                           uint32_t n_stride, uint32_t N_total) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_repack_q8_0_into: K %u is not a multiple of 32", K);
+  if ((uint64_t)n_off + (uint64_t)(N ? N - 1 : 0) * n_stride >= N_total && N)
+    return fail(c, "smith_repack_q8_0_into: columns exceed N_total=%u", N_total);
+  if (set_device(c)) return -1;
+  uint32_t G = K / 32;
+  uint64_t total = (uint64_t)N * G;
+  if (!total) return 0;
+  uint32_t pN = N, pG = G, po = n_off, ps = n_stride, pt = N_total;
+  void* args[] = {&blocks, &dst, &pN, &pG, &po, &ps, &pt};
+  return launch(c, "smith_repack_q8_0_cols", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_linear_q4_0(void* ctx, const float* x, const void* nib, const void* d, float* out, uint32_t M, uint32_t N,
+                      uint32_t K, const float* norm_gamma, float eps, const float* resid, uint32_t epilogue) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_linear_q4_0: K %u is not a multiple of 32", K);
+  if (epilogue > 2) return fail(c, "smith_linear_q4_0: unknown epilogue %u", epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q4_0: residual epilogue without a residual buffer");
+  Epi e;
+  e.gamma = norm_gamma;
+  e.eps = eps;
+  e.resid = epilogue == 1 ? resid : nullptr;
+  e.mode = epilogue;
+  return qmatmul(c, FQ40, x, nib, d, out, M, N, K, K / 32, e);
+}
+
+int smith_linear_q8(void* ctx, const float* x, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
+                    const float* norm_gamma, float eps, const float* resid, uint32_t epilogue) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (epilogue > 2) return fail(c, "smith_linear_q8: unknown epilogue %u", epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q8: residual epilogue without a residual buffer");
+  Epi e;
+  e.gamma = norm_gamma;
+  e.eps = eps;
+  e.resid = epilogue == 1 ? resid : nullptr;
+  e.mode = epilogue;
+  return qmatmul(c, FQ8, x, wq, nullptr, out, M, N, K, (K + 31) / 32, e);
+}
+
+int smith_rmsnorm(void* ctx, const float* x, const float* gamma, float* out, uint32_t rows, uint32_t cols, float eps) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (!rows || !cols) return 0;
+  void* args[] = {&x, &gamma, &out, &rows, &cols, &eps};
+  return launch(c, "smith_rmsnorm_rows", dim3(rows), dim3(256), args);
+}
+
+int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, uint32_t rows, uint32_t dim) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (!rows) return 0;
+  void* args[] = {&E, &tokens, &out, &rows, &dim};
+  return launch(c, "smith_embed_rows", dim3(rows), dim3(256), args);
+}
+
+int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
+                    uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
+                    float* kcache, float* vcache, uint32_t max_seq, float* out) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!n_kv_heads || n_heads % n_kv_heads) return fail(c, "smith_attention: %u heads not a multiple of %u kv heads", n_heads, n_kv_heads);
+  if (head_dim > 128 || 256 % head_dim) return fail(c, "smith_attention: head_dim %u unsupported (64 or 128)", head_dim);
+  if (S > 256) return fail(c, "smith_attention: %u rows per launch exceeds 256", S);
+  if (set_device(c)) return -1;
+  if (!S) return 0;
+  size_t smem = (128 + (size_t)S * 128 + std::max<size_t>(256, max_seq)) * sizeof(float);
+  if (smem > 160 * 1024) return fail(c, "smith_attention: %zu bytes of LDS needed (max_seq %u, S %u)", smem, max_seq, S);
+  void* args[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
+                  &kcache, &vcache, &max_seq, &out};
+  return launch(c, "smith_attention", dim3(n_heads, S), dim3(256), args, (unsigned)smem);
+}
+
+int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,
+                         uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (N % 32) return fail(c, "smith_lmhead_q4_0_nb: vocab %u is not a multiple of 32", N);
+  if (K > 8192) return fail(c, "smith_lmhead_q4_0_nb: dim %u exceeds 8192", K);
+  if (set_device(c)) return -1;
+  uint32_t gx = (N / 32 + 15) / 16;
+  uint32_t ksplit = std::max<uint32_t>(1, std::min<uint32_t>((256 + gx - 1) / gx, (K + 63) / 64));
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  void* args[] = {&x, &norm_gamma, &eps, &W, &y, &K, &N, &pws, &pcnt};
+  return launch(c, "smith_lmhead_q4_0_nb", dim3(gx, ksplit), dim3(512), args);
+}
+
+int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,
+                   uint32_t K, uint32_t N, int w_is_nk) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K > 8192) return fail(c, "smith_gemv_f32: K %u exceeds 8192", K);
+  if (set_device(c)) return -1;
+  void* args[] = {&x, &norm_gamma, &eps, &W, &y, &K, &N};
+  if (w_is_nk) return launch(c, "smith_gemv_f32_nk", dim3(std::min<uint32_t>((N + 3) / 4, 2048)), dim3(256), args);
+  return launch(c, "smith_gemv_f32_kn", dim3((N + 63) / 64), dim3(1024), args);
+}
+
+int smith_argmax_embed(void* ctx, const float* logits, uint32_t N, const float* E, uint32_t dim, float* x,
+                       int32_t* tokens, int32_t* count, int32_t* pos) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  void* args[] = {&logits, &N, &E, &dim, &x, &tokens, &count, &pos};
+  return launch(c, "smith_argmax_embed", dim3(1), dim3(1024), args);
+}
+
+int smith_set_i32(void* ctx, int32_t* p, int32_t v) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  void* args[] = {&p, &v};
+  return launch(c, "smith_set_i32", dim3(1), dim3(64), args);
+}
+
+int smith_randn(void* ctx, float* out, uint64_t n, uint64_t seed, uint64_t offset, float stdv, float mean) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (offset % 2) return fail(c, "smith_randn: offset must be even (Box-Muller pairs)");
+  if (set_device(c)) return -1;
+  if (!n) return 0;
+  void* args[] = {&out, &n, &seed, &offset, &stdv, &mean};
+  uint64_t pairs = (n + 1) / 2;
+  return launch(c, "smith_randn_f32", dim3((unsigned)std::min<uint64_t>((pairs + 255) / 256, 65536)), dim3(256),
+                args);
+}
+
+// ---------------- HIP graphs ----------------
+int smith_graph_begin(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (set_device(c)) return -1;
+  if (c->profile) return fail(c, "smith_graph_begin: kernel profiling must be off while capturing");
+  HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  c->capturing = true;
+  return 0;
+}
+
+void* smith_graph_end(void* ctx) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return nullptr;
+  c->capturing = false;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (e != hipSuccess || !g) {
+    fail(c, "smith_graph_end: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  hipGraphExec_t ge = nullptr;
+  e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    fail(c, "smith_graph_end: instantiate: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  return (void*)ge;
+}
+
+int smith_graph_launch(void* ctx, void* graph) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c || !graph) return -1;
+  if (set_device(c)) return -1;
+  HIPCHK(c, hipGraphLaunch((hipGraphExec_t)graph, c->stream));
+  return 0;
+}
+
+void smith_graph_destroy(void* graph) {
+  if (graph) hipGraphExecDestroy((hipGraphExec_t)graph);
 }
 
 // ---------------- timing ----------------

@@ -227,19 +227,39 @@ extern "C" __global__ void smith_quantize_q4_0_rows(const float* __restrict__ x,
 
 // Split GGUF Q4_0 blocks of a weight listed [out=N][in=K] (block (n,g) at
 // (n*G+g)*18) into the planar, column-interleaved layout the GEMV reads:
-// nib[(g*N+n)*16 + 0..15] and d[g*N+n].  Bytes are moved, never changed.
-extern "C" __global__ void smith_repack_q4_0(const uint8_t* __restrict__ src, uint8_t* __restrict__ nib,
-                                             uint16_t* __restrict__ dsc, uint32_t N, uint32_t G) {
+// nib[(g*Nt+col)*16 + 0..15] and d[g*Nt+col] with col = n_off + n*n_stride,
+// so several weights can share one buffer (q|k|v side by side, gate/up
+// interleaved).  Bytes are moved, never changed.
+extern "C" __global__ void smith_repack_q4_0_cols(const uint8_t* __restrict__ src, uint8_t* __restrict__ nib,
+                                                  uint16_t* __restrict__ dsc, uint32_t N, uint32_t G,
+                                                  uint32_t n_off, uint32_t n_stride, uint32_t Nt) {
   size_t total = (size_t)N * G;
   for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (size_t)gridDim.x * blockDim.x) {
     uint32_t n = (uint32_t)(idx / G), g = (uint32_t)(idx % G);
     const uint16_t* s = (const uint16_t*)(src + idx * 18);
-    size_t o = (size_t)g * N + n;
+    size_t o = (size_t)g * Nt + n_off + (size_t)n * n_stride;
     dsc[o] = s[0];
     uint16_t* dn = (uint16_t*)(nib + o * 16);
 #pragma unroll
     for (int i = 0; i < 8; i++) dn[i] = s[1 + i];
+  }
+}
+
+// GGUF Q8_0 blocks of a weight listed [out=N][in=K] into matmulQ8's record
+// order (shaders/matmul_q8.metal:40-52): record (g, col) at (g*Nt+col)*34,
+// col = n_off + n*n_stride.  34-byte blocks, moved unchanged.
+extern "C" __global__ void smith_repack_q8_0_cols(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                  uint32_t N, uint32_t G, uint32_t n_off, uint32_t n_stride,
+                                                  uint32_t Nt) {
+  size_t total = (size_t)N * G;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    uint32_t n = (uint32_t)(idx / G), g = (uint32_t)(idx % G);
+    const uint16_t* s = (const uint16_t*)(src + idx * 34);
+    uint16_t* d = (uint16_t*)(dst + ((size_t)g * Nt + n_off + (size_t)n * n_stride) * 34);
+#pragma unroll
+    for (int i = 0; i < 17; i++) d[i] = s[i];
   }
 }
 
@@ -340,6 +360,61 @@ DEF_QPREP(smith_qprep_q8_hilo, FMT_Q8, true)
 DEF_QPREP(smith_qprep_q8_plain, FMT_Q8, false)
 
 // ---------------------------------------------------------------------------
+// Epilogues shared by the GEMVs (the GGUF decode path fuses its elementwise
+// ops into the projection that produces their input):
+//   EPI_STORE   C[m][n] = v
+//   EPI_RESID   C[m][n] = R[m][n] + v            (residual add, gguf_cache.js:159,171)
+//   EPI_SWIGLU  columns hold interleaved (gate, up) pairs: C[m][n/2] =
+//               silu(v[2j]) * v[2j+1] with silu(g) = g / (1 + exp(-g))
+//               (shaders/swiglu.metal:12-21); C has N/2 columns.
+// ---------------------------------------------------------------------------
+#define EPI_STORE 0u
+#define EPI_RESID 1u
+#define EPI_SWIGLU 2u
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
+// Cross-workgroup split-K: this workgroup's partials are already in ws
+// (agent-scope atomic exchanges); the last-arriving workgroup of the column
+// block sums the ksplit partials in fixed order and applies the epilogue.
+__device__ __forceinline__ void splitk_finish(float* __restrict__ ws, uint32_t* __restrict__ counters,
+                                              float* __restrict__ C, const float* __restrict__ R, uint32_t epi,
+                                              uint32_t M, uint32_t N, uint32_t mrows, uint32_t nb, uint32_t BC,
+                                              uint32_t NT, uint32_t ksplit, int* s_last) {
+  __builtin_amdgcn_s_waitcnt(0);  // every exchange of this thread has been performed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = prev == ksplit - 1;
+  }
+  __syncthreads();
+  if (!*s_last) return;
+  auto part = [&](uint32_t m, uint32_t n) {
+    float v = 0.f;
+    for (uint32_t sp = 0; sp < ksplit; sp++)
+      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return v;
+  };
+  if (epi == EPI_SWIGLU) {
+    for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
+      uint32_t m = e / (BC / 2), n = nb + 2 * (e % (BC / 2));
+      if (n >= N) continue;
+      C[(size_t)m * (N / 2) + n / 2] = silu_mul(part(m, n), part(m, n + 1));
+    }
+  } else {
+    for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+      uint32_t m = e / BC, n = nb + e % BC;
+      if (n >= N) continue;
+      float v = part(m, n);
+      C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+    }
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // Decode GEMV for M <= 2 with the activation prep fused (no prep launch).
 //
 // Lane (c = lane%16, j = lane/16) loads the WHOLE weight record of column
@@ -426,7 +501,9 @@ template <int FMT, int MR, int CT, int WK, int WN, int S>
 __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
                                             const uint16_t* __restrict__ D, float* __restrict__ C,
                                             float* __restrict__ ws, uint32_t* __restrict__ counters,
-                                            uint32_t M, uint32_t N, uint32_t K, uint32_t G) {
+                                            uint32_t M, uint32_t N, uint32_t K, uint32_t G,
+                                            const float* __restrict__ gamma, float eps,
+                                            const float* __restrict__ R, uint32_t epi) {
   constexpr int GPW = 4 * S;           // groups per wave (S steps of 4)
   constexpr int KB = GPW * WK;         // groups per block
   constexpr int BC = 16 * CT * WN;     // block columns
@@ -436,6 +513,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   __shared__ u32x4 fragL[KB][2 * MR][4];  // [group][row u][mfma i]
   __shared__ float2 cL[KB][MR];           // (C1, S) with hi + lo/2048 folded
   __shared__ float red[WK][MR][BC];
+  __shared__ float nred[MR][WK * WN];
   __shared__ int s_last;
 
   const uint32_t lane = threadIdx.x & 63;
@@ -446,6 +524,18 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   const uint32_t gb = blockIdx.y * KB;
   const uint32_t gw = gb + wk * GPW;
   const uint32_t ksplit = gridDim.y;
+
+  // 0. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
+  //    that consumes it): every workgroup sums x^2 over its rows' full K
+  float nss[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) nss[m] = 0.f;
+  if (gamma) {
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+      if ((uint32_t)m < M)
+        for (uint32_t i = threadIdx.x; i < K; i += NT) nss[m] = __builtin_fmaf(A[(size_t)m * K + i], A[(size_t)m * K + i], nss[m]);
+  }
 
   // 1. activation loads first (small, cache resident): the in-order load
   //    counter then lets the conversion below run while weights are in flight
@@ -481,6 +571,35 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
 
   // 3. activations -> f16 hi/lo fragments + (C1, S) in LDS
+  float rms[MR];
+  if (gamma) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float v = nss[m];
+      for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+      if (lane == 0) nred[m][wave] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float tot = 0.f;
+      for (int w = 0; w < WK * WN; w++) tot += nred[m][w];
+      rms[m] = 1.0f / __builtin_sqrtf(tot / (float)K + eps);
+    }
+#pragma unroll
+    for (int cc = 0; cc < CPT; cc++) {
+      uint32_t ch = threadIdx.x + cc * NT;
+      uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
+      uint32_t k0 = (gb + gl) * 32 + 8 * i;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float r = 0.f;
+#pragma unroll
+        for (int q = 0; q < MR; q++) r = (uint32_t)q == m ? rms[q] : r;
+        av[cc][e] = (k0 + e < K) ? av[cc][e] * r * gamma[k0 + e] : 0.f;
+      }
+    }
+  }
 #pragma unroll
   for (int cc = 0; cc < CPT; cc++) {
     uint32_t ch = threadIdx.x + cc * NT;
@@ -576,46 +695,48 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   __syncthreads();
   const uint32_t nb = blockIdx.x * BC;
   const uint32_t mrows = M < (uint32_t)MR ? M : MR;
+  if (ksplit == 1) {
+    if (epi == EPI_SWIGLU) {
+      for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
+        uint32_t m = e / (BC / 2), cc = 2 * (e % (BC / 2)), n = nb + cc;
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int w = 0; w < WK; w++) {
+          g += red[w][m][cc];
+          u += red[w][m][cc + 1];
+        }
+        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(g, u);
+      }
+    } else {
+      for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+        uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < WK; w++) v += red[w][m][cc];
+        if (n >= N) continue;
+        C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+      }
+    }
+    return;
+  }
   for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
     uint32_t m = e / BC, cc = e % BC, n = nb + cc;
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < WK; w++) v += red[w][m][cc];
     if (n >= N) continue;
-    if (ksplit == 1)
-      C[(size_t)m * N + n] = v;
-    else
-      __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
-                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
+                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (ksplit == 1) return;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == ksplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
-    uint32_t m = e / BC, n = nb + e % BC;
-    if (n >= N) continue;
-    float v = 0.f;
-    for (uint32_t sp = 0; sp < ksplit; sp++)
-      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    C[(size_t)m * N + n] = v;
-  }
-  if (threadIdx.x == 0)
-    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
 }
 
 #define DEF_QGEMV1(NAME, FMT, MR, CT, WK, WN, S)                                                        \
-  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(const float* A, const uint8_t* B,     \
-                                                                  const uint16_t* D, float* C, float* ws, \
-                                                                  uint32_t* counters, uint32_t M,       \
-                                                                  uint32_t N, uint32_t K, uint32_t G) { \
-    qgemv1_body<FMT, MR, CT, WK, WN, S>(A, B, D, C, ws, counters, M, N, K, G);                           \
+  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                       \
+      const float* A, const uint8_t* B, const uint16_t* D, float* C, float* ws, uint32_t* counters,      \
+      uint32_t M, uint32_t N, uint32_t K, uint32_t G, const float* gamma, float eps, const float* R,     \
+      uint32_t epi) {                                                                                    \
+    qgemv1_body<FMT, MR, CT, WK, WN, S>(A, B, D, C, ws, counters, M, N, K, G, gamma, eps, R, epi);      \
   }
 
 // ---------------------------------------------------------------------------
@@ -650,7 +771,7 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
                                             const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
                                             float* __restrict__ C, float* __restrict__ ws,
                                             uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
-                                            uint32_t G) {
+                                            uint32_t G, const float* __restrict__ R, uint32_t epi) {
   constexpr int GPW = 4 * S;
   constexpr int BC = 16 * CT * WN;
   constexpr int NT = 64 * WK * WN;
@@ -762,8 +883,7 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   const uint32_t rows_per_rb = HILO ? 8 : 16;
   const uint32_t mrows = M < (uint32_t)(RB * rows_per_rb) ? M : RB * rows_per_rb;
   const uint32_t nb = blockIdx.x * BC;
-  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
-    uint32_t m = e / BC, cc = e % BC;
+  auto colsum = [&](uint32_t m, uint32_t cc) {
     uint32_t rb = m / rows_per_rb, rr = m % rows_per_rb;
     float v = 0.f;
 #pragma unroll
@@ -771,41 +891,38 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
       if (HILO) v += red[w][rb][rr][cc] + red[w][rb][rr + 8][cc] * (1.0f / 2048.0f);
       else v += red[w][rb][rr][cc];
     }
-    uint32_t n = nb + cc;
-    if (n >= N) continue;
-    if (ksplit == 1)
-      C[(size_t)m * N + n] = v;
-    else
-      __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
-                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+  };
+  if (ksplit == 1) {
+    if (epi == EPI_SWIGLU) {
+      for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
+        uint32_t m = e / (BC / 2), cc = 2 * (e % (BC / 2)), n = nb + cc;
+        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(colsum(m, cc), colsum(m, cc + 1));
+      }
+    } else {
+      for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+        uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+        if (n >= N) continue;
+        float v = colsum(m, cc);
+        C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+      }
+    }
+    return;
   }
-  if (ksplit == 1) return;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == ksplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
   for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
-    uint32_t m = e / BC, n = nb + e % BC;
+    uint32_t m = e / BC, cc = e % BC, n = nb + cc;
     if (n >= N) continue;
-    float v = 0.f;
-    for (uint32_t sp = 0; sp < ksplit; sp++)
-      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    C[(size_t)m * N + n] = v;
+    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(colsum(m, cc)),
+                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
 }
 
 #define DEF_QGEMV3(NAME, FMT, RB, HILO, VPL, CT, S, WK, WN)                                             \
   extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                       \
       const u32x4* frag, const float2* cst, const uint8_t* B, const uint16_t* D, float* C, float* ws,    \
-      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G) {                                          \
-    qgemv3_body<FMT, RB, HILO, VPL, CT, S, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G);           \
+      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G, const float* R, uint32_t epi) {            \
+    qgemv3_body<FMT, RB, HILO, VPL, CT, S, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G, R, epi);   \
   }
 
 // Fused M <= 2 variants: "k128" = 8 waves x 4 steps (128 groups per block),

@@ -13,6 +13,7 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsmith.so")
 CODE_OBJECT_PATH = os.path.join(_HERE, "lib", "smith_kernels.hsaco")
+LLAMA_CODE_OBJECT_PATH = os.path.join(_HERE, "lib", "smith_llama.hsaco")
 
 SHARED = 0
 PRIVATE = 1
@@ -74,6 +75,22 @@ SYMBOLS = {
     "smith_repack_q4_0": (_INT, [_P, _P, _P, _P, _U32, _U32]),
     "smith_matmul_q4_0": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32]),
     "smith_quantize_q4_0": (_INT, [_P, _P, _P, _U32, _U32]),
+    "smith_repack_q4_0_into": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32]),
+    "smith_repack_q8_0_into": (_INT, [_P, _P, _P, _U32, _U32, _U32, _U32, _U32]),
+    "smith_linear_q4_0": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
+    "smith_linear_q8": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
+    "smith_rmsnorm": (_INT, [_P, _P, _P, _P, _U32, _U32, ctypes.c_float]),
+    "smith_embed": (_INT, [_P, _P, _P, _P, _U32, _U32]),
+    "smith_attention": (_INT, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _U32, _P]),
+    "smith_lmhead_q4_0_nb": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _U32, _U32]),
+    "smith_gemv_f32": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _U32, _U32, _INT]),
+    "smith_argmax_embed": (_INT, [_P, _P, _U32, _P, _U32, _P, _P, _P, _P]),
+    "smith_set_i32": (_INT, [_P, _P, ctypes.c_int32]),
+    "smith_randn": (_INT, [_P, _P, _U64, _U64, _U64, ctypes.c_float, ctypes.c_float]),
+    "smith_graph_begin": (_INT, [_P]),
+    "smith_graph_end": (_P, [_P]),
+    "smith_graph_launch": (_INT, [_P, _P]),
+    "smith_graph_destroy": (None, [_P]),
     "smith_profile_kernels": (_INT, [_P, _INT]),
     "smith_profile_read": (_INT, [_P, _STR, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_U64)]),
     "smith_timer_start": (_INT, [_P]),
@@ -140,6 +157,9 @@ def shader_lib():
             raise RuntimeError("smith: failed to load code object at %s: %s"
                                % (CODE_OBJECT_PATH, lib.smith_last_error(c).decode()))
         _library = lp
+        if not lib.smith_load_library(c, LLAMA_CODE_OBJECT_PATH.encode()):
+            raise RuntimeError("smith: failed to load code object at %s: %s"
+                               % (LLAMA_CODE_OBJECT_PATH, lib.smith_last_error(c).decode()))
     return _library
 
 

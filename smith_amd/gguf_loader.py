@@ -1,0 +1,250 @@
+"""loadGGUF on MI355X -- mirror of src/gguf_loader.js for the Llama path.
+
+Differences from the reference, all on purpose (SURVEY.md finding 3): the
+reference dequantizes every tensor to f32 at load (gguf_loader.js:236) and
+runs f32 GEMMs; here Q4_0 / Q8_0 linear weights stay quantized on the device
+and `linear` runs the quantized GEMV.  The blocks are only moved (never
+changed) into the kernels' layouts:
+  * q|k|v of a layer side by side in one buffer (one GEMV per layer),
+  * gate/up interleaved column by column (the SwiGLU epilogue pairs them),
+  * output.weight kept as stored: the reference reads its flat data as
+    lmHead[dim][vocab] (gguf_loader.js:240-259 only transposes paths ending
+    in ".weight"), so its Q4_0 blocks run along the vocab axis and it gets
+    its own GEMV (smith_lmhead_q4_0_nb).
+Norms and the token embedding are f32 on the device.
+"""
+import numpy as np
+
+from . import device
+from . import gguf as G
+from .gguf_cache import (createGGUFCache, forwardLlamaCachedDecode, forwardLlamaCachedPrefill, generateGGUF,
+                         resetCache)
+
+LLAMA_MAP = {
+    "token_embd.weight": "embedding.tokenWeight",
+    "output_norm.weight": "lnFGamma",
+    "output.weight": "lmHead",
+    "blk.{L}.attn_norm.weight": "blocks.{L}.ln1Gamma",
+    "blk.{L}.ffn_norm.weight": "blocks.{L}.ln2Gamma",
+    "blk.{L}.attn_q.weight": "blocks.{L}.mha.qProj.weight",
+    "blk.{L}.attn_k.weight": "blocks.{L}.mha.kProj.weight",
+    "blk.{L}.attn_v.weight": "blocks.{L}.mha.vProj.weight",
+    "blk.{L}.attn_output.weight": "blocks.{L}.mha.outProj.weight",
+    "blk.{L}.ffn_gate.weight": "blocks.{L}.ffnGate.weight",
+    "blk.{L}.ffn_up.weight": "blocks.{L}.ffnUp.weight",
+    "blk.{L}.ffn_down.weight": "blocks.{L}.ffnDown.weight",
+}
+
+
+def getWeightMap(arch):
+    """gguf_loader.js:86-91 (only the Llama map drives generate, finding 8)."""
+    if arch == "llama":
+        return LLAMA_MAP
+    raise ValueError("Unsupported GGUF architecture: %s" % arch)
+
+
+def resolveWeight(name, weightMap):
+    """gguf_loader.js:94-109."""
+    if name in weightMap:
+        return weightMap[name]
+    parts = name.split(".", 2)
+    if len(parts) == 3 and parts[0] == "blk" and parts[1].isdigit():
+        pat = "blk.{L}." + parts[2]
+        if pat in weightMap:
+            return weightMap[pat].replace("{L}", parts[1])
+    return None
+
+
+def precomputeRoPE(dim, maxSeqLen, freqBase=10000):
+    """ops/rope.js:10-30: f32 inverse frequencies, f64 angles, f32 cos/sin,
+    flat [maxSeqLen, dim/2]."""
+    half = dim // 2
+    freqs = (1.0 / np.power(float(freqBase), (2.0 * np.arange(half)) / dim)).astype(np.float32)
+    ang = np.arange(maxSeqLen, dtype=np.float64)[:, None] * freqs.astype(np.float64)[None, :]
+    return np.cos(ang).astype(np.float32).ravel(), np.sin(ang).astype(np.float32).ravel()
+
+
+class DeviceArray:
+    """A device buffer with a shape (f32 unless stated)."""
+
+    def __init__(self, shape, dtype=np.float32, nbytes=None):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(nbytes if nbytes is not None else np.prod(self.shape) * self.dtype.itemsize)
+        self.ptr = device.alloc(max(self.nbytes, 4))
+
+    @classmethod
+    def from_host(cls, arr, dtype=np.float32):
+        a = np.ascontiguousarray(arr, dtype=dtype)
+        d = cls(a.shape, dtype)
+        device.upload(d.ptr, a)
+        return d
+
+    def numpy(self):
+        return device.download(self.ptr, self.nbytes, self.dtype).reshape(self.shape)
+
+
+class QLinear:
+    """A quantized linear weight on the device: y = x . W with W [in=K, out=N].
+    kind 'q4_0': planes nib/d; kind 'q8': matmulQ8 records."""
+
+    def __init__(self, kind, K, N, a, b=None):
+        self.kind, self.K, self.N, self.a, self.b = kind, K, N, a, b
+
+    def __call__(self, x_ptr, out_ptr, M, gamma=None, eps=0.0, resid=None, epilogue=0):
+        ctx = device.ops_ctx()
+        if self.kind == "q4_0":
+            rc = device.lib.smith_linear_q4_0(ctx, x_ptr, self.a.ptr, self.b.ptr, out_ptr, M, self.N, self.K,
+                                              gamma, eps, resid, epilogue)
+        else:
+            rc = device.lib.smith_linear_q8(ctx, x_ptr, self.a.ptr, out_ptr, M, self.N, self.K, gamma, eps,
+                                            resid, epilogue)
+        device.check(rc, "linear")
+
+
+def _pack_group(parsed, infos, K, cols, interleave):
+    """Repack one or more [out, in] Q4_0 / Q8_0 weights into one device
+    buffer: side by side (interleave=False) or column-interleaved."""
+    types = {i["type"] for i in infos}
+    if len(types) != 1:
+        raise ValueError("fused weights must share one GGML type, got %s" % sorted(types))
+    t = types.pop()
+    Ntot = sum(cols)
+    Gk = K // 32
+    ctx = device.ops_ctx()
+    if t == G.GGML_TYPE["Q4_0"]:
+        nib = DeviceArray((Gk * Ntot * 16,), np.uint8)
+        dsc = DeviceArray((Gk * Ntot,), np.uint16)
+        kind = "q4_0"
+    elif t == G.GGML_TYPE["Q8_0"]:
+        nib = DeviceArray((Gk * Ntot * 34,), np.uint8)
+        dsc = None
+        kind = "q8"
+    else:
+        raise NotImplementedError("linear weight type %s is not on the quantized path (Q4_0, Q8_0 only)"
+                                  % G.GGML_TYPE_NAME.get(t, t))
+    off = 0
+    for j, (info, n) in enumerate(zip(infos, cols)):
+        raw = G.readTensorData(parsed, info)
+        src = DeviceArray.from_host(np.asarray(raw), np.uint8)
+        n_off, stride = (j, len(infos)) if interleave else (off, 1)
+        if kind == "q4_0":
+            rc = device.lib.smith_repack_q4_0_into(ctx, src.ptr, nib.ptr, dsc.ptr, n, K, n_off, stride, Ntot)
+        else:
+            rc = device.lib.smith_repack_q8_0_into(ctx, src.ptr, nib.ptr, n, K, n_off, stride, Ntot)
+        device.check(rc, "repack %s" % info["name"])
+        device.sync()
+        device.release_buffer(src.ptr)
+        off += n
+    return QLinear(kind, K, Ntot, nib, dsc)
+
+
+def createGGUFModel(config):
+    """gguf_loader.js:151-212: derived sizes and the RoPE tables."""
+    dim, nH = config["dim"], config["numHeads"]
+    headDim = dim // nH
+    kvHeads = config["numKVHeads"] or nH
+    ffn = config["ffnDim"] or int(round(dim * 8 / 3 / 256) * 256)
+    cfg = dict(config, headDim=headDim, kvDim=kvHeads * headDim, ffnDim=ffn, numKVHeads=kvHeads)
+    cos, sin = precomputeRoPE(headDim, config["maxSeqLen"], config["ropeFreqBase"])
+    return {"config": cfg, "arch": config["arch"], "normEps": float(config["normEps"]),
+            "rope": {"cos": DeviceArray.from_host(cos), "sin": DeviceArray.from_host(sin)},
+            "blocks": [{} for _ in range(config["numLayers"])]}
+
+
+def loadWeights(parsed, model):
+    """gguf_loader.js:216-273 with the quantized blocks kept (see module doc)."""
+    cfg = model["config"]
+    wmap = getWeightMap(model["arch"])
+    dim, kvDim, ffn, vocab = cfg["dim"], cfg["kvDim"], cfg["ffnDim"], cfg["vocabSize"]
+    by_path, loaded, skipped = {}, [], []
+    for info in parsed["tensors"]:
+        path = resolveWeight(info["name"], wmap)
+        if path is None:
+            skipped.append(info["name"])
+            continue
+        by_path[path] = info
+        loaded.append(info["name"])
+
+    def expect_linear(info, n_in, n_out):
+        shp = info["shape"]
+        if len(shp) != 2 or int(np.prod(shp)) != n_in * n_out:
+            raise ValueError("%s: shape %s, expected %d x %d" % (info["name"], shp, n_out, n_in))
+        rows, cols = shp
+        if not (cols == n_in and rows == n_out):
+            # listed [in, out]: the reference copies the flat data untransposed
+            # (gguf_loader.js:254-256), i.e. blocks along out -- not supported
+            raise NotImplementedError("%s is listed [in, out]; only [out, in] listings are on the quantized path"
+                                      % info["name"])
+
+    def dense(path, n):
+        info = by_path.get(path)
+        if info is None:
+            return DeviceArray.from_host(np.ones(n, np.float32))  # createGGUFModel default (T.ones)
+        return DeviceArray.from_host(G.dense_f32(parsed, info).reshape(n))
+
+    E = by_path.get("embedding.tokenWeight")
+    if E is None:
+        raise ValueError("token_embd.weight missing")
+    model["embedding"] = DeviceArray.from_host(G.dense_f32(parsed, E).reshape(vocab, dim))
+    for L, blk in enumerate(model["blocks"]):
+        p = "blocks.%d." % L
+        q, k, v = (by_path[p + "mha.%sProj.weight" % n] for n in ("q", "k", "v"))
+        o = by_path[p + "mha.outProj.weight"]
+        g, u, d = (by_path[p + n + ".weight"] for n in ("ffnGate", "ffnUp", "ffnDown"))
+        for info, n_in, n_out in ((q, dim, dim), (k, dim, kvDim), (v, dim, kvDim), (o, dim, dim), (g, dim, ffn),
+                                  (u, dim, ffn), (d, ffn, dim)):
+            expect_linear(info, n_in, n_out)
+        blk["ln1Gamma"] = dense(p + "ln1Gamma", dim)
+        blk["ln2Gamma"] = dense(p + "ln2Gamma", dim)
+        blk["qkv"] = _pack_group(parsed, [q, k, v], dim, [dim, kvDim, kvDim], interleave=False)
+        blk["outProj"] = _pack_group(parsed, [o], dim, [dim], interleave=False)
+        blk["gateUp"] = _pack_group(parsed, [g, u], dim, [ffn, ffn], interleave=True)
+        blk["ffnDown"] = _pack_group(parsed, [d], ffn, [dim], interleave=False)
+    model["lnFGamma"] = dense("lnFGamma", dim)
+    head = by_path.get("lmHead")
+    if head is None:
+        # weight tying (gguf_loader.js:266-270): logits = x . E^T
+        model["lmHead"] = {"kind": "tied"}
+        model["weightTied"] = True
+    elif head["type"] == G.GGML_TYPE["Q4_0"]:
+        if vocab % 32:
+            raise NotImplementedError("Q4_0 output.weight needs vocab % 32 == 0")
+        model["lmHead"] = {"kind": "q4_0_nb", "w": DeviceArray.from_host(np.asarray(G.readTensorData(parsed, head)),
+                                                                          np.uint8)}
+    elif head["type"] in (G.GGML_TYPE["F32"], G.GGML_TYPE["F16"]):
+        model["lmHead"] = {"kind": "f32_kn", "w": DeviceArray.from_host(G.dense_f32(parsed, head))}
+    else:
+        raise NotImplementedError("output.weight type %s" % G.GGML_TYPE_NAME.get(head["type"], head["type"]))
+    device.sync()
+    return {"loaded": loaded, "skipped": skipped}
+
+
+class GGUFModel(dict):
+    """The object loadGGUF returns (gguf_loader.js:388-404)."""
+
+    def __getattr__(self, k):
+        try:
+            return self[k]
+        except KeyError:
+            raise AttributeError(k)
+
+
+def loadGGUF(path):
+    """gguf_loader.js:381-405."""
+    parsed = G.loadGGUFFile(path)
+    config = G.extractConfig(parsed["metadata"])
+    if config["arch"] != "llama":
+        raise ValueError("Forward not implemented for %s via GGUF loader" % config["arch"])
+    model = createGGUFModel(config)
+    res = loadWeights(parsed, model)
+    return GGUFModel(
+        model=model, config=config, metadata=parsed["metadata"], loaded=res["loaded"], skipped=res["skipped"],
+        forward=lambda tokenIds: forwardLlamaCachedPrefill(model, tokenIds, createGGUFCache(model["config"])),
+        createCache=lambda: createGGUFCache(model["config"]),
+        forwardPrefill=lambda tokenIds, caches: forwardLlamaCachedPrefill(model, tokenIds, caches),
+        forwardDecode=lambda tokenId, position, caches: forwardLlamaCachedDecode(model, tokenId, position, caches),
+        generate=lambda promptIds, genConfig=None, callbacks=None: generateGGUF(model, promptIds, genConfig or {},
+                                                                               callbacks or {}),
+        resetCache=resetCache,
+    )

@@ -44,13 +44,18 @@ def test_code_object_has_kernels():
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     need = ["matmul_q4", "matmul_q8", "smith_quantize_q4s", "smith_quantize_q8", "smith_quantize_q4_0_rows",
-            "smith_repack_q4_0", "smith_zero_u32"]
+            "smith_repack_q4_0_cols", "smith_repack_q8_0_cols", "smith_zero_u32"]
     for fmt in ("q4", "q8", "q40"):
         need += ["smith_qprep_%s_hilo" % fmt, "smith_qprep_%s_plain" % fmt]
     for fmt in ("q4s", "q8", "q40"):
         need += ["smith_qgemv3_%s_m%d" % (fmt, m) for m in (4, 8, 16, 32)]
         need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 128)]
     for k in need:
+        assert re.search(r"\b%s\.kd\b" % k, out), k
+    out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_lmhead_q4_0_nb",
+              "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
 
 

@@ -1,0 +1,113 @@
+"""GPU parity of loadGGUF(...).generate against the Llama oracle.
+
+Bars: logits normwise max|y - ref| / max|ref| <= 1e-2 per step (the path's
+stated tolerance; observed ~1e-5) with teacher forcing, so GPU and oracle
+consume the same tokens; greedy tokens equal the oracle's argmax except
+where the oracle's top-2 logits are within 1e-4 of each other.
+"""
+import numpy as np
+import pytest
+
+from oracle import llama_oracle as LO
+from oracle.oracle import normwise_rel_err
+from smith_amd.gguf_loader import loadGGUF
+from tests.llama_fixtures import write_tiny_llama
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+SMALL = dict(dim=256, layers=2, heads=4, kv_heads=2, ffn=512, vocab=320, context=2048)
+
+
+def _files(tmp_path_factory, name, **kw):
+    p = str(tmp_path_factory.mktemp("gguf") / name)
+    write_tiny_llama(p, **dict(SMALL, **kw))
+    return p
+
+
+@pytest.fixture(scope="module")
+def q4(tmp_path_factory):
+    return _files(tmp_path_factory, "q4.gguf")
+
+
+def check_tokens(gpu_tokens, ref_logits):
+    for i, (t, lg) in enumerate(zip(gpu_tokens, ref_logits)):
+        top2 = np.sort(lg)[-2:]
+        if t != int(np.argmax(lg)):
+            assert top2[1] - top2[0] < 1e-4 * max(1.0, abs(top2[1])), (i, t, int(np.argmax(lg)))
+
+
+def test_prefill_and_decode_logits(q4):
+    m = loadGGUF(q4)
+    ref = LO.LlamaOracle(q4)
+    prompt = [3, 77, 150, 9, 210, 44, 1]
+    caches = m.createCache()
+    got = m.forwardPrefill(prompt, caches)["logits"]
+    want = ref.forward(prompt, 0)
+    assert got.shape == (len(prompt), SMALL["vocab"])
+    assert normwise_rel_err(got, want) <= TOL
+    feed = [5, 250, 17]
+    for i, t in enumerate(feed):
+        g = m.forwardDecode(t, len(prompt) + i, caches)["logits"]
+        w = ref.forward([t], len(prompt) + i)
+        assert normwise_rel_err(g, w) <= TOL, i
+
+
+def test_generate_greedy_graph_and_sync_paths(q4):
+    m = loadGGUF(q4)
+    prompt = [11, 22, 33, 44, 55]
+    out = m.generate(prompt, {"maxTokens": 12, "temperature": 0})
+    assert out[:5] == prompt and len(out) == 5 + 12
+    gen = out[5:]
+    ref = LO.LlamaOracle(q4)
+    _, logits = ref.generate_greedy(prompt, 12, teacher=gen)
+    check_tokens(gen, logits)
+    seen = []
+    out2 = m.generate(prompt, {"maxTokens": 12, "temperature": 0}, {"onToken": lambda t, i: seen.append(t)})
+    assert out2 == out and seen == gen
+    # early stop through the callback and through eosToken
+    out3 = m.generate(prompt, {"maxTokens": 12, "temperature": 0}, {"onToken": lambda t, i: i >= 3})
+    assert out3 == out[:8]
+    out4 = m.generate(prompt, {"maxTokens": 12, "temperature": 0, "eosToken": gen[4]})
+    assert out4 == out[:5 + gen.index(gen[4]) + 1]
+
+
+@pytest.mark.parametrize("kw", [dict(tie=True), dict(linear_type="q8_0"), dict(kv_heads=4)])
+def test_variants(tmp_path_factory, kw):
+    p = _files(tmp_path_factory, "v.gguf", **kw)
+    m = loadGGUF(p)
+    ref = LO.LlamaOracle(p)
+    prompt = [1, 2, 3, 200]
+    out = m.generate(prompt, {"maxTokens": 6, "temperature": 0})
+    gen = out[4:]
+    _, logits = ref.generate_greedy(prompt, 6, teacher=gen)
+    check_tokens(gen, logits)
+    caches = m.createCache()
+    assert normwise_rel_err(m.forwardPrefill(prompt, caches)["logits"], ref.forward(prompt, 0)) <= TOL
+
+
+def test_long_prompt_chunked_prefill(q4):
+    m = loadGGUF(q4)
+    prompt = [int(x) for x in (np.arange(300) * 7919 % SMALL["vocab"])]
+    out = m.generate(prompt, {"maxTokens": 3, "temperature": 0})
+    ref = LO.LlamaOracle(q4)
+    _, logits = ref.generate_greedy(prompt, 3, teacher=out[300:])
+    check_tokens(out[300:], logits)
+
+
+def test_config5_dims_two_layers(tmp_path_factory):
+    """Config-5 widths (dim 3072, 24/8 heads, FFN 9216, vocab 32000), 2 layers."""
+    from smith_amd.synthetic_gguf import build_llama_gguf
+    p = str(tmp_path_factory.mktemp("c5") / "c5.gguf")
+    build_llama_gguf(p, dim=3072, layers=2, heads=24, kv_heads=8, ffn=9216, vocab=32000, context=8192, seed=5)
+    m = loadGGUF(p)
+    prompt = [int(x) for x in (np.arange(8) * 1237 % 32000)]
+    out = m.generate(prompt, {"maxTokens": 4, "temperature": 0})
+    ref = LO.LlamaOracle(p)
+    _, logits = ref.generate_greedy(prompt, 4, teacher=out[8:])
+    caches = m.createCache()
+    assert normwise_rel_err(m.forwardPrefill(prompt, caches)["logits"][-1], logits[0]) <= TOL
+    for i, t in enumerate(out[8:11]):
+        g = m.forwardDecode(t, 8 + i, caches)["logits"][0]
+        assert normwise_rel_err(g, logits[i + 1]) <= TOL, i
+    check_tokens(out[8:], logits)
