@@ -214,6 +214,47 @@ def calibrate(D, steps):
     return res
 
 
+def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3):
+    """Config 5: seeded synthetic Llama GGUF (Q4_0 linears), loadGGUF, then
+    generate(prompt of 128 seeded ids, maxTokens 128, temperature 0).
+    Decode tok/s = decode steps / decode time (HIP events around the greedy
+    graph replays); prefill reported separately."""
+    from smith_amd import prng
+    from smith_amd.gguf_loader import loadGGUF
+    from smith_amd.synthetic_gguf import CONFIG5, build_llama_gguf
+    t0 = time.perf_counter()
+    if not os.path.exists(path):
+        c = CONFIG5
+        build_llama_gguf(path, dim=c["dim"], layers=c["layers"], heads=c["heads"], kv_heads=c["kv_heads"],
+                         ffn=c["ffn"], vocab=c["vocab"], context=c["context"], seed=1)
+    t_write = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    m = loadGGUF(path)
+    t_load = time.perf_counter() - t0
+    prompt = [int(x) for x in prng.randint(prompt_len, m.config["vocabSize"], 7)]
+    m.generate(prompt, {"maxTokens": 4, "temperature": 0})  # warm-up (captures the decode graph)
+    best = None
+    for _ in range(reps):
+        D.timer_start()
+        out = m.generate(prompt, {"maxTokens": 1, "temperature": 0})
+        t_prefill = D.timer_stop()
+        D.timer_start()
+        out = m.generate(prompt, {"maxTokens": new_tokens, "temperature": 0})
+        t_all = D.timer_stop()
+        dec_ms = t_all - t_prefill
+        r = {"decode_tok_s": round((new_tokens - 1) / (dec_ms * 1e-3), 1), "decode_ms_per_token": round(dec_ms / (new_tokens - 1), 4),
+             "prefill_ms": round(t_prefill, 3), "prefill_tok_s": round(prompt_len / (t_prefill * 1e-3), 1),
+             "generate_ms": round(t_all, 3)}
+        if best is None or r["decode_tok_s"] > best["decode_tok_s"]:
+            best = r
+    gb_per_token = 1981808640 + 55296000  # Q4_0 linears + Q4_0 LM head (SURVEY.md §8 d)
+    best.update({"weights_GB_per_token": round(gb_per_token / 1e9, 3),
+                 "weight_stream_GBps": round(gb_per_token / (best["decode_ms_per_token"] * 1e-3) / 1e9, 1),
+                 "tokens_generated": len(out) - prompt_len, "gguf_write_s": round(t_write, 1),
+                 "load_s": round(t_load, 1), "first_tokens": out[prompt_len:prompt_len + 8]})
+    return best
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,6 +263,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no sweep / cpu baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate", action="store_true", help="print the platform floor (empty kernel, streaming read)")
+    ap.add_argument("--e2e-only", action="store_true", help="only the config-5 end-to-end decode")
+    ap.add_argument("--gguf", default="/tmp/smith_config5.gguf", help="synthetic config-5 GGUF path (written if absent)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (--gpus %d requested); the sharding design is "
@@ -236,6 +279,9 @@ def main():
     log("device:", D.device_name())
     if args.calibrate:
         print(json.dumps({"calibration": calibrate(D, args.steps)}), flush=True)
+        return
+    if args.e2e_only:
+        print(json.dumps({"cfg5_e2e": bench_e2e(D, args.gguf)}), flush=True)
         return
     K = N = 4096
     ms, kt, nbytes = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup)

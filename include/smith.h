@@ -162,7 +162,8 @@ int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, ui
 /* RoPE (whole-row indexing of rope.metal:18-37 as gguf_cache.js applies it)
  * + KV-cache append + GQA softmax attention for S rows at positions
  * *pos_ptr .. *pos_ptr+S-1 (gguf_cache.js:128-157, 212-231).  qkv rows are
- * [q | k | v] with stride ld; caches are [n_kv_heads, max_seq, head_dim]. */
+ * [q | k | v] with stride ld; caches are [n_kv_heads, max_seq, head_dim];
+ * head_dim <= 128 and a multiple of 4. */
 int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
                     uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
                     float* kcache, float* vcache, uint32_t max_seq, float* out);

@@ -62,104 +62,160 @@ __device__ __forceinline__ float rope_elem(const float* __restrict__ row, uint32
 // Fused RoPE + KV-cache append + GQA attention, for S query rows at positions
 // p0 .. p0+S-1 with p0 = *pos_ptr (gguf_cache.js:128-157 for decode,
 // :212-231 for prefill).  qkv rows hold [q | k | v] (ld floats per row).
-// Workgroup (h, s): q head h, row s; KV head kvh = h / (nH/nKV) (repeatKV,
-// gguf_cache.js:90-105).  Keys of positions < p0 come from the cache; keys of
-// p0..p0+s are roped here from the raw k of this launch (so no workgroup
-// depends on another); the workgroup with h % (nH/nKV) == 0 writes row s's
-// roped k and raw v into the cache.  scale = 1/sqrt(hd) after the dot
-// product, softmax with max subtraction, out = P V.  hd <= 128, positions
-// p0+S <= maxSeq, 256 threads.
+// q head h uses KV head h / (nH/nKV) (repeatKV, gguf_cache.js:90-105);
+// scores (q.k) * 1/sqrt(hd), softmax over positions 0..p0+s, out = P V.
+//
+// Workgroup (h, s, z): query row s, head h, split z of the NSPLIT splits of
+// its T = p0+s+1 key rows.  Keys/values of positions < p0 come from the
+// cache; those of p0..p0+s are formed here from the raw k (roped) and v of
+// this launch's qkv rows, so no workgroup depends on another's writes.  The
+// (h % rep == 0, z == 0) workgroup of row s writes row s's roped key and its
+// value into the cache.  Each split stages 32-row K and V tiles in LDS with
+// 128-bit loads and keeps an online softmax (running max m, sum l, output
+// o); partials go to a workspace and the last split to finish (per (h, s),
+// agent-scope atomics) combines them: out = sum_z e^(m_z-M) o_z /
+// sum_z e^(m_z-M) l_z.  hd <= 128, 256 threads.
 // ---------------------------------------------------------------------------
+#define ATT_SPLIT 8
+#define ATT_TILE 32
+
 extern "C" __global__ __launch_bounds__(256) void smith_attention(
     const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
     uint32_t nKV, uint32_t hd, const float* __restrict__ cosT, const float* __restrict__ sinT,
-    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out) {
-  extern __shared__ float sm[];
-  const uint32_t h = blockIdx.x, s = blockIdx.y;
+    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out,
+    float* __restrict__ ws, uint32_t* __restrict__ counters) {
+  __shared__ __attribute__((aligned(16))) float qr[128];
+  __shared__ __attribute__((aligned(16))) float Kt[ATT_TILE][129];
+  __shared__ __attribute__((aligned(16))) float Vt[ATT_TILE][128];
+  __shared__ float sc[ATT_TILE];
+  __shared__ float ored[2][128];
+  __shared__ int s_last;
+  const uint32_t h = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
+  const uint32_t tid = threadIdx.x;
   const uint32_t p0 = (uint32_t)pos_ptr[0];
   const uint32_t pos = p0 + s;
   const uint32_t T = pos + 1;
   const uint32_t rep = nH / nKV, kvh = h / rep;
   const uint32_t Wq = nH * hd, Wk = nKV * hd;
-  float* qr = sm;              // [hd]
-  float* kn = sm + 128;        // [S][hd] roped new keys of rows 0..s (only 0..s used)
-  float* sc = kn + S * 128;    // [T] scores
-  __shared__ float red[8];
-  __shared__ float stat[2];
-
+  const float scale = 1.0f / __builtin_sqrtf((float)hd);
   const float* qrow = qkv + (size_t)s * ld;
-  for (uint32_t e = threadIdx.x; e < hd; e += blockDim.x) qr[e] = rope_elem(qrow, Wq, h * hd + e, pos, cosT, sinT);
-  for (uint32_t idx = threadIdx.x; idx < (s + 1) * hd; idx += blockDim.x) {
-    uint32_t r = idx / hd, e = idx % hd;
-    kn[r * 128 + e] = rope_elem(qkv + (size_t)r * ld + Wq, Wk, kvh * hd + e, p0 + r, cosT, sinT);
-  }
-  __syncthreads();
-  if (h % rep == 0) {
-    const float* vrow = qkv + (size_t)s * ld + Wq + Wk;
-    for (uint32_t e = threadIdx.x; e < hd; e += blockDim.x) {
+  for (uint32_t e = tid; e < hd; e += 256) qr[e] = rope_elem(qrow, Wq, h * hd + e, pos, cosT, sinT);
+  if (h % rep == 0 && z == 0) {
+    const float* krow = qkv + (size_t)s * ld + Wq;
+    for (uint32_t e = tid; e < hd; e += 256) {
       size_t o = ((size_t)kvh * maxSeq + pos) * hd + e;
-      kcache[o] = kn[s * 128 + e];
-      vcache[o] = vrow[kvh * hd + e];
+      kcache[o] = rope_elem(krow, Wk, kvh * hd + e, pos, cosT, sinT);
+      vcache[o] = krow[Wk + kvh * hd + e];
     }
   }
-  const float scale = 1.0f / __builtin_sqrtf((float)hd);
-  // scores: one thread per position
-  float mx = -__builtin_inff();
-  for (uint32_t t = threadIdx.x; t < T; t += blockDim.x) {
-    const float* kr = t < p0 ? kcache + ((size_t)kvh * maxSeq + t) * hd : kn + (t - p0) * 128;
-    float d = 0.f;
-    for (uint32_t e = 0; e < hd; e++) d = __builtin_fmaf(qr[e], kr[e], d);
-    d *= scale;
-    sc[t] = d;
-    mx = d > mx ? d : mx;
+  // this split's key rows
+  const uint32_t per = (T + ATT_SPLIT - 1) / ATT_SPLIT;
+  const uint32_t t0 = z * per, t1 = t0 + per < T ? t0 + per : T;
+  const uint32_t e = tid % 128, part = tid / 128;  // output element, row half
+  float m = -__builtin_inff(), l = 0.f, o = 0.f;
+  __syncthreads();
+  for (uint32_t tb = t0; tb < t1; tb += ATT_TILE) {
+    const uint32_t nt = t1 - tb < ATT_TILE ? t1 - tb : ATT_TILE;
+    // stage K and V rows of the tile
+    for (uint32_t idx = tid; idx < nt * (hd / 4); idx += 256) {
+      uint32_t r = idx / (hd / 4), c4 = idx % (hd / 4);
+      uint32_t t = tb + r;
+      float4 kv4, vv4;
+      if (t < p0) {
+        kv4 = *(const float4*)(kcache + ((size_t)kvh * maxSeq + t) * hd + 4 * c4);
+        vv4 = *(const float4*)(vcache + ((size_t)kvh * maxSeq + t) * hd + 4 * c4);
+      } else {
+        const float* kr = qkv + (size_t)(t - p0) * ld + Wq;
+        uint32_t e0 = kvh * hd + 4 * c4;
+        kv4 = make_float4(rope_elem(kr, Wk, e0, t, cosT, sinT), rope_elem(kr, Wk, e0 + 1, t, cosT, sinT),
+                          rope_elem(kr, Wk, e0 + 2, t, cosT, sinT), rope_elem(kr, Wk, e0 + 3, t, cosT, sinT));
+        vv4 = *(const float4*)(kr + Wk + e0);
+      }
+      Kt[r][4 * c4] = kv4.x;
+      Kt[r][4 * c4 + 1] = kv4.y;
+      Kt[r][4 * c4 + 2] = kv4.z;
+      Kt[r][4 * c4 + 3] = kv4.w;
+      *(float4*)&Vt[r][4 * c4] = vv4;
+    }
+    __syncthreads();
+    // scores: 8 lanes per row
+    {
+      uint32_t r = tid / 8, sub = tid % 8;
+      float d = 0.f;
+      if (r < nt)
+        for (uint32_t c = sub; c < hd; c += 8) d = __builtin_fmaf(qr[c], Kt[r][c], d);
+      d += __shfl_xor(d, 1);
+      d += __shfl_xor(d, 2);
+      d += __shfl_xor(d, 4);
+      if (sub == 0 && r < ATT_TILE) sc[r] = r < nt ? d * scale : -__builtin_inff();
+    }
+    __syncthreads();
+    float tm = -__builtin_inff();
+    for (uint32_t r = 0; r < nt; r++) tm = sc[r] > tm ? sc[r] : tm;
+    const float mn = tm > m ? tm : m;
+    const float alpha = __expf(m - mn);
+    float ps = 0.f, acc = 0.f;
+    for (uint32_t r = 0; r < nt; r++) {
+      float p = __expf(sc[r] - mn);
+      ps += p;
+      if ((r & 1) == part && e < hd) acc = __builtin_fmaf(p, Vt[r][e], acc);
+    }
+    l = l * alpha + ps;
+    o = o * alpha + acc;
+    m = mn;
+    __syncthreads();
   }
-  for (int dd = 32; dd >= 1; dd >>= 1) {
-    float o = __shfl_xor(mx, dd);
-    mx = o > mx ? o : mx;
+  // combine the two row halves of this split
+  if (e < hd) ored[part][e] = o;
+  __syncthreads();
+  const size_t slot = ((size_t)s * nH + h) * ATT_SPLIT + z;
+  float* wsp = ws + slot * 130;
+  if (tid < hd) {
+    float v = ored[0][tid] + ored[1][tid];
+    __hip_atomic_exchange((uint32_t*)wsp + 2 + tid, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float m = red[0];
-    for (uint32_t w = 1; w < blockDim.x / 64; w++) m = red[w] > m ? red[w] : m;
-    stat[0] = m;
+  if (tid == 0) {
+    __hip_atomic_exchange((uint32_t*)wsp, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_exchange((uint32_t*)wsp + 1, __float_as_uint(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  mx = stat[0];
-  float sum = 0.f;
-  for (uint32_t t = threadIdx.x; t < T; t += blockDim.x) {
-    float e = __expf(sc[t] - mx);
-    sc[t] = e;
-    sum += e;
-  }
-  for (int dd = 32; dd >= 1; dd >>= 1) sum += __shfl_xor(sum, dd);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float tot = 0.f;
-    for (uint32_t w = 0; w < blockDim.x / 64; w++) tot += red[w];
-    stat[1] = 1.0f / tot;
+  uint32_t* cnt = counters + (size_t)s * nH + h;
+  if (tid == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == ATT_SPLIT - 1;
   }
   __syncthreads();
-  const float inv = stat[1];
-  // out[e] = sum_t p_t v_t[e]: thread (e, part) over interleaved positions
-  const uint32_t parts = blockDim.x / hd;  // hd divides 256 (64 or 128)
-  const uint32_t e = threadIdx.x % hd, part = threadIdx.x / hd;
-  float acc = 0.f;
-  for (uint32_t t = part; t < T; t += parts) {
-    float v = t < p0 ? vcache[((size_t)kvh * maxSeq + t) * hd + e]
-                     : qkv[(size_t)(t - p0) * ld + Wq + Wk + kvh * hd + e];
-    acc = __builtin_fmaf(sc[t], v, acc);
+  if (!s_last) return;
+  const float* base = ws + ((size_t)s * nH + h) * ATT_SPLIT * 130;
+  auto ld32 = [&](const float* p) {
+    return __uint_as_float(__hip_atomic_fetch_add((uint32_t*)p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  };
+  __shared__ float mz_s[ATT_SPLIT], wz_s[ATT_SPLIT];
+  if (tid < ATT_SPLIT) {
+    mz_s[tid] = ld32(base + tid * 130);
+    wz_s[tid] = ld32(base + tid * 130 + 1);
   }
   __syncthreads();
-  sc[threadIdx.x] = acc;  // scores are consumed; reuse for the part reduction
-  __syncthreads();
-  if (part == 0) {
+  float M = -__builtin_inff();
+#pragma unroll
+  for (int zz = 0; zz < ATT_SPLIT; zz++) M = mz_s[zz] > M ? mz_s[zz] : M;
+  float L = 0.f, wz[ATT_SPLIT];
+#pragma unroll
+  for (int zz = 0; zz < ATT_SPLIT; zz++) {
+    wz[zz] = mz_s[zz] == -__builtin_inff() ? 0.f : __expf(mz_s[zz] - M);
+    L = __builtin_fmaf(wz[zz], wz_s[zz], L);
+  }
+  if (tid < hd) {
+    float ov[ATT_SPLIT];
+#pragma unroll
+    for (int zz = 0; zz < ATT_SPLIT; zz++) ov[zz] = ld32(base + zz * 130 + 2 + tid);
     float v = 0.f;
-    for (uint32_t q = 0; q < parts; q++) v += sc[q * hd + e];
-    out[(size_t)s * Wq + h * hd + e] = v * inv;
+#pragma unroll
+    for (int zz = 0; zz < ATT_SPLIT; zz++) v = __builtin_fmaf(wz[zz], ov[zz], v);
+    out[(size_t)s * Wq + h * hd + tid] = v / L;
   }
+  if (tid == 0) __hip_atomic_exchange(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -212,14 +268,26 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
   const uint32_t kper = (kb1 - kb0 + 7) / 8;
   const uint32_t k0 = kb0 + wave * kper, k1 = k0 + kper < kb1 ? k0 + kper : kb1;
   if (vb < NB) {
-    for (uint32_t k = k0; k < k1; k++) {
-      const uint8_t* b = W + ((size_t)k * NB + vb) * 18;
-      float c = xs[k] * (float)__builtin_bit_cast(_Float16, *(const uint16_t*)b);
-      const uint16_t* q = (const uint16_t*)(b + 2 + 4 * sub);  // records are only 2-byte aligned
-      uint32_t w = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
-      corr += c;
+    // 16 rows per batch: all of a batch's loads are issued before any use
+    for (uint32_t kb8 = k0; kb8 < k1; kb8 += 16) {
+      uint16_t dh[16], lo[16], hi[16];
 #pragma unroll
-      for (int e = 0; e < 8; e++) acc[e] = __builtin_fmaf(c, (float)((w >> (4 * e)) & 15u), acc[e]);
+      for (int r = 0; r < 16; r++) {
+        uint32_t k = kb8 + r < k1 ? kb8 + r : k1 - 1;
+        const uint16_t* b = (const uint16_t*)(W + ((size_t)k * NB + vb) * 18);  // 2-byte aligned records
+        dh[r] = b[0];
+        lo[r] = b[1 + 2 * sub];
+        hi[r] = b[2 + 2 * sub];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        if (kb8 + r >= k1) break;
+        float c = xs[kb8 + r] * (float)__builtin_bit_cast(_Float16, dh[r]);
+        uint32_t w = (uint32_t)lo[r] | ((uint32_t)hi[r] << 16);
+        corr += c;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = __builtin_fmaf(c, (float)((w >> (4 * e)) & 15u), acc[e]);
+      }
     }
   }
 #pragma unroll

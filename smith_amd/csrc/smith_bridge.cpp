@@ -56,6 +56,10 @@ struct Ctx {
   size_t counters_n = 0;
   void* normbuf = nullptr;
   size_t normbuf_bytes = 0;
+  void* att_ws = nullptr;
+  size_t att_ws_bytes = 0;
+  uint32_t* att_cnt = nullptr;
+  size_t att_cnt_n = 0;
   bool capturing = false;
   // per-launch HIP event pairs of op-level kernels while profiling is on
   bool profile = false;
@@ -267,9 +271,10 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
 int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
                  uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
   const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
-  bool small = G <= 64;
-  uint32_t kb = small ? 64 : 128;
-  uint32_t threads = small ? 256 : 512;
+  // block K coverage (groups): the smallest variant that covers K in one
+  // block, else 128 with a cross-block split
+  uint32_t kb = G <= 64 ? 64 : (G <= 96 ? 96 : (G <= 128 ? 128 : (G <= 288 ? 288 : 128)));
+  uint32_t threads = kb == 64 ? 256 : 512;
   uint32_t gx = (N + 15) / 16;
   uint32_t ksplit = (G + kb - 1) / kb;
   if (ksplit > 1) {
@@ -364,6 +369,8 @@ void smith_destroy(void* ctx) {
   }
   if (c->prep) hipFree(c->prep);
   if (c->normbuf) hipFree(c->normbuf);
+  if (c->att_ws) hipFree(c->att_ws);
+  if (c->att_cnt) hipFree(c->att_cnt);
   if (c->ws) hipFree(c->ws);
   if (c->counters) hipFree(c->counters);
   for (auto& r : c->recs) {
@@ -895,6 +902,7 @@ int smith_linear_q8(void* ctx, const float* x, const void* wq, float* out, uint3
                     const float* norm_gamma, float eps, const float* resid, uint32_t epilogue) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
+  if (K % 32) return fail(c, "smith_linear_q8: K %u is not a multiple of 32 (GGUF Q8_0 rows)", K);
   if (epilogue > 2) return fail(c, "smith_linear_q8: unknown epilogue %u", epilogue);
   if (epilogue == 1 && !resid) return fail(c, "smith_linear_q8: residual epilogue without a residual buffer");
   Epi e;
@@ -928,16 +936,30 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
                     float* kcache, float* vcache, uint32_t max_seq, float* out) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
-  if (!n_kv_heads || n_heads % n_kv_heads) return fail(c, "smith_attention: %u heads not a multiple of %u kv heads", n_heads, n_kv_heads);
-  if (head_dim > 128 || 256 % head_dim) return fail(c, "smith_attention: head_dim %u unsupported (64 or 128)", head_dim);
-  if (S > 256) return fail(c, "smith_attention: %u rows per launch exceeds 256", S);
+  if (!n_kv_heads || n_heads % n_kv_heads)
+    return fail(c, "smith_attention: %u heads not a multiple of %u kv heads", n_heads, n_kv_heads);
+  if (head_dim > 128 || head_dim % 4) return fail(c, "smith_attention: head_dim %u unsupported (<= 128, % 4)", head_dim);
   if (set_device(c)) return -1;
   if (!S) return 0;
-  size_t smem = (128 + (size_t)S * 128 + std::max<size_t>(256, max_seq)) * sizeof(float);
-  if (smem > 160 * 1024) return fail(c, "smith_attention: %zu bytes of LDS needed (max_seq %u, S %u)", smem, max_seq, S);
+  const uint32_t nsplit = 8;  // ATT_SPLIT in llama_kernels.hip
+  size_t slots = (size_t)S * n_heads;
+  if (ensure(c, &c->att_ws, &c->att_ws_bytes, slots * nsplit * 130 * sizeof(float))) return -1;
+  if (slots > c->att_cnt_n) {
+    if (c->capturing) return fail(c, "smith_attention: counters needed while capturing; run once first");
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (c->att_cnt) HIPCHK(c, hipFree(c->att_cnt));
+    c->att_cnt = nullptr;
+    c->att_cnt_n = 0;
+    size_t cap = std::max<size_t>(slots, 4096);
+    HIPCHK(c, hipMalloc((void**)&c->att_cnt, cap * sizeof(uint32_t)));
+    HIPCHK(c, hipMemset(c->att_cnt, 0, cap * sizeof(uint32_t)));
+    c->att_cnt_n = cap;
+  }
+  void* pws = c->att_ws;
+  uint32_t* pcnt = c->att_cnt;
   void* args[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
-                  &kcache, &vcache, &max_seq, &out};
-  return launch(c, "smith_attention", dim3(n_heads, S), dim3(256), args, (unsigned)smem);
+                  &kcache, &vcache, &max_seq, &out, &pws, &pcnt};
+  return launch(c, "smith_attention", dim3(n_heads, S, nsplit), dim3(256), args);
 }
 
 int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,
@@ -948,7 +970,8 @@ int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, flo
   if (K > 8192) return fail(c, "smith_lmhead_q4_0_nb: dim %u exceeds 8192", K);
   if (set_device(c)) return -1;
   uint32_t gx = (N / 32 + 15) / 16;
-  uint32_t ksplit = std::max<uint32_t>(1, std::min<uint32_t>((256 + gx - 1) / gx, (K + 63) / 64));
+  // enough K splits that each of a workgroup's 8 waves has <= 32 rows
+  uint32_t ksplit = std::max<uint32_t>(1, std::min<uint32_t>((K + 255) / 256, 64));
   if (ksplit > 1) {
     if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
     if (ensure_counters(c, gx)) return -1;

@@ -427,9 +427,9 @@ __device__ __forceinline__ void splitk_finish(float* __restrict__ ws, uint32_t* 
 // the accumulator layout -- the lanes that hold that group's scale and zero.
 // Rows u: 0 = hi(row 0), 1 = lo(row 0)*2048, 2 = hi(row 1), 3 = lo(row 1).
 //
-// The block loads its K range of the activations, issues all of its weight
-// loads, and converts the activations into those f16 fragments in LDS (plus
-// per-group C1 and S) while the weights are in flight.  WK waves split the
+// The block issues all of its weight loads first, then loads its K range of
+// the activations (and, with a fused RMSNorm, the full rows) and converts
+// them into those f16 fragments in LDS (plus per-group C1 and S).  WK waves split the
 // block's groups (reduced through LDS), WN waves sit side by side along N.
 // Grid: x = column blocks of 16*CT*WN, y = K splits of 4*S*WK groups.
 // ---------------------------------------------------------------------------
@@ -525,24 +525,50 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   const uint32_t gw = gb + wk * GPW;
   const uint32_t ksplit = gridDim.y;
 
-  // 0. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
+  // 1. weights first: every record of this wave, all loads in flight
+  Rec<FMT> wr[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+
+  // 2. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
   //    that consumes it): every workgroup sums x^2 over its rows' full K
   float nss[MR];
 #pragma unroll
   for (int m = 0; m < MR; m++) nss[m] = 0.f;
   if (gamma) {
+    // K % 32 == 0 on this path: float4 loads, all of a thread's issued together
 #pragma unroll
     for (int m = 0; m < MR; m++)
-      if ((uint32_t)m < M)
-        for (uint32_t i = threadIdx.x; i < K; i += NT) nss[m] = __builtin_fmaf(A[(size_t)m * K + i], A[(size_t)m * K + i], nss[m]);
+      if ((uint32_t)m < M) {
+        const float4* ar = (const float4*)(A + (size_t)m * K);
+        for (uint32_t i = threadIdx.x; i < K / 4; i += NT) {
+          float4 v = ar[i];
+          nss[m] = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, nss[m]))));
+        }
+      }
   }
 
-  // 1. activation loads first (small, cache resident): the in-order load
-  //    counter then lets the conversion below run while weights are in flight
+  // 3. activation loads (small, cache resident), with the RMSNorm gammas
   const int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
   const int perm_q8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
   const float off_q4[8] = {1024.f, 1024.f, 64.f, 64.f, 1024.f, 1024.f, 64.f, 64.f};
   float av[CPT][8];
+  float gv[CPT][8];
+  if (gamma) {
+#pragma unroll
+    for (int cc = 0; cc < CPT; cc++) {
+      uint32_t ch = threadIdx.x + cc * NT;
+      uint32_t i = ch & 3, gl = (ch >> 2) / MR;
+      uint32_t k0 = (gb + gl) * 32 + 8 * i;
+      bool in = ch < (uint32_t)NCH && k0 + 8 <= K;
+      const float4* gp = (const float4*)(gamma + (in ? k0 : 0));
+      float4 g0 = gp[0], g1 = gp[1];
+      gv[cc][0] = g0.x; gv[cc][1] = g0.y; gv[cc][2] = g0.z; gv[cc][3] = g0.w;
+      gv[cc][4] = g1.x; gv[cc][5] = g1.y; gv[cc][6] = g1.z; gv[cc][7] = g1.w;
+    }
+  }
 #pragma unroll
   for (int cc = 0; cc < CPT; cc++) {
     uint32_t ch = threadIdx.x + cc * NT;
@@ -563,14 +589,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     }
   }
 
-  // 2. weights: every record of this wave, all loads in flight
-  Rec<FMT> wr[S][CT];
-#pragma unroll
-  for (int st = 0; st < S; st++)
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
-
-  // 3. activations -> f16 hi/lo fragments + (C1, S) in LDS
+  // 4. activations -> f16 hi/lo fragments + (C1, S) in LDS
   float rms[MR];
   if (gamma) {
 #pragma unroll
@@ -591,13 +610,11 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
       uint32_t ch = threadIdx.x + cc * NT;
       uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
       uint32_t k0 = (gb + gl) * 32 + 8 * i;
+      float r = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        float r = 0.f;
+      for (int q = 0; q < MR; q++) r = (uint32_t)q == m ? rms[q] : r;
 #pragma unroll
-        for (int q = 0; q < MR; q++) r = (uint32_t)q == m ? rms[q] : r;
-        av[cc][e] = (k0 + e < K) ? av[cc][e] * r * gamma[k0 + e] : 0.f;
-      }
+      for (int e = 0; e < 8; e++) av[cc][e] = (k0 + e < K) ? av[cc][e] * r * gv[cc][e] : 0.f;
     }
   }
 #pragma unroll
@@ -644,7 +661,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   }
   __syncthreads();
 
-  // 4. MFMAs: lane (r = lane%16, j) feeds A row r from K slice j only
+  // 5. MFMAs: lane (r = lane%16, j) feeds A row r from K slice j only
   const uint32_t r = lane & 15;
   const bool a_active = (r >> 2) == j && (r & 3) < 2 * MR;
   const uint32_t ru = a_active ? (r & 3) : 0;
@@ -681,7 +698,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     }
   }
 
-  // 5. sum the four lane groups (different K groups, same column), then the
+  // 6. sum the four lane groups (different K groups, same column), then the
   //    WK waves of the block in fixed order
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
@@ -925,13 +942,18 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
     qgemv3_body<FMT, RB, HILO, VPL, CT, S, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G, R, epi);   \
   }
 
-// Fused M <= 2 variants: "k128" = 8 waves x 4 steps (128 groups per block),
-// "k64" = 4 waves x 4 steps (64 groups per block).
+// Fused M <= 2 variants, named by the groups one block covers: k64 = 4 waves
+// x 4 steps, k96 / k128 / k288 = 8 waves x 3 / 4 / 9 steps (K = 3072, 4096,
+// 9216 in one block).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96, FMT, 1, 1, 8, 1, 3)             \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288, FMT, 1, 1, 8, 1, 9)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k128, FMT, 2, 1, 8, 1, 4)            \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)             \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k96, FMT, 2, 1, 8, 1, 3)             \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k288, FMT, 2, 1, 8, 1, 9)
 
 // M > 2 row buckets (RB, HILO, VPL): m4 / m8 hi/lo, m16 / m32 plain f16;
 // 2 column tiles x 1 step per wave, 8 waves split the block's 32 groups.

@@ -12,11 +12,22 @@ then the LM head (final RMSNorm fused) and a device-side greedy step
 lives in device memory, so the greedy decode step is captured once as a HIP
 graph and replayed.
 """
+import os
+
 import numpy as np
 
 from . import device
 
+# SMITH_DECODE_GRAPH=0 runs every decode step eagerly (kernel-level profilers
+# that cannot trace graph replays); results are identical.
+USE_GRAPH = os.environ.get("SMITH_DECODE_GRAPH", "1") != "0"
+
 PREFILL_CHUNK = 256
+
+
+def _chunk_rows(cfg):
+    """Rows per prefill launch (bounded by the activation buffers)."""
+    return PREFILL_CHUNK
 
 
 def createGGUFCache(config):
@@ -108,8 +119,9 @@ class _Engine:
         LDS); returns the logits of every row if asked, else of the last."""
         n = len(tokens)
         rows = []
-        for r0 in range(0, n, PREFILL_CHUNK):
-            r1 = min(n, r0 + PREFILL_CHUNK)
+        step = _chunk_rows(self.cfg)
+        for r0 in range(0, n, step):
+            r1 = min(n, r0 + step)
             self.embed(model, tokens[r0:r1])
             self.set_pos(r0)
             self.layers(model, caches, r1 - r0)
@@ -117,7 +129,7 @@ class _Engine:
                 for r in range(r1 - r0):
                     self.lm_head(model, self.x.ptr + r * self.cfg["dim"] * 4)
                     rows.append(self.logits.numpy().copy())
-        last = (n - 1) % PREFILL_CHUNK
+        last = (n - 1) % step
         if not all_logits:
             self.lm_head(model, self.x.ptr + last * self.cfg["dim"] * 4)
         for c in caches:
@@ -242,7 +254,7 @@ def generateGGUF(model, promptIds, config=None, callbacks=None):
                 return generated
         graph = None
         for i in range(1, steps + 1):
-            if graph is None and i >= 2:
+            if USE_GRAPH and graph is None and i >= 2:
                 graph = _decode_graph(model, e, caches)
             if graph is not None:
                 device.check(device.lib.smith_graph_launch(device.ops_ctx(), graph), "graph launch")

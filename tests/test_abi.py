@@ -49,7 +49,7 @@ def test_code_object_has_kernels():
         need += ["smith_qprep_%s_hilo" % fmt, "smith_qprep_%s_plain" % fmt]
     for fmt in ("q4s", "q8", "q40"):
         need += ["smith_qgemv3_%s_m%d" % (fmt, m) for m in (4, 8, 16, 32)]
-        need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 128)]
+        need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 96, 128, 288)]
     for k in need:
         assert re.search(r"\b%s\.kd\b" % k, out), k
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
