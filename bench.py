@@ -30,7 +30,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 400 << 20
 # HBM bytes per config-1 GEMV launch from two rocprofv3 --pmc passes
-# (profiles/qgemv1_q4s_m1_cfg1_hbm_traffic.md): FETCH_SIZE 6251.5 KiB x 1.996
+# (the committed qgemv1 config-1 HBM traffic profile): FETCH_SIZE 6251.5 KiB x 1.996
 # (factor from a 12,582,912 B device copy) + WRITE_SIZE 16.0 KiB x 1.0.
 TRAFFIC_CFG1 = 12793900
 
@@ -247,7 +247,7 @@ def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3):
              "generate_ms": round(t_all, 3)}
         if best is None or r["decode_tok_s"] > best["decode_tok_s"]:
             best = r
-    gb_per_token = 1981808640 + 55296000  # Q4_0 linears + Q4_0 LM head (SURVEY.md §8 d)
+    gb_per_token = 1981808640 + 55296000  # Q4_0 linears + Q4_0 LM head of config 5
     best.update({"weights_GB_per_token": round(gb_per_token / 1e9, 3),
                  "weight_stream_GBps": round(gb_per_token / (best["decode_ms_per_token"] * 1e-3) / 1e9, 1),
                  "tokens_generated": len(out) - prompt_len, "gguf_write_s": round(t_write, 1),
@@ -267,8 +267,8 @@ def main():
     ap.add_argument("--gguf", default="/tmp/smith_config5.gguf", help="synthetic config-5 GGUF path (written if absent)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU only (--gpus %d requested); the sharding design is "
-              "described in DESIGN.md" % args.gpus, file=sys.stderr)
+        print("bench.py: this build measures one GPU only (--gpus %d requested); multi-GPU "
+              "sharding is not implemented" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
     import smith_amd as S

@@ -140,8 +140,9 @@ int smith_quantize_q4_0(void* ctx, const float* x, void* out, uint32_t rows, uin
  * Weights listed [out=N, in=K] in the file.  The *_into repacks place column
  * n of a weight at column n_off + n*n_stride of a shared N_total-column
  * buffer (q|k|v concatenated; gate/up interleaved for the SwiGLU epilogue),
- * moving blocks without changing a byte (gguf_loader.js:216-273 keeps
- * nothing quantized; this is the wiring SURVEY.md f1 calls for). */
+ * moving blocks without changing a byte (gguf_loader.js:216-273 dequantizes
+ * everything to f32 instead; keeping the blocks is what makes the decode
+ * HBM-bound on 4.5 bits per weight). */
 int smith_repack_q4_0_into(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K,
                            uint32_t n_off, uint32_t n_stride, uint32_t N_total);
 int smith_repack_q8_0_into(void* ctx, const void* blocks, void* dst, uint32_t N, uint32_t K, uint32_t n_off,
@@ -155,18 +156,42 @@ int smith_linear_q4_0(void* ctx, const float* x, const void* nib, const void* d,
                       uint32_t K, const float* norm_gamma, float eps, const float* resid, uint32_t epilogue);
 int smith_linear_q8(void* ctx, const float* x, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
                     const float* norm_gamma, float eps, const float* resid, uint32_t epilogue);
+/* Q4_0 in tile-major planes (16-column tiles, each G*256 nibble bytes
+ * contiguous; f16 scales at the same record index): the layout the decode
+ * kernels stream.  N_total % 16 == 0.  Same placement rules as
+ * smith_repack_q4_0_into. */
+int smith_repack_q4_0_t_into(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K,
+                             uint32_t n_off, uint32_t n_stride, uint32_t N_total);
+/* smith_linear_q4_0 on tile-major planes (N % 16 == 0). */
+int smith_linear_q4_0_t(void* ctx, const float* x, const void* nib, const void* d, float* out, uint32_t M,
+                        uint32_t N, uint32_t K, const float* norm_gamma, float eps, const float* resid,
+                        uint32_t epilogue);
+/* Single-row linear on a prepared activation ("act": the input vector in the
+ * MFMA operand form plus per-8-element sums, K*4 + K/8*12 bytes) written by
+ * the producing kernel.  norm != 0: RMSNorm of the input (its gamma was
+ * applied when the act was written; rms comes from the act's sums of
+ * squares).  Epilogues as smith_linear_q4_0; out may be NULL.  act_out !=
+ * NULL: also write the act of the output vector (times gamma_out, when not
+ * NULL) for the next projection; the output length must be a multiple of
+ * 32.  Same results as smith_linear_q4_0_t up to f32 rounding order. */
+int smith_linear_q4_0_t_act(void* ctx, const void* act_in, int norm, float eps, const void* nib, const void* d,
+                            float* out, uint32_t N, uint32_t K, const float* resid, uint32_t epilogue,
+                            void* act_out, const float* gamma_out);
 /* rmsnormForward (ops/rmsnorm.js:19-37) over rows. */
 int smith_rmsnorm(void* ctx, const float* x, const float* gamma, float* out, uint32_t rows, uint32_t cols, float eps);
-/* embedding gather (autograd.js:308-334): out[r] = E[tokens[r]]. */
-int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, uint32_t rows, uint32_t dim);
+/* embedding gather (autograd.js:308-334): out[r] = E[tokens[r]]; with
+ * act_out (rows == 1) also the act of out times gamma_out. */
+int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, uint32_t rows, uint32_t dim,
+                void* act_out, const float* gamma_out);
 /* RoPE (whole-row indexing of rope.metal:18-37 as gguf_cache.js applies it)
  * + KV-cache append + GQA softmax attention for S rows at positions
  * *pos_ptr .. *pos_ptr+S-1 (gguf_cache.js:128-157, 212-231).  qkv rows are
  * [q | k | v] with stride ld; caches are [n_kv_heads, max_seq, head_dim];
- * head_dim <= 128 and a multiple of 4. */
+ * head_dim <= 128 and a multiple of 4.  act_out (S == 1): also the act of
+ * the output row for the output projection. */
 int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
                     uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
-                    float* kcache, float* vcache, uint32_t max_seq, float* out);
+                    float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out);
 /* LM head on a Q4_0 output.weight read as lmHead[K=dim][N=vocab] (blocks run
  * along the vocab axis, gguf_loader.js:240-259), optional fused final RMSNorm. */
 int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,
@@ -175,9 +200,10 @@ int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, flo
 int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,
                    uint32_t K, uint32_t N, int w_is_nk);
 /* greedy step on device: token = argmax(logits) (generate.js:70-76),
- * tokens[*count] = token, x = E[token], ++*count, ++*pos. */
+ * tokens[*count] = token, x = E[token], ++*count, ++*pos; with act_out also
+ * the act of x times gamma_out. */
 int smith_argmax_embed(void* ctx, const float* logits, uint32_t N, const float* E, uint32_t dim, float* x,
-                       int32_t* tokens, int32_t* count, int32_t* pos);
+                       int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out);
 int smith_set_i32(void* ctx, int32_t* p, int32_t v);
 /* seeded N(mean, std) f32 stream (SplitMix64 + Box-Muller), offset even. */
 int smith_randn(void* ctx, float* out, uint64_t n, uint64_t seed, uint64_t offset, float stdv, float mean);

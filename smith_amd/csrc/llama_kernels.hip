@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "act_frag.h"
+
 // ---------------------------------------------------------------------------
 // RMSNorm rows: y = x * rsqrt(mean(x^2) + eps) * gamma
 // (shaders/rmsnorm.metal:15-47; one workgroup per row).
@@ -35,11 +37,16 @@ extern "C" __global__ __launch_bounds__(256) void smith_rmsnorm_rows(const float
 // Embedding gather (autograd.js:308-334): out[r] = E[tokens[r]].
 // ---------------------------------------------------------------------------
 extern "C" __global__ void smith_embed_rows(const float* __restrict__ E, const int32_t* __restrict__ tokens,
-                                            float* __restrict__ out, uint32_t rows, uint32_t dim) {
+                                            float* __restrict__ out, uint32_t rows, uint32_t dim,
+                                            uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out) {
   uint32_t r = blockIdx.x;
   if (r >= rows) return;
   const float* src = E + (size_t)tokens[r] * dim;
-  for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) out[(size_t)r * dim + i] = src[i];
+  for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+    const float v = src[i];
+    out[(size_t)r * dim + i] = v;
+    if (act_out) act_emit8(act_out, dim, i, v, gamma_out ? gamma_out[i] : 1.0f);  // rows == 1, dim % 32 == 0
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -83,7 +90,7 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention(
     const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
     uint32_t nKV, uint32_t hd, const float* __restrict__ cosT, const float* __restrict__ sinT,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out,
-    float* __restrict__ ws, uint32_t* __restrict__ counters) {
+    float* __restrict__ ws, uint32_t* __restrict__ counters, uint8_t* __restrict__ act_out) {
   __shared__ __attribute__((aligned(16))) float qr[128];
   __shared__ __attribute__((aligned(16))) float Kt[ATT_TILE][129];
   __shared__ __attribute__((aligned(16))) float Vt[ATT_TILE][128];
@@ -213,7 +220,9 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention(
     float v = 0.f;
 #pragma unroll
     for (int zz = 0; zz < ATT_SPLIT; zz++) v = __builtin_fmaf(wz[zz], ov[zz], v);
-    out[(size_t)s * Wq + h * hd + tid] = v / L;
+    const float y = v / L;
+    out[(size_t)s * Wq + h * hd + tid] = y;
+    if (act_out) act_emit8(act_out, Wq, h * hd + tid, y, 1.0f);  // S == 1, hd % 8 == 0
   }
   if (tid == 0) __hip_atomic_exchange(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -284,9 +293,13 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
         if (kb8 + r >= k1) break;
         float c = xs[kb8 + r] * (float)__builtin_bit_cast(_Float16, dh[r]);
         uint32_t w = (uint32_t)lo[r] | ((uint32_t)hi[r] << 16);
+        uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 2j / 2j+1 in byte j
         corr += c;
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = __builtin_fmaf(c, (float)((w >> (4 * e)) & 15u), acc[e]);
+        for (int jb = 0; jb < 4; jb++) {
+          acc[2 * jb] = __builtin_fmaf(c, (float)((ev >> (8 * jb)) & 0xFFu), acc[2 * jb]);
+          acc[2 * jb + 1] = __builtin_fmaf(c, (float)((od >> (8 * jb)) & 0xFFu), acc[2 * jb + 1]);
+        }
       }
     }
   }
@@ -414,7 +427,9 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(const floa
                                                                       float* __restrict__ x,
                                                                       int32_t* __restrict__ tokens,
                                                                       int32_t* __restrict__ count,
-                                                                      int32_t* __restrict__ pos) {
+                                                                      int32_t* __restrict__ pos,
+                                                                      uint8_t* __restrict__ act_out,
+                                                                      const float* __restrict__ gamma_out) {
   __shared__ float bv[16];
   __shared__ int32_t bi[16];
   __shared__ int32_t s_tok;
@@ -456,7 +471,11 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(const floa
   }
   __syncthreads();
   const int32_t t = s_tok;
-  for (uint32_t i = threadIdx.x; i < dim; i += 1024) x[i] = E[(size_t)t * dim + i];
+  for (uint32_t i = threadIdx.x; i < dim; i += 1024) {
+    const float v = E[(size_t)t * dim + i];
+    x[i] = v;
+    if (act_out) act_emit8(act_out, dim, i, v, gamma_out ? gamma_out[i] : 1.0f);  // dim % 32 == 0
+  }
   __syncthreads();
   if (threadIdx.x == 0) pos[0] = pos[0] + 1;
 }

@@ -201,7 +201,9 @@ int ensure_counters(Ctx* c, size_t n) {
   return 0;
 }
 
-enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2 };
+enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2, FQ40T = 3 };
+
+const char* fmt_tag(Fmt f) { return f == FQ4S ? "q4s" : (f == FQ8 ? "q8" : (f == FQ40 ? "q40" : "q40t")); }
 
 // M > 2: prepare the activations once (smith_qprep_*), then the 16-row
 // MFMA GEMV (smith_qgemv3_*).  Buckets must match DEF_QGEMV3_FMT.
@@ -214,8 +216,8 @@ struct Epi {
 
 int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
                  uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
-  const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
-  const char* ptag = fmt == FQ4S ? "q4" : (fmt == FQ8 ? "q8" : "q40");
+  const char* tag = fmt_tag(fmt);
+  const char* ptag = fmt == FQ4S ? "q4" : (fmt == FQ8 ? "q8" : "q40");  // Q4_0 layouts share one prep
   uint32_t bucket = M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
   bool hilo = bucket <= 8;
   uint32_t RB = bucket == 32 ? 2 : 1;
@@ -270,19 +272,21 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
 // block's 64/128 groups do not cover K).
 int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
                  uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
-  const char* tag = fmt == FQ4S ? "q4s" : (fmt == FQ8 ? "q8" : "q40");
+  const char* tag = fmt_tag(fmt);
   // block K coverage (groups): the smallest variant that covers K in one
   // block, else 128 with a cross-block split
   uint32_t kb = G <= 64 ? 64 : (G <= 96 ? 96 : (G <= 128 ? 128 : (G <= 288 ? 288 : 128)));
   uint32_t threads = kb == 64 ? 256 : 512;
-  uint32_t gx = (N + 15) / 16;
+  // wide outputs: two column tiles per wave halve the workgroup count
+  bool c2 = M == 1 && (kb == 96 || kb == 128) && N >= 16384;
+  uint32_t gx = c2 ? (N + 31) / 32 : (N + 15) / 16;
   uint32_t ksplit = (G + kb - 1) / kb;
   if (ksplit > 1) {
     if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
     if (ensure_counters(c, gx)) return -1;
   }
   char name[64];
-  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u", tag, M, kb);
+  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s", tag, M, kb, c2 ? "_c2" : "");
   const float* pa = a;
   const void* pB = B;
   const void* pD = D;
@@ -898,6 +902,81 @@ int smith_linear_q4_0(void* ctx, const float* x, const void* nib, const void* d,
   return qmatmul(c, FQ40, x, nib, d, out, M, N, K, K / 32, e);
 }
 
+int smith_repack_q4_0_t_into(void* ctx, const void* blocks, void* nib, void* d, uint32_t N, uint32_t K,
+                             uint32_t n_off, uint32_t n_stride, uint32_t N_total) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_repack_q4_0_t_into: K %u is not a multiple of 32", K);
+  if (N_total % 16) return fail(c, "smith_repack_q4_0_t_into: N_total %u is not a multiple of 16", N_total);
+  if ((uint64_t)n_off + (uint64_t)(N ? N - 1 : 0) * n_stride >= N_total && N)
+    return fail(c, "smith_repack_q4_0_t_into: columns exceed N_total=%u", N_total);
+  if (set_device(c)) return -1;
+  uint32_t G = K / 32;
+  uint64_t total = (uint64_t)N * G;
+  if (!total) return 0;
+  uint32_t pN = N, pG = G, po = n_off, ps = n_stride;
+  void* args[] = {&blocks, &nib, &d, &pN, &pG, &po, &ps};
+  return launch(c, "smith_repack_q4_0_tiles", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_linear_q4_0_t(void* ctx, const float* x, const void* nib, const void* d, float* out, uint32_t M,
+                        uint32_t N, uint32_t K, const float* norm_gamma, float eps, const float* resid,
+                        uint32_t epilogue) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (K % 32) return fail(c, "smith_linear_q4_0_t: K %u is not a multiple of 32", K);
+  if (N % 16) return fail(c, "smith_linear_q4_0_t: N %u is not a multiple of 16", N);
+  if (epilogue > 2) return fail(c, "smith_linear_q4_0_t: unknown epilogue %u", epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q4_0_t: residual epilogue without a residual buffer");
+  Epi e;
+  e.gamma = norm_gamma;
+  e.eps = eps;
+  e.resid = epilogue == 1 ? resid : nullptr;
+  e.mode = epilogue;
+  return qmatmul(c, FQ40T, x, nib, d, out, M, N, K, K / 32, e);
+}
+
+int smith_linear_q4_0_t_act(void* ctx, const void* act_in, int norm, float eps, const void* nib, const void* d,
+                            float* out, uint32_t N, uint32_t K, const float* resid, uint32_t epilogue,
+                            void* act_out, const float* gamma_out) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!act_in) return fail(c, "smith_linear_q4_0_t_act: no input act");
+  if (K % 32 || !K) return fail(c, "smith_linear_q4_0_t_act: K %u is not a positive multiple of 32", K);
+  if (N % 16 || !N) return fail(c, "smith_linear_q4_0_t_act: N %u is not a positive multiple of 16", N);
+  if (epilogue > 2) return fail(c, "smith_linear_q4_0_t_act: unknown epilogue %u", epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q4_0_t_act: residual epilogue without a residual buffer");
+  const uint32_t nout = epilogue == 2 ? N / 2 : N;
+  if (act_out && nout % 32) return fail(c, "smith_linear_q4_0_t_act: act output needs %u %% 32 == 0", nout);
+  if (set_device(c)) return -1;
+  // smallest block K coverage that holds all K groups (no split), else 288
+  // groups per block and a K split across blocks
+  static const uint32_t kbs[] = {32, 48, 64, 72, 96, 128, 144, 192, 288};
+  const uint32_t G = K / 32;
+  uint32_t kb = 288;
+  for (uint32_t v : kbs)
+    if (v >= G) {
+      kb = v;
+      break;
+    }
+  const uint32_t ksplit = (G + kb - 1) / kb;
+  const uint32_t threads = kb == 32 || kb == 48 || kb == 64 ? 256 : (kb == 72 ? 384 : (kb == 144 ? 768 : 512));
+  const uint32_t gx = N / 16;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_agemv_q40t_k%u", kb);
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pN = N, pK = K, pnorm = norm ? 1u : 0u, pepi = epilogue;
+  const float* pR = epilogue == 1 ? resid : nullptr;
+  void* args[] = {&act_in, &nib, &d, &out, &pN, &pK, &pnorm, &eps, &pR, &pepi, &act_out, &gamma_out, &pws, &pcnt};
+  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
+}
+
 int smith_linear_q8(void* ctx, const float* x, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
                     const float* norm_gamma, float eps, const float* resid, uint32_t epilogue) {
   Ctx* c = (Ctx*)ctx;
@@ -922,20 +1001,25 @@ int smith_rmsnorm(void* ctx, const float* x, const float* gamma, float* out, uin
   return launch(c, "smith_rmsnorm_rows", dim3(rows), dim3(256), args);
 }
 
-int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, uint32_t rows, uint32_t dim) {
+int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, uint32_t rows, uint32_t dim,
+                void* act_out, const float* gamma_out) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
+  if (act_out && (rows != 1 || dim % 32))
+    return fail(c, "smith_embed: an act output needs one row and dim %% 32 == 0 (rows %u, dim %u)", rows, dim);
   if (set_device(c)) return -1;
   if (!rows) return 0;
-  void* args[] = {&E, &tokens, &out, &rows, &dim};
+  void* args[] = {&E, &tokens, &out, &rows, &dim, &act_out, &gamma_out};
   return launch(c, "smith_embed_rows", dim3(rows), dim3(256), args);
 }
 
 int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
                     uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
-                    float* kcache, float* vcache, uint32_t max_seq, float* out) {
+                    float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
+  if (act_out && (S != 1 || head_dim % 8 || (n_heads * head_dim) % 32))
+    return fail(c, "smith_attention: an act output needs one row, head_dim %% 8 == 0 and heads*head_dim %% 32 == 0");
   if (!n_kv_heads || n_heads % n_kv_heads)
     return fail(c, "smith_attention: %u heads not a multiple of %u kv heads", n_heads, n_kv_heads);
   if (head_dim > 128 || head_dim % 4) return fail(c, "smith_attention: head_dim %u unsupported (<= 128, % 4)", head_dim);
@@ -958,7 +1042,7 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   void* pws = c->att_ws;
   uint32_t* pcnt = c->att_cnt;
   void* args[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
-                  &kcache, &vcache, &max_seq, &out, &pws, &pcnt};
+                  &kcache, &vcache, &max_seq, &out, &pws, &pcnt, &act_out};
   return launch(c, "smith_attention", dim3(n_heads, S, nsplit), dim3(256), args);
 }
 
@@ -994,11 +1078,12 @@ int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps
 }
 
 int smith_argmax_embed(void* ctx, const float* logits, uint32_t N, const float* E, uint32_t dim, float* x,
-                       int32_t* tokens, int32_t* count, int32_t* pos) {
+                       int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
+  if (act_out && dim % 32) return fail(c, "smith_argmax_embed: an act output needs dim %% 32 == 0 (dim %u)", dim);
   if (set_device(c)) return -1;
-  void* args[] = {&logits, &N, &E, &dim, &x, &tokens, &count, &pos};
+  void* args[] = {&logits, &N, &E, &dim, &x, &tokens, &count, &pos, &act_out, &gamma_out};
   return launch(c, "smith_argmax_embed", dim3(1), dim3(1024), args);
 }
 

@@ -16,7 +16,7 @@
 //
 // Decode GEMV (M <= 32) -- the HBM-bound hot path -- on
 // v_mfma_f32_16x16x32_f16 with EXACT weights: nibbles / int8 become f16
-// integers plus a known per-slot offset with one v_and_or_b32 (or v_perm_b32)
+// integers plus a known per-slot offset with one v_bfi_b32 (or v_perm_b32)
 // per pair, using exponent-bias magic numbers (0x6400 -> 1024+q for a low
 // nibble, 0x5400 -> 64+q for a high nibble, 1024+(q+128) for int8).
 // Activations are split into f16 hi + f16 lo*2048 ("hi/lo", M <= 8) so the
@@ -26,12 +26,18 @@
 // S = sum(a), accumulated in f32; scale and zero never touch the f16 path.
 //   smith_qgemv1_*  M <= 2: activation prep fused (LDS), one kernel per call
 //   smith_qgemv3_*  M >  2: activations prepared once by smith_qprep_*
+//   smith_agemv_*   M == 1 on an act (act_frag.h) its producer wrote
+// Q4_0 weights for the decode path use tile-major planes (FMT_Q40T): the 16
+// columns of a tile are contiguous over all of K, so a wave's records sit at
+// fixed offsets from one base address.
 // Split-K across workgroups (only when a block does not cover K) is reduced
 // deterministically: partials go to a workspace through agent-scope atomic
 // RMWs and the last-arriving workgroup of each column block sums them in
 // fixed order (the counter self-resets).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "act_frag.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -40,6 +46,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #define FMT_Q4S 0
 #define FMT_Q8 1
 #define FMT_Q40 2
+#define FMT_Q40T 3  // Q4_0 planes in column-tile-major order (16-column tiles)
+__host__ __device__ constexpr bool is_q40(int f) { return f == FMT_Q40 || f == FMT_Q40T; }
 
 // ---------------------------------------------------------------------------
 // Reference-semantics kernels (one thread per output element).  They take the
@@ -246,6 +254,27 @@ extern "C" __global__ void smith_repack_q4_0_cols(const uint8_t* __restrict__ sr
   }
 }
 
+// Same, into the tile-major planes of FMT_Q40T: column col = n_off +
+// n*n_stride of tile t = col/16 has record (g, col) at ((t*G + g)*16 + col%16)
+// (16 nibble bytes each, f16 scale at the same index of dsc), so one 16-column
+// tile is G*256 contiguous nibble bytes.
+extern "C" __global__ void smith_repack_q4_0_tiles(const uint8_t* __restrict__ src, uint8_t* __restrict__ nib,
+                                                   uint16_t* __restrict__ dsc, uint32_t N, uint32_t G,
+                                                   uint32_t n_off, uint32_t n_stride) {
+  size_t total = (size_t)N * G;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    uint32_t n = (uint32_t)(idx / G), g = (uint32_t)(idx % G);
+    const uint16_t* s = (const uint16_t*)(src + idx * 18);
+    const uint32_t col = n_off + n * n_stride;
+    size_t o = ((size_t)(col >> 4) * G + g) * 16 + (col & 15);
+    dsc[o] = s[0];
+    uint16_t* dn = (uint16_t*)(nib + o * 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) dn[i] = s[1 + i];
+  }
+}
+
 // GGUF Q8_0 blocks of a weight listed [out=N][in=K] into matmulQ8's record
 // order (shaders/matmul_q8.metal:40-52): record (g, col) at (g*Nt+col)*34,
 // col = n_off + n*n_stride.  34-byte blocks, moved unchanged.
@@ -333,7 +362,7 @@ __device__ __forceinline__ void qprep_body(const float* __restrict__ A, u32x4* _
   hp.z = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[4], hv[5]});
   hp.w = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[6], hv[7]});
   frag[fbase + r + 16 * kq] = hp;
-  float fold = FMT == FMT_Q40 ? 8.0f : 0.0f;
+  float fold = is_q40(FMT) ? 8.0f : 0.0f;
   if (kq == 0) cst[cbase + r] = make_float2(__builtin_fmaf(fold, hi_s, hi_c1), hi_s);
   if (HILO) {
     u32x4 lp;
@@ -456,6 +485,12 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
     float2 sz = *(const float2*)(p + 16);
     r.s = sz.x;
     r.z = sz.y;
+  } else if (FMT == FMT_Q40T) {
+    // tile-major: the 16 columns of a tile, group after group, contiguous
+    uint32_t nn = n < N ? n : N - 1, gg = g < G ? g : G - 1;
+    rec = ((size_t)(nn >> 4) * G + gg) * 16 + (nn & 15);
+    r.q = *(const u32x4*)(B + rec * 16);
+    r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
   } else if (FMT == FMT_Q40) {
     r.q = *(const u32x4*)(B + rec * 16);
     r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
@@ -474,6 +509,15 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
   return r;
 }
 
+// (x & mask) | (base & ~mask) in one v_bfi_b32: the and/or pair the compiler
+// would emit costs two VALU slots per converted dword (VOP3 takes no literal,
+// so the mask goes in an SGPR and the base in a VGPR, both loop invariant).
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t base) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(base));
+  return r;
+}
+
 // B operand of MFMA i (K elements 8i..8i+7 of the record).
 template <int FMT>
 __device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
@@ -489,10 +533,10 @@ __device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
   } else {
     uint32_t x = i == 0 ? r.q.x : (i == 1 ? r.q.y : (i == 2 ? r.q.z : r.q.w));
     uint32_t y = x >> 8;
-    u.x = (x & 0x000F000Fu) | 0x64006400u;
-    u.y = (x & 0x00F000F0u) | 0x54005400u;
-    u.z = (y & 0x000F000Fu) | 0x64006400u;
-    u.w = (y & 0x00F000F0u) | 0x54005400u;
+    u.x = bfi(0x000F000Fu, x, 0x64006400u);
+    u.y = bfi(0x00F000F0u, x, 0x54005400u);
+    u.z = bfi(0x000F000Fu, y, 0x64006400u);
+    u.w = bfi(0x00F000F0u, y, 0x54005400u);
   }
   return __builtin_bit_cast(half8, u);
 }
@@ -510,7 +554,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   constexpr int NT = 64 * WK * WN;     // threads
   constexpr int NCH = KB * MR * 4;     // prep chunks: (group, row, mfma slice)
   constexpr int CPT = (NCH + NT - 1) / NT;
-  __shared__ u32x4 fragL[KB][2 * MR][4];  // [group][row u][mfma i]
+  __shared__ u32x4 fragL[KB][2 * MR + 1][4];  // [group][row u][mfma i]; row 2*MR stays zero
   __shared__ float2 cL[KB][MR];           // (C1, S) with hi + lo/2048 folded
   __shared__ float red[WK][MR][BC];
   __shared__ float nred[MR][WK * WN];
@@ -527,10 +571,27 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 
   // 1. weights first: every record of this wave, all loads in flight
   Rec<FMT> wr[S][CT];
+  if (FMT == FMT_Q40T && n0 + 16 * CT <= N && gw + 4 * S <= G) {
+    // interior wave of the tile-major layout: one base address, the records
+    // of step st / tile ct at fixed offsets (1 KB per step of 4 groups)
+    const size_t rec0 = ((size_t)(n0 >> 4) * G + gw + j) * 16 + c;
+    const uint8_t* pb = B + rec0 * 16;
+    const uint16_t* pd = D + rec0;
 #pragma unroll
-  for (int st = 0; st < S; st++)
+    for (int st = 0; st < S; st++)
 #pragma unroll
-    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+      for (int ct = 0; ct < CT; ct++) {
+        wr[st][ct].q = *(const u32x4*)(pb + (size_t)ct * G * 256 + st * 1024);
+        wr[st][ct].s = (float)__builtin_bit_cast(_Float16, pd[(size_t)ct * G * 16 + st * 64]);
+        wr[st][ct].z = 0.f;
+        wr[st][ct].sh = 0;
+      }
+  } else {
+#pragma unroll
+    for (int st = 0; st < S; st++)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+  }
 
   // 2. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
   //    that consumes it): every workgroup sums x^2 over its rows' full K
@@ -590,6 +651,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   }
 
   // 4. activations -> f16 hi/lo fragments + (C1, S) in LDS
+  for (uint32_t e = threadIdx.x; e < (uint32_t)KB * 4; e += NT) fragL[e >> 2][2 * MR][e & 3] = (u32x4){0u, 0u, 0u, 0u};
   float rms[MR];
   if (gamma) {
 #pragma unroll
@@ -646,7 +708,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     sm += __shfl_xor(sm, 1);
     c1 += __shfl_xor(c1, 2);
     sm += __shfl_xor(sm, 2);
-    if (FMT == FMT_Q40) c1 = __builtin_fmaf(8.0f, sm, c1);
+    if (is_q40(FMT)) c1 = __builtin_fmaf(8.0f, sm, c1);
     if (ch < (uint32_t)NCH) {
       u32x4 hp, lp;
 #pragma unroll
@@ -664,7 +726,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   // 5. MFMAs: lane (r = lane%16, j) feeds A row r from K slice j only
   const uint32_t r = lane & 15;
   const bool a_active = (r >> 2) == j && (r & 3) < 2 * MR;
-  const uint32_t ru = a_active ? (r & 3) : 0;
+  const uint32_t ru = a_active ? (r & 3) : 2 * MR;  // inactive rows read the zero row
   float acc[CT][MR];
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
@@ -675,10 +737,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     const uint32_t gl = wk * GPW + 4 * st + j;
     half8 af[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      u32x4 v = fragL[gl][ru][i];
-      af[i] = __builtin_bit_cast(half8, a_active ? v : (u32x4){0u, 0u, 0u, 0u});
-    }
+    for (int i = 0; i < 4; i++) af[i] = __builtin_bit_cast(half8, fragL[gl][ru][i]);
     float2 cv[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) cv[m] = cL[gl][m];
@@ -944,12 +1003,14 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 
 // Fused M <= 2 variants, named by the groups one block covers: k64 = 4 waves
 // x 4 steps, k96 / k128 / k288 = 8 waves x 3 / 4 / 9 steps (K = 3072, 4096,
-// 9216 in one block).
+// 9216 in one block); _c2: two 16-column tiles per wave (wide N).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96, FMT, 1, 1, 8, 1, 3)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288, FMT, 1, 1, 8, 1, 9)            \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2, FMT, 1, 2, 8, 1, 3)          \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2, FMT, 1, 2, 8, 1, 4)         \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k128, FMT, 2, 1, 8, 1, 4)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k96, FMT, 2, 1, 8, 1, 3)             \
@@ -963,13 +1024,239 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   DEF_QGEMV3(smith_qgemv3_##TAG##_m16, FMT, 1, false, 4, 2, 1, 8, 1)      \
   DEF_QGEMV3(smith_qgemv3_##TAG##_m32, FMT, 2, false, 4, 2, 1, 8, 1)
 
+
+// ---------------------------------------------------------------------------
+// Single-row decode GEMV on a prepared activation (act_frag.h) and Q4_0
+// weights in tile-major order (FMT_Q40T).  Same MFMA scheme as qgemv1 with
+// the activation side reduced to loads: lane (r, j) of a wave feeds A row r
+// (r = 4j: hi, 4j+1: lo of group g+j; other rows zero) straight from the act
+// buffer, and (C1) of its group from the act's tile sums.  With `norm` the
+// result is scaled by rms = 1/sqrt(mean(v^2) + eps) from the act's sums of
+// squares (an RMSNorm on the input, gguf_cache.js:121,167).  A block covers
+// the whole K (4*S*WK groups >= K/32), so no cross-block reduction.
+// Wave 0 finishes its BC columns: sum of the WK partials, rms, epilogue
+// (store / residual / SwiGLU), the f32 store (C may be null) and, with
+// act_out, the act of the produced vector for the next projection.
+// ---------------------------------------------------------------------------
+template <int CT, int S, int WK>
+__device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, const uint8_t* __restrict__ B,
+                                           const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t N,
+                                           uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,
+                                           uint32_t epi, uint8_t* __restrict__ act_out,
+                                           const float* __restrict__ gamma_out, float* __restrict__ ws,
+                                           uint32_t* __restrict__ counters) {
+  constexpr int GPW = 4 * S;
+  constexpr int BC = 16 * CT;
+  constexpr int GMAX = 4 * S * WK;
+  __shared__ u32x4 fragL[8 * GMAX + 4];  // [g][hi/lo][slice] + one zero fragment
+  __shared__ float red[WK][BC];
+  const uint32_t G = K / 32, T = K / 8;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t c = lane & 15, j = lane >> 4;
+  const uint32_t n0 = blockIdx.x * BC;
+  const uint32_t ksplit = gridDim.y;
+  const uint32_t gb = blockIdx.y * GMAX;  // first group of this block
+  const uint32_t gw = gb + wk * GPW;
+
+  // 1. activation fragments: the act's frag words copied to LDS as they are
+  //    (no conversion), group sums C1 from the act's tile sums
+  const uint32_t r = lane & 15;
+  const bool a_active = (r >> 2) == j && (r & 3) < 2;
+  const u32x4* frag = (const u32x4*)act;
+  const float* c1p = (const float*)(act + (size_t)K * 4);
+  constexpr int NT = 64 * WK;
+  constexpr int CPT = (8 * GMAX + NT - 1) / NT;   // frag words per thread (this block's groups)
+  constexpr int SPL = (4 * GMAX + 63) / 64;       // part sums of squares per lane
+  u32x4 fv[CPT];
+#pragma unroll
+  for (int q = 0; q < CPT; q++) {
+    const uint32_t e = 8 * gb + threadIdx.x + q * NT;
+    fv[q] = frag[e < 8 * G ? e : 8 * G - 1];  // clamped: branch-free issue
+  }
+  float c1[S];
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const uint32_t g = gw + 4 * st + j;
+    const uint32_t gc = g < G ? g : G - 1;
+    const float4 cc = *(const float4*)(c1p + 4 * gc);
+    c1[st] = (cc.x + cc.y) + (cc.z + cc.w);
+  }
+  // sums of squares for the RMSNorm (one block covers K; with a K split the
+  // finishing block reads them at the end)
+  float ssv[SPL];
+#pragma unroll
+  for (int q = 0; q < SPL; q++) {
+    const uint32_t t = lane + 64 * q;
+    ssv[q] = c1p[2 * T + (t < T ? t : T - 1)];
+  }
+  // epilogue operands of wave 0 (residual, next norm's gamma), loaded now so
+  // the tail after the reduction has no global load in its dependency chain
+  float rv = 0.f, gv = 1.f;
+  if (wk == 0) {
+    const uint32_t n = n0 + (lane < BC ? lane : 0);
+    if (epi == EPI_RESID) rv = R[n < N ? n : N - 1];
+    if (act_out && gamma_out) {
+      const uint32_t no = epi == EPI_SWIGLU ? N / 2 : N;
+      const uint32_t o = (epi == EPI_SWIGLU ? n0 / 2 : n0) + (lane & 31);
+      gv = gamma_out[o < no ? o : no - 1];
+    }
+  }
+  // 2. weights (after the small act loads: loads complete in order), then the
+  //    LDS copy is published
+  // one clamped base per wave; records at fixed offsets (1 KB per step of 4
+  // groups, G*256 bytes per tile).  Out-of-range records (ragged N or K) are
+  // read clamped and get scale 0.
+  u32x4 wq[S][CT];
+  uint16_t wd[S][CT];
+  {
+    const uint32_t nt = n0 >> 4, ntl = (N - 1) >> 4;
+#pragma unroll
+    for (int st = 0; st < S; st++)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const uint32_t g = gw + 4 * st + j, t = nt + ct;
+        const size_t rec = ((size_t)(t < ntl ? t : ntl) * G + (g < G ? g : G - 1)) * 16 + c;
+        wq[st][ct] = *(const u32x4*)(B + rec * 16);
+        wd[st][ct] = D[rec];
+      }
+  }
+#pragma unroll
+  for (int q = 0; q < CPT; q++) {
+    const uint32_t e = threadIdx.x + q * NT;
+    if (e < 8 * GMAX) fragL[e] = fv[q];
+  }
+  if (threadIdx.x < 4) fragL[8 * GMAX + threadIdx.x] = (u32x4){0u, 0u, 0u, 0u};
+  float ssum = 0.f;
+  if (ksplit == 1)
+#pragma unroll
+    for (int q = 0; q < SPL; q++) ssum += lane + 64 * q < T ? ssv[q] : 0.f;
+  __syncthreads();
+
+  // 3. MFMAs and the exact per-group post-step (inactive lanes read zeros)
+  uint32_t abase[S];
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const uint32_t g = gw + 4 * st + j;
+    abase[st] = a_active && g < G ? ((g - gb) * 2 + (r & 3)) * 4 : 8 * GMAX;
+  }
+  float acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++) acc[ct] = 0.f;
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
+      Rec<FMT_Q40T> rr;
+      rr.q = wq[st][ct];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fragL[abase[st] + i]),
+                                                   rec_to_f16<FMT_Q40T>(rr, i), p, 0, 0, 0);
+      const uint32_t g = gw + 4 * st + j, n = n0 + 16 * ct + c;
+      const float sc = g < G && n < N ? (float)__builtin_bit_cast(_Float16, wd[st][ct]) : 0.f;
+      const float t = __builtin_fmaf(p[1], 1.0f / 2048.0f, p[0]) - c1[st];
+      acc[ct] = __builtin_fmaf(sc, t, acc[ct]);
+    }
+  }
+
+  // 4. lane groups (K groups g+j), then the WK waves in fixed order
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++) {
+    float v = acc[ct];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (j == 0) red[wk][ct * 16 + c] = v;
+  }
+  __syncthreads();
+  if (wk != 0) return;
+  // wave 0: block partial of column n0 + lane (lane < BC)
+  float v = 0.f;
+  if (lane < BC) {
+#pragma unroll
+    for (int w = 0; w < WK; w++) v += red[w][lane];
+  }
+  if (ksplit > 1) {
+    // deterministic split-K: partials through agent-scope atomics, the last
+    // block of the column block sums them in split order (counter self-resets)
+    if (lane < BC && n0 + lane < N)
+      __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n0 + lane, __float_as_uint(v),
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev != ksplit - 1) return;
+    v = 0.f;
+    if (lane < BC && n0 + lane < N)
+      for (uint32_t sp = 0; sp < ksplit; sp++)
+        v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n0 + lane, 0u,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (lane == 0) __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (norm)
+      for (uint32_t t = lane; t < T; t += 64) ssum += c1p[2 * T + t];
+  }
+  float rms = 1.0f;
+  if (norm) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) ssum += __shfl_xor(ssum, d);
+    rms = 1.0f / __builtin_sqrtf(ssum / (float)K + eps);
+  }
+  v *= rms;
+  if (epi == EPI_SWIGLU) {
+    // lane o < BC/2 takes the interleaved (gate, up) pair of columns 2o, 2o+1
+    const float g = __shfl(v, (int)(2 * (lane & 31))), u = __shfl(v, (int)(2 * (lane & 31) + 1));
+    if (lane < BC / 2) {
+      const uint32_t o = n0 / 2 + lane;
+      const bool in = n0 + 2 * lane < N;
+      const float y = silu_mul(g, u);
+      if (C && in) C[o] = y;
+      if (act_out) act_emit8(act_out, N / 2, o, in ? y : 0.f, gv);
+    }
+  } else if (lane < BC) {
+    const uint32_t n = n0 + lane;
+    const bool in = n < N;
+    if (epi == EPI_RESID) v += rv;
+    if (C && in) C[n] = v;
+    if (act_out) act_emit8(act_out, N, n, in ? v : 0.f, gv);
+  }
+}
+
+#define DEF_AGEMV(NAME, CT, S, WK)                                                                           \
+  extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                                \
+      const uint8_t* __restrict__ act, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,        \
+      float* __restrict__ C, uint32_t N, uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,   \
+      uint32_t epi, uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out, float* __restrict__ ws, \
+      uint32_t* __restrict__ counters) {                                                                     \
+    agemv_body<CT, S, WK>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters);          \
+  }
+
+// named by the groups one block covers (4*S*WK) and the column tiles per wave;
+// a K longer than one block is split over gridDim.y blocks
+DEF_AGEMV(smith_agemv_q40t_k32, 1, 2, 4)
+DEF_AGEMV(smith_agemv_q40t_k48, 1, 3, 4)
+DEF_AGEMV(smith_agemv_q40t_k64, 1, 4, 4)
+DEF_AGEMV(smith_agemv_q40t_k72, 1, 3, 6)
+DEF_AGEMV(smith_agemv_q40t_k96, 1, 3, 8)
+DEF_AGEMV(smith_agemv_q40t_k128, 1, 4, 8)
+DEF_AGEMV(smith_agemv_q40t_k144, 1, 3, 12)
+DEF_AGEMV(smith_agemv_q40t_k192, 1, 6, 8)
+DEF_AGEMV(smith_agemv_q40t_k288, 1, 9, 8)
+DEF_AGEMV(smith_agemv_q40t_k96_c2, 2, 3, 8)
+DEF_AGEMV(smith_agemv_q40t_k128_c2, 2, 4, 8)
+DEF_AGEMV(smith_agemv_q40t_k144_c2, 2, 3, 12)
+
 #ifndef SMITH_NO_INSTANCES
 DEF_QGEMV3_FMT(q4s, FMT_Q4S)
 DEF_QGEMV3_FMT(q8, FMT_Q8)
 DEF_QGEMV3_FMT(q40, FMT_Q40)
+DEF_QGEMV3_FMT(q40t, FMT_Q40T)
 DEF_QGEMV1_FMT(q4s, FMT_Q4S)
 DEF_QGEMV1_FMT(q8, FMT_Q8)
 DEF_QGEMV1_FMT(q40, FMT_Q40)
+DEF_QGEMV1_FMT(q40t, FMT_Q40T)
 #endif
 
 // Zero fill (used instead of hipMemsetAsync so the op stays a plain kernel).

@@ -11,6 +11,13 @@ then the LM head (final RMSNorm fused) and a device-side greedy step
 (argmax, embedding of the chosen token, position advance).  The position
 lives in device memory, so the greedy decode step is captured once as a HIP
 graph and replayed.
+
+Single-row steps on Q4_0 models pass activations between kernels as "acts"
+(the vector already in the GEMV's MFMA operand form, with per-8-element sums
+and sums of squares; smith_linear_q4_0_t_act): every producer -- embedding,
+attention, o-proj, gate|up, down -- writes the act its consumer reads, with
+the next RMSNorm's gamma folded in, and the consumer applies the norm's rms
+as one scalar.  Prefill rows (M > 1) take the f32 path.
 """
 import os
 
@@ -66,12 +73,23 @@ class _Engine:
         self.tok_in = DeviceArray((R,), np.int32)
         self.graph = None
         self.graph_caches = None
+        hd = cfg["headDim"]
+        self.use_act = (all(b[k].kind == "q4_0t" for b in model["blocks"] for k in ("qkv", "outProj", "gateUp",
+                                                                                   "ffnDown"))
+                        and dim % 32 == 0 and ffn % 32 == 0 and hd % 8 == 0 and cfg["numHeads"] * hd == dim)
+
+        def act(K):
+            return DeviceArray((K * 4 + K // 8 * 12,), np.uint8)
+        if self.use_act:
+            self.act_x, self.act_a, self.act_x2, self.act_h = act(dim), act(dim), act(dim), act(ffn)
 
     def set_pos(self, p):
         device.check(device.lib.smith_set_i32(device.ops_ctx(), self.pos.ptr, int(p)), "set_pos")
 
     def layers(self, model, caches, M):
         """Run every layer on rows x[0:M] at positions *pos .. *pos+M-1."""
+        if M == 1 and self.use_act:
+            return self.layers_act(model, caches)
         cfg, ctx, eps = self.cfg, device.ops_ctx(), model["normEps"]
         dim = cfg["dim"]
         x, x2, qkv, attn, h = self.x.ptr, self.x2.ptr, self.qkv.ptr, self.attn.ptr, self.h.ptr
@@ -80,12 +98,38 @@ class _Engine:
             blk["qkv"](x, qkv, M, gamma=blk["ln1Gamma"].ptr, eps=eps)
             device.check(device.lib.smith_attention(
                 ctx, qkv, self.qkv_ld, self.pos.ptr, M, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
-                rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn),
+                rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, None),
                 "attention")
             blk["outProj"](attn, x2, M, resid=x, epilogue=1)
             blk["gateUp"](x2, h, M, gamma=blk["ln2Gamma"].ptr, eps=eps, epilogue=2)
             blk["ffnDown"](h, x, M, resid=x2, epilogue=1)
         del dim
+
+    def layers_act(self, model, caches):
+        """One row through every layer on acts; needs self.act_x written (with
+        layer 0's attention-norm gamma) by the embedding of the row."""
+        cfg, ctx, eps = self.cfg, device.ops_ctx(), model["normEps"]
+        x, x2, qkv, attn = self.x.ptr, self.x2.ptr, self.qkv.ptr, self.attn.ptr
+        ax, aa, ax2, ah = self.act_x.ptr, self.act_a.ptr, self.act_x2.ptr, self.act_h.ptr
+        rope = model["rope"]
+        blocks = model["blocks"]
+        for li, (blk, cache) in enumerate(zip(blocks, caches)):
+            blk["qkv"].act(ax, True, eps, qkv)
+            device.check(device.lib.smith_attention(
+                ctx, qkv, self.qkv_ld, self.pos.ptr, 1, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
+                rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, aa),
+                "attention")
+            blk["outProj"].act(aa, False, 0.0, x2, resid=x, epilogue=1, act_out=ax2, gamma_out=blk["ln2Gamma"].ptr)
+            blk["gateUp"].act(ax2, True, eps, None, epilogue=2, act_out=ah)
+            last = li + 1 == len(blocks)
+            blk["ffnDown"].act(ah, False, 0.0, x, resid=x2, epilogue=1, act_out=None if last else ax,
+                               gamma_out=None if last else blocks[li + 1]["ln1Gamma"].ptr)
+
+    def _act0(self, model):
+        """(act, gamma) the embedding of a single decode row writes."""
+        if not self.use_act:
+            return None, None
+        return self.act_x.ptr, model["blocks"][0]["ln1Gamma"].ptr
 
     def lm_head(self, model, x_ptr):
         """Final RMSNorm fused into the LM head (gguf_cache.js:174-184)."""
@@ -102,17 +146,19 @@ class _Engine:
                                            cfg["vocabSize"], 1)
         device.check(rc, "lm head")
 
-    def greedy_step(self):
+    def greedy_step(self, model):
         cfg = self.cfg
+        a0, g0 = self._act0(model)
         device.check(device.lib.smith_argmax_embed(device.ops_ctx(), self.logits.ptr, cfg["vocabSize"],
                                                    self.model_embedding, cfg["dim"], self.x.ptr, self.tokens.ptr,
-                                                   self.count.ptr, self.pos.ptr), "argmax")
+                                                   self.count.ptr, self.pos.ptr, a0, g0), "argmax")
 
     def embed(self, model, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         device.upload(self.tok_in.ptr, t)
+        a0, g0 = self._act0(model) if len(t) == 1 else (None, None)
         device.check(device.lib.smith_embed(device.ops_ctx(), model["embedding"].ptr, self.tok_in.ptr, self.x.ptr,
-                                            len(t), self.cfg["dim"]), "embed")
+                                            len(t), self.cfg["dim"], a0, g0), "embed")
 
     def prefill(self, model, tokens, caches, all_logits=False):
         """Prompt rows in chunks of <= 256 (attention keeps a chunk's keys in
@@ -238,7 +284,7 @@ def generateGGUF(model, promptIds, config=None, callbacks=None):
     if greedy:
         device.check(device.lib.smith_set_i32(device.ops_ctx(), e.count.ptr, 0), "count")
         e.set_pos(n - 1)
-        e.greedy_step()  # token 1; pos -> n; x = E[token]
+        e.greedy_step(model)  # token 1; pos -> n; x = E[token]
         steps = 0
         for i in range(1, cfg["maxTokens"]):
             if n + i - 1 >= mcfg["maxSeqLen"]:
@@ -261,7 +307,7 @@ def generateGGUF(model, promptIds, config=None, callbacks=None):
             else:
                 e.layers(model, caches, 1)
                 e.lm_head(model, e.x.ptr)
-                e.greedy_step()
+                e.greedy_step(model)
             if sync_each:
                 tok = int(e.tokens.numpy()[i])
                 generated.append(tok)
@@ -309,7 +355,7 @@ def _decode_graph(model, e, caches):
     try:
         e.layers(model, caches, 1)
         e.lm_head(model, e.x.ptr)
-        e.greedy_step()
+        e.greedy_step(model)
     finally:
         g = device.lib.smith_graph_end(ctx)
     if not g:

@@ -1,6 +1,6 @@
 """loadGGUF on MI355X -- mirror of src/gguf_loader.js for the Llama path.
 
-Differences from the reference, all on purpose (SURVEY.md finding 3): the
+Differences from the reference, all on purpose: the
 reference dequantizes every tensor to f32 at load (gguf_loader.js:236) and
 runs f32 GEMMs; here Q4_0 / Q8_0 linear weights stay quantized on the device
 and `linear` runs the quantized GEMV.  The blocks are only moved (never
@@ -86,20 +86,27 @@ class DeviceArray:
 
 class QLinear:
     """A quantized linear weight on the device: y = x . W with W [in=K, out=N].
-    kind 'q4_0': planes nib/d; kind 'q8': matmulQ8 records."""
+    kind 'q4_0t': tile-major nib/d planes; kind 'q8': matmulQ8 records."""
 
     def __init__(self, kind, K, N, a, b=None):
         self.kind, self.K, self.N, self.a, self.b = kind, K, N, a, b
 
     def __call__(self, x_ptr, out_ptr, M, gamma=None, eps=0.0, resid=None, epilogue=0):
         ctx = device.ops_ctx()
-        if self.kind == "q4_0":
-            rc = device.lib.smith_linear_q4_0(ctx, x_ptr, self.a.ptr, self.b.ptr, out_ptr, M, self.N, self.K,
-                                              gamma, eps, resid, epilogue)
+        if self.kind == "q4_0t":
+            rc = device.lib.smith_linear_q4_0_t(ctx, x_ptr, self.a.ptr, self.b.ptr, out_ptr, M, self.N, self.K,
+                                                gamma, eps, resid, epilogue)
         else:
             rc = device.lib.smith_linear_q8(ctx, x_ptr, self.a.ptr, out_ptr, M, self.N, self.K, gamma, eps,
                                             resid, epilogue)
         device.check(rc, "linear")
+
+    def act(self, act_in, norm, eps, out_ptr, resid=None, epilogue=0, act_out=None, gamma_out=None):
+        """Single-row linear on a prepared activation (smith_linear_q4_0_t_act)."""
+        rc = device.lib.smith_linear_q4_0_t_act(device.ops_ctx(), act_in, 1 if norm else 0, eps, self.a.ptr,
+                                                self.b.ptr, out_ptr, self.N, self.K, resid, epilogue, act_out,
+                                                gamma_out)
+        device.check(rc, "linear (act)")
 
 
 def _pack_group(parsed, infos, K, cols, interleave):
@@ -115,7 +122,7 @@ def _pack_group(parsed, infos, K, cols, interleave):
     if t == G.GGML_TYPE["Q4_0"]:
         nib = DeviceArray((Gk * Ntot * 16,), np.uint8)
         dsc = DeviceArray((Gk * Ntot,), np.uint16)
-        kind = "q4_0"
+        kind = "q4_0t"
     elif t == G.GGML_TYPE["Q8_0"]:
         nib = DeviceArray((Gk * Ntot * 34,), np.uint8)
         dsc = None
@@ -128,8 +135,8 @@ def _pack_group(parsed, infos, K, cols, interleave):
         raw = G.readTensorData(parsed, info)
         src = DeviceArray.from_host(np.asarray(raw), np.uint8)
         n_off, stride = (j, len(infos)) if interleave else (off, 1)
-        if kind == "q4_0":
-            rc = device.lib.smith_repack_q4_0_into(ctx, src.ptr, nib.ptr, dsc.ptr, n, K, n_off, stride, Ntot)
+        if kind == "q4_0t":
+            rc = device.lib.smith_repack_q4_0_t_into(ctx, src.ptr, nib.ptr, dsc.ptr, n, K, n_off, stride, Ntot)
         else:
             rc = device.lib.smith_repack_q8_0_into(ctx, src.ptr, nib.ptr, n, K, n_off, stride, Ntot)
         device.check(rc, "repack %s" % info["name"])

@@ -44,12 +44,15 @@ def test_code_object_has_kernels():
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     need = ["matmul_q4", "matmul_q8", "smith_quantize_q4s", "smith_quantize_q8", "smith_quantize_q4_0_rows",
-            "smith_repack_q4_0_cols", "smith_repack_q8_0_cols", "smith_zero_u32"]
+            "smith_repack_q4_0_cols", "smith_repack_q8_0_cols", "smith_repack_q4_0_tiles", "smith_zero_u32"]
     for fmt in ("q4", "q8", "q40"):
         need += ["smith_qprep_%s_hilo" % fmt, "smith_qprep_%s_plain" % fmt]
-    for fmt in ("q4s", "q8", "q40"):
+    need += ["smith_agemv_q40t_k%d" % k for k in (32, 48, 64, 72, 96, 128, 144, 192, 288)]
+    need += ["smith_agemv_q40t_k%d_c2" % k for k in (96, 128, 144)]
+    for fmt in ("q4s", "q8", "q40", "q40t"):
         need += ["smith_qgemv3_%s_m%d" % (fmt, m) for m in (4, 8, 16, 32)]
         need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 96, 128, 288)]
+        need += ["smith_qgemv1_%s_m1_k%d_c2" % (fmt, k) for k in (96, 128)]
     for k in need:
         assert re.search(r"\b%s\.kd\b" % k, out), k
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],

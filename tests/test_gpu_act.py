@@ -1,0 +1,180 @@
+"""GPU parity of the tile-major Q4_0 layout and the single-row act path
+(smith_repack_q4_0_t_into, smith_linear_q4_0_t, smith_linear_q4_0_t_act and
+the act outputs of smith_embed / the GEMV epilogues) against float64
+references built from the oracle's Q4_0 dequantization.
+
+Bars: the repack is byte-exact; GEMV outputs are within normwise 2e-5 of the
+float64 reference (hi/lo f16 activations keep ~22 bits, the same bar as the
+f32-activation Q4_0 GEMV tests); a SwiGLU output silu(g)*u carries the
+relative errors of both of its GEMV columns and silu's slope (<= 1.1), so
+its bar is 3x that, 6e-5.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from smith_amd import device, prng
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-5
+TOL_SWIGLU = 6e-5
+EPS = 1e-5
+
+
+def _q4_0(N, K, seed):
+    """GGUF [out=N, in=K] Q4_0 blocks, tile-major planes on the device, and
+    the dequantized float64 weight [N, K]."""
+    w = prng.randn((N, K), seed, std=0.02)
+    blocks = O.quantize_rows(O.GGML_Q4_0, w)
+    G = K // 32
+    src = device.alloc(blocks.size)
+    device.upload(src, blocks)
+    nib = device.alloc(N * G * 16)
+    dsc = device.alloc(N * G * 2)
+    device.check(device.lib.smith_repack_q4_0_t_into(device.ops_ctx(), src, nib, dsc, N, K, 0, 1, N))
+    device.sync()
+    device.release_buffer(src)
+    wd = O.dequantize_tensor(O.GGML_Q4_0, blocks, N * K).reshape(N, K).astype(np.float64)
+    return blocks, nib, dsc, wd
+
+
+def _buf(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = device.alloc(a.nbytes)
+    device.upload(b, a)
+    return b
+
+
+def _get(b, n):
+    device.sync()
+    return device.download(b, n * 4, np.float32).astype(np.float64)
+
+
+def _act_bytes(K):
+    return K * 4 + K // 8 * 12
+
+
+def _act_of(x, gamma):
+    """An act of vector x (times gamma) through the embedding's act output."""
+    K = x.size
+    E = _buf(x)
+    tok = device.alloc(4)
+    device.upload(tok, np.zeros(1, np.int32))
+    out = device.alloc(K * 4)
+    act = device.alloc(_act_bytes(K))
+    g = _buf(gamma) if gamma is not None else None
+    device.check(device.lib.smith_embed(device.ops_ctx(), E, tok, out, 1, K, act, g))
+    return act
+
+
+def _rms(x, g):
+    return x / np.sqrt(np.mean(x * x) + EPS) * g
+
+
+def _silu_mul(y):
+    g, u = y[0::2], y[1::2]
+    return g / (1 + np.exp(-g)) * u
+
+
+def test_tiles_repack_layout_and_interleave():
+    N, K = 48, 96
+    G = K // 32
+    w = prng.randn((N, K), 7, std=0.02)
+    blocks = O.quantize_rows(O.GGML_Q4_0, w)
+    src = device.alloc(blocks.size)
+    device.upload(src, blocks)
+    Nt = 2 * N  # two weights column-interleaved
+    nib = device.alloc(Nt * G * 16)
+    dsc = device.alloc(Nt * G * 2)
+    ctx = device.ops_ctx()
+    for j in range(2):
+        device.check(device.lib.smith_repack_q4_0_t_into(ctx, src, nib, dsc, N, K, j, 2, Nt))
+    got_nib = device.download(nib, Nt * G * 16, np.uint8).reshape(Nt // 16, G, 16, 16)
+    got_d = device.download(dsc, Nt * G * 2, np.uint8).reshape(Nt // 16, G, 16, 2)
+    b = blocks.reshape(N, G, 18)
+    for col in range(Nt):
+        n = col // 2
+        t, c = divmod(col, 16)
+        assert np.array_equal(got_nib[t, :, c], b[n, :, 2:]), col
+        assert np.array_equal(got_d[t, :, c], b[n, :, :2]), col
+    # rejected shapes
+    assert device.lib.smith_repack_q4_0_t_into(ctx, src, nib, dsc, N, K, 0, 1, 40) != 0
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 17])
+def test_linear_t_all_epilogues(M):
+    N, K = 160, 320
+    _, nib, dsc, wd = _q4_0(N, K, 11)
+    x = prng.randn((M, K), 12)
+    g = 1 + prng.randn((K,), 13, std=0.1)
+    r = prng.randn((M, N), 14)
+    ctx = device.ops_ctx()
+    xb, gb, rb, ob = _buf(x), _buf(g), _buf(r), device.alloc(M * N * 4)
+    xn = np.stack([_rms(x[m].astype(np.float64), g) for m in range(M)])
+    for epi in (0, 1, 2):
+        device.check(device.lib.smith_linear_q4_0_t(ctx, xb, nib, dsc, ob, M, N, K, gb, EPS, rb, epi))
+        y = xn @ wd.T
+        if epi == 1:
+            y = y + r
+        if epi == 2:
+            y = np.stack([_silu_mul(y[m]) for m in range(M)])
+        got = _get(ob, y.size).reshape(y.shape)
+        tol = (TOL_SWIGLU if epi == 2 else TOL) if M <= 8 else 1e-3
+        assert O.normwise_rel_err(got, y) <= tol, (M, epi)
+
+
+@pytest.mark.parametrize("N,K", [(64, 256), (5120, 3072), (96, 9600), (48, 32 * 7)])
+@pytest.mark.parametrize("norm", [0, 1])
+def test_act_gemv_matches_reference(N, K, norm):
+    _, nib, dsc, wd = _q4_0(N, K, 21 + N)
+    x = prng.randn((K,), 22).astype(np.float64)
+    g = 1 + prng.randn((K,), 23, std=0.1).astype(np.float64)
+    act = _act_of(x, g if norm else None)
+    out = device.alloc(N * 4)
+    device.check(device.lib.smith_linear_q4_0_t_act(device.ops_ctx(), act, norm, EPS, nib, dsc, out, N, K, None, 0,
+                                                    None, None))
+    xn = _rms(x, g) if norm else x
+    assert O.normwise_rel_err(_get(out, N), wd @ xn) <= TOL
+
+
+def test_act_chain_residual_swiglu_down():
+    """x -> [norm] q|k|v-like GEMV; o-proj with residual writing the act of
+    x2 (next norm's gamma folded in) -> gate|up with SwiGLU writing h's act ->
+    down with residual: every act output checked through its consumer."""
+    D, F = 256, 512
+    ctx = device.ops_ctx()
+    _, nib_o, d_o, wo = _q4_0(D, D, 31)
+    _, nib_gu, d_gu, wgu = _q4_0(2 * F, D, 32)
+    _, nib_dn, d_dn, wdn = _q4_0(D, F, 33)
+    a_in = prng.randn((D,), 34).astype(np.float64)
+    x = prng.randn((D,), 35).astype(np.float64)
+    g2 = 1 + prng.randn((D,), 36, std=0.1).astype(np.float64)
+    act_a = _act_of(a_in, None)
+    xb, g2b = _buf(x), _buf(g2)
+    x2b = device.alloc(D * 4)
+    act_x2 = device.alloc(_act_bytes(D))
+    device.check(device.lib.smith_linear_q4_0_t_act(ctx, act_a, 0, 0.0, nib_o, d_o, x2b, D, D, xb, 1, act_x2, g2b))
+    x2 = _get(x2b, D)
+    assert O.normwise_rel_err(x2, x + wo @ a_in) <= TOL
+    hb = device.alloc(F * 4)
+    act_h = device.alloc(_act_bytes(F))
+    device.check(device.lib.smith_linear_q4_0_t_act(ctx, act_x2, 1, EPS, nib_gu, d_gu, hb, 2 * F, D, None, 2,
+                                                    act_h, None))
+    h = _get(hb, F)
+    assert O.normwise_rel_err(h, _silu_mul(wgu @ _rms(x2, g2))) <= TOL_SWIGLU
+    outb = device.alloc(D * 4)
+    device.check(device.lib.smith_linear_q4_0_t_act(ctx, act_h, 0, 0.0, nib_dn, d_dn, outb, D, F, x2b, 1, None,
+                                                    None))
+    assert O.normwise_rel_err(_get(outb, D), x2 + wdn @ h) <= TOL
+
+
+def test_act_gemv_rejects_bad_shapes():
+    ctx = device.ops_ctx()
+    assert device.lib.smith_linear_q4_0_t_act(ctx, None, 0, 0.0, None, None, None, 64, 256, None, 0, None,
+                                              None) != 0
+    dummy = device.alloc(4096)
+    assert device.lib.smith_linear_q4_0_t_act(ctx, dummy, 0, 0.0, dummy, dummy, dummy, 64, 100, None, 0, None,
+                                              None) != 0
+    assert device.lib.smith_linear_q4_0_t_act(ctx, dummy, 0, 0.0, dummy, dummy, dummy, 48, 256, None, 0, dummy,
+                                              None) != 0
