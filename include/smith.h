@@ -192,6 +192,19 @@ int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, ui
 int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
                     uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
                     float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out);
+/* Single-row attention (S == 1, position *pos_ptr) that leaves the
+ * combination of its key splits to the output projection: parts receives,
+ * per head and split, (m, l, pad, pad, o[head_dim]) in 132-float records
+ * (n_heads * 8 * 132 floats); caches appended as smith_attention.
+ * head_dim <= 128, % 32. */
+int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, uint32_t n_heads, uint32_t n_kv_heads,
+                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, float* kcache,
+                          float* vcache, uint32_t max_seq, float* parts);
+/* smith_linear_q4_0_t_act whose input is smith_attention_parts' partials
+ * (K = n_heads * head_dim; the splits are combined per head first). */
+int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_ptr, uint32_t head_dim,
+                             const void* nib, const void* d, float* out, uint32_t N, uint32_t K, const float* resid,
+                             uint32_t epilogue, void* act_out, const float* gamma_out);
 /* LM head on a Q4_0 output.weight read as lmHead[K=dim][N=vocab] (blocks run
  * along the vocab axis, gguf_loader.js:240-259), optional fused final RMSNorm. */
 int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,

@@ -66,6 +66,146 @@ __device__ __forceinline__ float rope_elem(const float* __restrict__ row, uint32
 }
 
 // ---------------------------------------------------------------------------
+// One key split of one query row, shared by the attention kernels (256
+// threads): keys t0 .. t1-1, 32-row K/V tiles staged in LDS; rows t < p0
+// come from the caches, rows t >= p0 (this launch's rows) from qkv row
+// t - p0 with RoPE.  Each thread's share of a tile (4 float4 of K and of V)
+// is loaded into registers one tile ahead, the first tile before `qfill`
+// (which writes the roped query to qr) runs, so those loads overlap.
+// Softmax per tile runs across lanes (lane l: row l % 32), P.V as thread
+// (e, half) over the rows of one parity.  Returns the running (m, l) and
+// this thread's o for element e = tid % 128, row parity tid / 128.
+// ---------------------------------------------------------------------------
+#define ATT_TILE 32
+
+struct AttShared {
+  float qr[128] __attribute__((aligned(16)));
+  float Kt[ATT_TILE][129];
+  float Vt[ATT_TILE][128] __attribute__((aligned(16)));
+  float sc[ATT_TILE];
+};
+
+template <bool NEW>
+__device__ __forceinline__ void att_load_tile(float4 (&kreg)[4], float4 (&vreg)[4], const float* __restrict__ kb,
+                                              const float* __restrict__ vb, const float* __restrict__ newk,
+                                              uint32_t ld, uint32_t Wk, uint32_t kvh, uint32_t hd, uint32_t p0,
+                                              uint32_t tb, uint32_t t1, const float* __restrict__ cosT,
+                                              const float* __restrict__ sinT) {
+  const uint32_t tid = threadIdx.x, c4n = hd / 4;
+  const uint32_t nt = t1 - tb < ATT_TILE ? t1 - tb : ATT_TILE;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t idx = tid + 256 * i, r = idx / c4n, c4 = idx % c4n;
+    const uint32_t t = tb + (r < nt ? r : nt - 1);  // rows past nt: copies of a real row (weight 0)
+    float4 kv, vv;
+    if (!NEW || t < p0) {
+      kv = *(const float4*)(kb + (size_t)t * hd + 4 * c4);
+      vv = *(const float4*)(vb + (size_t)t * hd + 4 * c4);
+    } else {
+      const float* kr = newk + (size_t)(t - p0) * ld;
+      const uint32_t e0 = kvh * hd + 4 * c4;
+      kv = make_float4(rope_elem(kr, Wk, e0, t, cosT, sinT), rope_elem(kr, Wk, e0 + 1, t, cosT, sinT),
+                       rope_elem(kr, Wk, e0 + 2, t, cosT, sinT), rope_elem(kr, Wk, e0 + 3, t, cosT, sinT));
+      vv = *(const float4*)(kr + Wk + e0);
+    }
+    kreg[i] = kv;
+    vreg[i] = vv;
+  }
+}
+
+template <bool NEW, class QF>
+__device__ __forceinline__ void att_split(AttShared& sh, const float* __restrict__ kb, const float* __restrict__ vb,
+                                          const float* __restrict__ newk, uint32_t ld, uint32_t Wk, uint32_t kvh,
+                                          uint32_t hd, uint32_t p0, uint32_t t0, uint32_t t1,
+                                          const float* __restrict__ cosT, const float* __restrict__ sinT,
+                                          float scale, QF qfill, float& m, float& l, float& o) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t c4n = hd / 4;
+  float4 kreg[4], vreg[4];
+  if (t0 < t1) att_load_tile<NEW>(kreg, vreg, kb, vb, newk, ld, Wk, kvh, hd, p0, t0, t1, cosT, sinT);
+  qfill();
+  const uint32_t e = tid % 128, part = tid / 128;
+  m = -__builtin_inff();
+  l = 0.f;
+  o = 0.f;
+  __syncthreads();  // qr visible
+  for (uint32_t tb = t0; tb < t1; tb += ATT_TILE) {
+    const uint32_t nt = t1 - tb < ATT_TILE ? t1 - tb : ATT_TILE;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t idx = tid + 256 * i, r = idx / c4n, c4 = idx % c4n;
+      if (r < ATT_TILE) {
+        sh.Kt[r][4 * c4] = kreg[i].x;
+        sh.Kt[r][4 * c4 + 1] = kreg[i].y;
+        sh.Kt[r][4 * c4 + 2] = kreg[i].z;
+        sh.Kt[r][4 * c4 + 3] = kreg[i].w;
+        *(float4*)&sh.Vt[r][4 * c4] = vreg[i];
+      }
+    }
+    __syncthreads();
+    if (tb + ATT_TILE < t1)  // next tile in flight during this one
+      att_load_tile<NEW>(kreg, vreg, kb, vb, newk, ld, Wk, kvh, hd, p0, tb + ATT_TILE, t1, cosT, sinT);
+    {
+      const uint32_t r = tid / 8, sub = tid % 8;
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint32_t c = sub + 8 * i;
+        if (c < hd) d = __builtin_fmaf(sh.qr[c], sh.Kt[r][c], d);
+      }
+      d += __shfl_xor(d, 1);
+      d += __shfl_xor(d, 2);
+      d += __shfl_xor(d, 4);
+      if (sub == 0) sh.sc[r] = r < nt ? d * scale : -__builtin_inff();
+    }
+    __syncthreads();
+    const float sl = sh.sc[tid & 31];
+    float tm = sl;
+#pragma unroll
+    for (int k = 16; k >= 1; k >>= 1) {
+      const float ov = __shfl_xor(tm, k);
+      tm = ov > tm ? ov : tm;
+    }
+    const float mn = tm > m ? tm : m;
+    const float alpha = __expf(m - mn);  // first tile: m = -inf -> 0
+    const float pl = __expf(sl - mn);    // rows >= nt: exp(-inf) = 0
+    float ps = pl;
+#pragma unroll
+    for (int k = 16; k >= 1; k >>= 1) ps += __shfl_xor(ps, k);
+    float acc = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < ATT_TILE / 2; rr++) {
+      const uint32_t row = 2 * rr + part;
+      acc = __builtin_fmaf(__shfl(pl, (int)row), sh.Vt[row][e < hd ? e : 0], acc);
+    }
+    l = l * alpha + ps;
+    o = o * alpha + acc;
+    m = mn;
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// KV-cache append for S rows at positions p0 .. p0+S-1 (p0 = *pos_ptr):
+// kcache[kv][p] = RoPE(k row) (the reference's whole-row indexing), vcache
+// [kv][p] = v row (gguf_cache.js:212-231).  Workgroup s, threads over Wk.
+// ---------------------------------------------------------------------------
+extern "C" __global__ void smith_kv_append(const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr,
+                                           uint32_t Wq, uint32_t nKV, uint32_t hd, const float* __restrict__ cosT,
+                                           const float* __restrict__ sinT, float* __restrict__ kcache,
+                                           float* __restrict__ vcache, uint32_t maxSeq) {
+  const uint32_t s = blockIdx.x, pos = (uint32_t)pos_ptr[0] + s;
+  const uint32_t Wk = nKV * hd;
+  const float* krow = qkv + (size_t)s * ld + Wq;
+  for (uint32_t i = threadIdx.x; i < Wk; i += blockDim.x) {
+    const uint32_t kv = i / hd, e = i % hd;
+    const size_t o = ((size_t)kv * maxSeq + pos) * hd + e;
+    kcache[o] = rope_elem(krow, Wk, i, pos, cosT, sinT);
+    vcache[o] = krow[Wk + i];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Fused RoPE + KV-cache append + GQA attention, for S query rows at positions
 // p0 .. p0+S-1 with p0 = *pos_ptr (gguf_cache.js:128-157 for decode,
 // :212-231 for prefill).  qkv rows hold [q | k | v] (ld floats per row).
@@ -84,17 +224,14 @@ __device__ __forceinline__ float rope_elem(const float* __restrict__ row, uint32
 // sum_z e^(m_z-M) l_z.  hd <= 128, 256 threads.
 // ---------------------------------------------------------------------------
 #define ATT_SPLIT 8
-#define ATT_TILE 32
 
-extern "C" __global__ __launch_bounds__(256) void smith_attention(
+template <bool APPENDED>
+__device__ __forceinline__ void attention_body(
     const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
     uint32_t nKV, uint32_t hd, const float* __restrict__ cosT, const float* __restrict__ sinT,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out,
     float* __restrict__ ws, uint32_t* __restrict__ counters, uint8_t* __restrict__ act_out) {
-  __shared__ __attribute__((aligned(16))) float qr[128];
-  __shared__ __attribute__((aligned(16))) float Kt[ATT_TILE][129];
-  __shared__ __attribute__((aligned(16))) float Vt[ATT_TILE][128];
-  __shared__ float sc[ATT_TILE];
+  __shared__ AttShared sh;
   __shared__ float ored[2][128];
   __shared__ int s_last;
   const uint32_t h = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
@@ -106,72 +243,26 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention(
   const uint32_t Wq = nH * hd, Wk = nKV * hd;
   const float scale = 1.0f / __builtin_sqrtf((float)hd);
   const float* qrow = qkv + (size_t)s * ld;
-  for (uint32_t e = tid; e < hd; e += 256) qr[e] = rope_elem(qrow, Wq, h * hd + e, pos, cosT, sinT);
-  if (h % rep == 0 && z == 0) {
-    const float* krow = qkv + (size_t)s * ld + Wq;
-    for (uint32_t e = tid; e < hd; e += 256) {
-      size_t o = ((size_t)kvh * maxSeq + pos) * hd + e;
-      kcache[o] = rope_elem(krow, Wk, kvh * hd + e, pos, cosT, sinT);
-      vcache[o] = krow[Wk + kvh * hd + e];
-    }
-  }
   // this split's key rows
   const uint32_t per = (T + ATT_SPLIT - 1) / ATT_SPLIT;
   const uint32_t t0 = z * per, t1 = t0 + per < T ? t0 + per : T;
   const uint32_t e = tid % 128, part = tid / 128;  // output element, row half
-  float m = -__builtin_inff(), l = 0.f, o = 0.f;
-  __syncthreads();
-  for (uint32_t tb = t0; tb < t1; tb += ATT_TILE) {
-    const uint32_t nt = t1 - tb < ATT_TILE ? t1 - tb : ATT_TILE;
-    // stage K and V rows of the tile
-    for (uint32_t idx = tid; idx < nt * (hd / 4); idx += 256) {
-      uint32_t r = idx / (hd / 4), c4 = idx % (hd / 4);
-      uint32_t t = tb + r;
-      float4 kv4, vv4;
-      if (t < p0) {
-        kv4 = *(const float4*)(kcache + ((size_t)kvh * maxSeq + t) * hd + 4 * c4);
-        vv4 = *(const float4*)(vcache + ((size_t)kvh * maxSeq + t) * hd + 4 * c4);
-      } else {
-        const float* kr = qkv + (size_t)(t - p0) * ld + Wq;
-        uint32_t e0 = kvh * hd + 4 * c4;
-        kv4 = make_float4(rope_elem(kr, Wk, e0, t, cosT, sinT), rope_elem(kr, Wk, e0 + 1, t, cosT, sinT),
-                          rope_elem(kr, Wk, e0 + 2, t, cosT, sinT), rope_elem(kr, Wk, e0 + 3, t, cosT, sinT));
-        vv4 = *(const float4*)(kr + Wk + e0);
-      }
-      Kt[r][4 * c4] = kv4.x;
-      Kt[r][4 * c4 + 1] = kv4.y;
-      Kt[r][4 * c4 + 2] = kv4.z;
-      Kt[r][4 * c4 + 3] = kv4.w;
-      *(float4*)&Vt[r][4 * c4] = vv4;
-    }
-    __syncthreads();
-    // scores: 8 lanes per row
-    {
-      uint32_t r = tid / 8, sub = tid % 8;
-      float d = 0.f;
-      if (r < nt)
-        for (uint32_t c = sub; c < hd; c += 8) d = __builtin_fmaf(qr[c], Kt[r][c], d);
-      d += __shfl_xor(d, 1);
-      d += __shfl_xor(d, 2);
-      d += __shfl_xor(d, 4);
-      if (sub == 0 && r < ATT_TILE) sc[r] = r < nt ? d * scale : -__builtin_inff();
-    }
-    __syncthreads();
-    float tm = -__builtin_inff();
-    for (uint32_t r = 0; r < nt; r++) tm = sc[r] > tm ? sc[r] : tm;
-    const float mn = tm > m ? tm : m;
-    const float alpha = __expf(m - mn);
-    float ps = 0.f, acc = 0.f;
-    for (uint32_t r = 0; r < nt; r++) {
-      float p = __expf(sc[r] - mn);
-      ps += p;
-      if ((r & 1) == part && e < hd) acc = __builtin_fmaf(p, Vt[r][e], acc);
-    }
-    l = l * alpha + ps;
-    o = o * alpha + acc;
-    m = mn;
-    __syncthreads();
-  }
+  float m, l, o;
+  // APPENDED: smith_kv_append already put this launch's rows in the caches
+  att_split<!APPENDED>(sh, kcache + (size_t)kvh * maxSeq * hd, vcache + (size_t)kvh * maxSeq * hd, qkv + Wq, ld, Wk, kvh, hd,
+            APPENDED ? p0 + S : p0, t0, t1, cosT, sinT, scale,
+            [&]() {
+              for (uint32_t e2 = tid; e2 < hd; e2 += 256) sh.qr[e2] = rope_elem(qrow, Wq, h * hd + e2, pos, cosT, sinT);
+              if (!APPENDED && h % rep == 0 && z == 0) {
+                const float* krow = qkv + (size_t)s * ld + Wq;
+                for (uint32_t e2 = tid; e2 < hd; e2 += 256) {
+                  size_t oo = ((size_t)kvh * maxSeq + pos) * hd + e2;
+                  kcache[oo] = rope_elem(krow, Wk, kvh * hd + e2, pos, cosT, sinT);
+                  vcache[oo] = krow[Wk + kvh * hd + e2];
+                }
+              }
+            },
+            m, l, o);
   // combine the two row halves of this split
   if (e < hd) ored[part][e] = o;
   __syncthreads();
@@ -225,6 +316,84 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention(
     if (act_out) act_emit8(act_out, Wq, h * hd + tid, y, 1.0f);  // S == 1, hd % 8 == 0
   }
   if (tid == 0) __hip_atomic_exchange(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define ATT_ARGS                                                                                              \
+  const float *__restrict__ qkv, uint32_t ld, const int32_t *__restrict__ pos_ptr, uint32_t S, uint32_t nH,    \
+      uint32_t nKV, uint32_t hd, const float *__restrict__ cosT, const float *__restrict__ sinT,               \
+      float *__restrict__ kcache, float *__restrict__ vcache, uint32_t maxSeq, float *__restrict__ out,        \
+      float *__restrict__ ws, uint32_t *__restrict__ counters, uint8_t *__restrict__ act_out
+// rows' keys formed here from qkv (and appended to the caches)
+extern "C" __global__ __launch_bounds__(256) void smith_attention(ATT_ARGS) {
+  attention_body<false>(qkv, ld, pos_ptr, S, nH, nKV, hd, cosT, sinT, kcache, vcache, maxSeq, out, ws, counters,
+                        act_out);
+}
+// every key already in the caches (smith_kv_append ran first)
+extern "C" __global__ __launch_bounds__(256) void smith_attention_cached(ATT_ARGS) {
+  attention_body<true>(qkv, ld, pos_ptr, S, nH, nKV, hd, cosT, sinT, kcache, vcache, maxSeq, out, ws, counters,
+                       act_out);
+}
+
+// ---------------------------------------------------------------------------
+// Single-row decode attention writing per-split partials for the output
+// projection to combine (smith_agemv_att_*), so no workgroup of this kernel
+// waits for another.  Row position p0 = *pos_ptr, T = p0 + 1 keys, split
+// count nsplit = min(ATTP_MAXSPLIT, ceil(T / ATTP_ROWS)) decided on the
+// device (one captured grid serves every position; workgroups past nsplit
+// leave at once).  Workgroup (b, z): query head h of KV head b % nKV (the
+// rep query heads of a KV head get workgroup ids congruent mod nKV, i.e. the
+// same XCD when nKV is a multiple of 8, so they share its L2), key split z.
+// Math as smith_attention (RoPE'd q, 1/sqrt(hd) scores, online softmax over
+// 32-row K/V tiles staged in LDS); the partial (m, l, o[hd]) of (h, z) goes
+// to parts[(h*ATTP_MAXSPLIT + z)*ATTP_STRIDE ..] with plain stores.  The
+// (h % rep == 0, z == 0) workgroup appends the row's key/value to the caches.
+// ---------------------------------------------------------------------------
+#define ATTP_ROWS 32
+#define ATTP_MAXSPLIT 8
+#define ATTP_STRIDE 132  // floats per partial: m, l, 2 pad, o[128] (16-byte aligned)
+
+extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
+    const float* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, uint32_t nH, uint32_t nKV, uint32_t hd,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, float* __restrict__ kcache,
+    float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts) {
+  __shared__ AttShared sh;
+  __shared__ float ored[2][128];
+  const uint32_t rep = nH / nKV;
+  const uint32_t kvh = blockIdx.x % nKV, h = kvh * rep + blockIdx.x / nKV, z = blockIdx.y;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t p0 = (uint32_t)pos_ptr[0];
+  const uint32_t T = p0 + 1;
+  uint32_t nsplit = (T + ATTP_ROWS - 1) / ATTP_ROWS;
+  nsplit = nsplit < ATTP_MAXSPLIT ? nsplit : ATTP_MAXSPLIT;
+  if (z >= nsplit) return;
+  const uint32_t Wq = nH * hd, Wk = nKV * hd;
+  const float scale = 1.0f / __builtin_sqrtf((float)hd);
+  const float* krow = qkv + Wq;
+  const uint32_t per = (T + nsplit - 1) / nsplit;
+  const uint32_t t0 = z * per, t1 = t0 + per < T ? t0 + per : T;
+  const uint32_t e = tid % 128, part = tid / 128;
+  float m, l, o;
+  att_split<true>(sh, kcache + (size_t)kvh * maxSeq * hd, vcache + (size_t)kvh * maxSeq * hd, krow, 0, Wk, kvh, hd, p0, t0,
+            t1, cosT, sinT, scale,
+            [&]() {
+              for (uint32_t e2 = tid; e2 < hd; e2 += 256) sh.qr[e2] = rope_elem(qkv, Wq, h * hd + e2, p0, cosT, sinT);
+              if (h % rep == 0 && z == 0) {
+                for (uint32_t e2 = tid; e2 < hd; e2 += 256) {
+                  size_t oo = ((size_t)kvh * maxSeq + p0) * hd + e2;
+                  kcache[oo] = rope_elem(krow, Wk, kvh * hd + e2, p0, cosT, sinT);
+                  vcache[oo] = krow[Wk + kvh * hd + e2];
+                }
+              }
+            },
+            m, l, o);
+  if (e < hd) ored[part][e] = o;
+  __syncthreads();
+  float* pp = parts + ((size_t)h * ATTP_MAXSPLIT + z) * ATTP_STRIDE;
+  if (tid < hd) pp[4 + tid] = ored[0][tid] + ored[1][tid];
+  if (tid == 0) {
+    pp[0] = m;
+    pp[1] = l;
+  }
 }
 
 // ---------------------------------------------------------------------------

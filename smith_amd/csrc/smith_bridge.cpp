@@ -1041,9 +1041,75 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   }
   void* pws = c->att_ws;
   uint32_t* pcnt = c->att_cnt;
+  uint32_t appended = 0;
+  if (S > 1) {
+    // prompt rows: rope + append every row's key/value first, so the
+    // attention workgroups read all keys from the caches
+    uint32_t Wq = n_heads * head_dim;
+    void* aargs[] = {&qkv, &ld, &pos_ptr, &Wq, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &kcache, &vcache,
+                     &max_seq};
+    if (launch(c, "smith_kv_append", dim3(S), dim3(256), aargs)) return -1;
+    appended = 1;
+  }
   void* args[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
                   &kcache, &vcache, &max_seq, &out, &pws, &pcnt, &act_out};
-  return launch(c, "smith_attention", dim3(n_heads, S, nsplit), dim3(256), args);
+  return launch(c, appended ? "smith_attention_cached" : "smith_attention", dim3(n_heads, S, nsplit), dim3(256),
+                args);
+}
+
+int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, uint32_t n_heads, uint32_t n_kv_heads,
+                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, float* kcache,
+                          float* vcache, uint32_t max_seq, float* parts) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!n_kv_heads || n_heads % n_kv_heads)
+    return fail(c, "smith_attention_parts: %u heads not a multiple of %u kv heads", n_heads, n_kv_heads);
+  if (head_dim > 128 || head_dim % 32)
+    return fail(c, "smith_attention_parts: head_dim %u unsupported (<= 128, %% 32)", head_dim);
+  if (set_device(c)) return -1;
+  void* args[] = {&qkv, &pos_ptr, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
+                  &kcache, &vcache, &max_seq, &parts};
+  return launch(c, "smith_attention_part", dim3(n_heads, 8), dim3(256), args);  // ATTP_MAXSPLIT splits
+}
+
+int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_ptr, uint32_t head_dim,
+                             const void* nib, const void* d, float* out, uint32_t N, uint32_t K, const float* resid,
+                             uint32_t epilogue, void* act_out, const float* gamma_out) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!parts || !pos_ptr) return fail(c, "smith_linear_q4_0_t_attn: no attention partials");
+  if (!head_dim || head_dim > 128 || head_dim % 32 || K % head_dim)
+    return fail(c, "smith_linear_q4_0_t_attn: head_dim %u unsupported for K %u", head_dim, K);
+  if (K % 32 || !K) return fail(c, "smith_linear_q4_0_t_attn: K %u is not a positive multiple of 32", K);
+  if (N % 16 || !N) return fail(c, "smith_linear_q4_0_t_attn: N %u is not a positive multiple of 16", N);
+  if (epilogue > 2) return fail(c, "smith_linear_q4_0_t_attn: unknown epilogue %u", epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q4_0_t_attn: residual epilogue without a residual buffer");
+  const uint32_t nout = epilogue == 2 ? N / 2 : N;
+  if (act_out && nout % 32) return fail(c, "smith_linear_q4_0_t_attn: act output needs %u %% 32 == 0", nout);
+  if (set_device(c)) return -1;
+  static const uint32_t kbs[] = {64, 96, 128, 192};
+  const uint32_t G = K / 32;
+  uint32_t kb = 192;
+  for (uint32_t v : kbs)
+    if (v >= G) {
+      kb = v;
+      break;
+    }
+  const uint32_t ksplit = (G + kb - 1) / kb;
+  const uint32_t threads = kb == 64 ? 256 : 512;
+  const uint32_t gx = N / 16;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_agemv_att_q40t_k%u", kb);
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pN = N, pK = K, phd = head_dim, pepi = epilogue;
+  const float* pR = epilogue == 1 ? resid : nullptr;
+  void* args[] = {&parts, &pos_ptr, &phd, &nib, &d, &out, &pN, &pK, &pR, &pepi, &act_out, &gamma_out, &pws, &pcnt};
+  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
 }
 
 int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,

@@ -1038,18 +1038,29 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 // (store / residual / SwiGLU), the f32 store (C may be null) and, with
 // act_out, the act of the produced vector for the next projection.
 // ---------------------------------------------------------------------------
-template <int CT, int S, int WK>
+// SRC 0: the input is an act.  SRC 1: the input is the attention output as
+// per-split partials (smith_attention_part: (m, l, o[hd]) per head and key
+// split, ATTP_STRIDE floats each); the block combines the splits of the
+// heads in its K range (softmax weights e^(m_z - M) / L) and converts them
+// to the MFMA operand in LDS itself.  No RMSNorm in front (norm == 0).
+#define ATTP_MAXSPLIT 8  // as llama_kernels.hip
+#define ATTP_ROWS 32
+#define ATTP_STRIDE 132
+template <int CT, int S, int WK, int SRC>
 __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, const uint8_t* __restrict__ B,
                                            const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t N,
                                            uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,
                                            uint32_t epi, uint8_t* __restrict__ act_out,
                                            const float* __restrict__ gamma_out, float* __restrict__ ws,
-                                           uint32_t* __restrict__ counters) {
+                                           uint32_t* __restrict__ counters, const int32_t* __restrict__ pos_ptr,
+                                           uint32_t hd) {
   constexpr int GPW = 4 * S;
   constexpr int BC = 16 * CT;
   constexpr int GMAX = 4 * S * WK;
   __shared__ u32x4 fragL[8 * GMAX + 4];  // [g][hi/lo][slice] + one zero fragment
   __shared__ float red[WK][BC];
+  __shared__ float c1L[SRC == 1 ? 4 * GMAX : 1];                 // per-part C1 (SRC 1)
+  __shared__ float coefL[SRC == 1 ? GMAX : 1][ATTP_MAXSPLIT];    // per-head split weights (SRC 1)
   const uint32_t G = K / 32, T = K / 8;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1069,26 +1080,61 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   constexpr int CPT = (8 * GMAX + NT - 1) / NT;   // frag words per thread (this block's groups)
   constexpr int SPL = (4 * GMAX + 63) / 64;       // part sums of squares per lane
   u32x4 fv[CPT];
-#pragma unroll
-  for (int q = 0; q < CPT; q++) {
-    const uint32_t e = 8 * gb + threadIdx.x + q * NT;
-    fv[q] = frag[e < 8 * G ? e : 8 * G - 1];  // clamped: branch-free issue
-  }
   float c1[S];
-#pragma unroll
-  for (int st = 0; st < S; st++) {
-    const uint32_t g = gw + 4 * st + j;
-    const uint32_t gc = g < G ? g : G - 1;
-    const float4 cc = *(const float4*)(c1p + 4 * gc);
-    c1[st] = (cc.x + cc.y) + (cc.z + cc.w);
-  }
-  // sums of squares for the RMSNorm (one block covers K; with a K split the
-  // finishing block reads them at the end)
   float ssv[SPL];
+  // SRC 1: split partials of this block's parts (part = 8 elements)
+  constexpr int PPT = SRC == 1 ? (4 * GMAX + NT - 1) / NT : 1;
+  float4 oa[PPT][ATTP_MAXSPLIT], ob[PPT][ATTP_MAXSPLIT];
+  float mlv[2 * ATTP_MAXSPLIT];
+  uint32_t nsplit = 1, h0 = 0;
+  if (SRC == 0) {
 #pragma unroll
-  for (int q = 0; q < SPL; q++) {
-    const uint32_t t = lane + 64 * q;
-    ssv[q] = c1p[2 * T + (t < T ? t : T - 1)];
+    for (int q = 0; q < CPT; q++) {
+      const uint32_t e = 8 * gb + threadIdx.x + q * NT;
+      fv[q] = frag[e < 8 * G ? e : 8 * G - 1];  // clamped: branch-free issue
+    }
+#pragma unroll
+    for (int st = 0; st < S; st++) {
+      const uint32_t g = gw + 4 * st + j;
+      const uint32_t gc = g < G ? g : G - 1;
+      const float4 cc = *(const float4*)(c1p + 4 * gc);
+      c1[st] = (cc.x + cc.y) + (cc.z + cc.w);
+    }
+    // sums of squares for the RMSNorm (one block covers K; with a K split the
+    // finishing block reads them at the end)
+#pragma unroll
+    for (int q = 0; q < SPL; q++) {
+      const uint32_t t = lane + 64 * q;
+      ssv[q] = c1p[2 * T + (t < T ? t : T - 1)];
+    }
+  } else {
+    const uint32_t T1 = (uint32_t)pos_ptr[0] + 1;
+    nsplit = (T1 + ATTP_ROWS - 1) / ATTP_ROWS;
+    nsplit = nsplit < ATTP_MAXSPLIT ? nsplit : ATTP_MAXSPLIT;
+    const float* parts = (const float*)act;
+    h0 = gb * 32 / hd;
+    const uint32_t hend = ((gb + GMAX < G ? gb + GMAX : G) * 32 + hd - 1) / hd;
+    {  // (m, l) of head h0 + threadIdx.x
+      const uint32_t hh = h0 + threadIdx.x < hend ? h0 + threadIdx.x : hend - 1;
+#pragma unroll
+      for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
+        const float2 ml = *(const float2*)(parts + ((size_t)hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE);
+        mlv[2 * zz] = ml.x;
+        mlv[2 * zz + 1] = ml.y;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PPT; q++) {
+      uint32_t pi = 4 * gb + threadIdx.x + q * NT;
+      pi = pi < 4 * G ? pi : 4 * G - 1;
+      const uint32_t e0 = 8 * pi, hh = e0 / hd, d0 = e0 % hd;
+#pragma unroll
+      for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
+        const float4* op = (const float4*)(parts + ((size_t)hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE + 4 + d0);
+        oa[q][zz] = op[0];
+        ob[q][zz] = op[1];
+      }
+    }
   }
   // epilogue operands of wave 0 (residual, next norm's gamma), loaded now so
   // the tail after the reduction has no global load in its dependency chain
@@ -1121,17 +1167,96 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         wd[st][ct] = D[rec];
       }
   }
-#pragma unroll
-  for (int q = 0; q < CPT; q++) {
-    const uint32_t e = threadIdx.x + q * NT;
-    if (e < 8 * GMAX) fragL[e] = fv[q];
-  }
   if (threadIdx.x < 4) fragL[8 * GMAX + threadIdx.x] = (u32x4){0u, 0u, 0u, 0u};
   float ssum = 0.f;
-  if (ksplit == 1)
+  if (SRC == 0) {
 #pragma unroll
-    for (int q = 0; q < SPL; q++) ssum += lane + 64 * q < T ? ssv[q] : 0.f;
+    for (int q = 0; q < CPT; q++) {
+      const uint32_t e = threadIdx.x + q * NT;
+      if (e < 8 * GMAX) fragL[e] = fv[q];
+    }
+    if (ksplit == 1)
+#pragma unroll
+      for (int q = 0; q < SPL; q++) ssum += lane + 64 * q < T ? ssv[q] : 0.f;
+  } else {
+    // softmax weights of each head's splits: e^(m_z - M) / sum_z e^(m_z - M) l_z
+    if (threadIdx.x < GMAX) {
+      float M = -__builtin_inff();
+#pragma unroll
+      for (int zz = 0; zz < ATTP_MAXSPLIT; zz++)
+        if ((uint32_t)zz < nsplit) M = mlv[2 * zz] > M ? mlv[2 * zz] : M;
+      float f[ATTP_MAXSPLIT], L = 0.f;
+#pragma unroll
+      for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
+        const bool live = (uint32_t)zz < nsplit && mlv[2 * zz] != -__builtin_inff();
+        f[zz] = live ? __expf(mlv[2 * zz] - M) : 0.f;
+        L = live ? __builtin_fmaf(f[zz], mlv[2 * zz + 1], L) : L;  // unwritten splits may hold anything
+      }
+#pragma unroll
+      for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) coefL[threadIdx.x][zz] = f[zz] / L;
+    }
+    __syncthreads();
+    // combined elements -> f16 hi/lo operand slots + per-part C1 (act_frag.h order)
+#pragma unroll
+    for (int q = 0; q < PPT; q++) {
+      const uint32_t pl = threadIdx.x + q * NT;  // part within the block
+      const uint32_t pi = 4 * gb + pl;
+      if (pl < 4 * GMAX && pi < 4 * G) {
+        const uint32_t hl = 8 * pi / hd - h0;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = 0.f;
+#pragma unroll
+        for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
+          if ((uint32_t)zz >= nsplit) break;  // unwritten splits (never multiply stale memory)
+          const float cz = coefL[hl][zz];
+          v[0] = __builtin_fmaf(cz, oa[q][zz].x, v[0]);
+          v[1] = __builtin_fmaf(cz, oa[q][zz].y, v[1]);
+          v[2] = __builtin_fmaf(cz, oa[q][zz].z, v[2]);
+          v[3] = __builtin_fmaf(cz, oa[q][zz].w, v[3]);
+          v[4] = __builtin_fmaf(cz, ob[q][zz].x, v[4]);
+          v[5] = __builtin_fmaf(cz, ob[q][zz].y, v[5]);
+          v[6] = __builtin_fmaf(cz, ob[q][zz].z, v[6]);
+          v[7] = __builtin_fmaf(cz, ob[q][zz].w, v[7]);
+        }
+        const int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+        _Float16 hv[8], lv[8];
+        float c1p_ = 0.f, sp_ = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float a = v[perm[e]];
+          const _Float16 hh = (_Float16)a;
+          const float hf = (float)hh;
+          const _Float16 ll = (_Float16)((a - hf) * 2048.0f);
+          const float lf = (float)ll;
+          hv[e] = hh;
+          lv[e] = ll;
+          const float off = (e & 2) ? 64.0f : 1024.0f;
+          c1p_ += __builtin_fmaf(lf * off, 1.0f / 2048.0f, hf * off);
+          sp_ += __builtin_fmaf(lf, 1.0f / 2048.0f, hf);
+        }
+        u32x4 hp, lp;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          hp[k] = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[2 * k], hv[2 * k + 1]});
+          lp[k] = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[2 * k], lv[2 * k + 1]});
+        }
+        const uint32_t gl = pl >> 2, sl = pl & 3;
+        fragL[(gl * 2 + 0) * 4 + sl] = hp;
+        fragL[(gl * 2 + 1) * 4 + sl] = lp;
+        c1L[pl] = __builtin_fmaf(8.0f, sp_, c1p_);
+      }
+    }
+  }
   __syncthreads();
+  if (SRC == 1) {
+#pragma unroll
+    for (int st = 0; st < S; st++) {
+      const uint32_t g = gw + 4 * st + j;
+      const uint32_t gl = (g < G ? g : G - 1) - gb;
+      c1[st] = (c1L[4 * gl] + c1L[4 * gl + 1]) + (c1L[4 * gl + 2] + c1L[4 * gl + 3]);
+    }
+  }
 
   // 3. MFMAs and the exact per-group post-step (inactive lanes read zeros)
   uint32_t abase[S];
@@ -1230,7 +1355,19 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       float* __restrict__ C, uint32_t N, uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,   \
       uint32_t epi, uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out, float* __restrict__ ws, \
       uint32_t* __restrict__ counters) {                                                                     \
-    agemv_body<CT, S, WK>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters);          \
+    agemv_body<CT, S, WK, 0>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters,        \
+                             nullptr, 0);                                                                    \
+  }
+
+// o-projection on attention split partials (SRC 1); parts in place of the act
+#define DEF_AGEMV_ATT(NAME, CT, S, WK)                                                                       \
+  extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                                \
+      const float* __restrict__ parts, const int32_t* __restrict__ pos_ptr, uint32_t hd,                     \
+      const uint8_t* __restrict__ B, const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t N,       \
+      uint32_t K, const float* __restrict__ R, uint32_t epi, uint8_t* __restrict__ act_out,                   \
+      const float* __restrict__ gamma_out, float* __restrict__ ws, uint32_t* __restrict__ counters) {        \
+    agemv_body<CT, S, WK, 1>((const uint8_t*)parts, B, D, C, N, K, 0u, 0.f, R, epi, act_out, gamma_out, ws,  \
+                             counters, pos_ptr, hd);                                                         \
   }
 
 // named by the groups one block covers (4*S*WK) and the column tiles per wave;
@@ -1247,6 +1384,10 @@ DEF_AGEMV(smith_agemv_q40t_k288, 1, 9, 8)
 DEF_AGEMV(smith_agemv_q40t_k96_c2, 2, 3, 8)
 DEF_AGEMV(smith_agemv_q40t_k128_c2, 2, 4, 8)
 DEF_AGEMV(smith_agemv_q40t_k144_c2, 2, 3, 12)
+DEF_AGEMV_ATT(smith_agemv_att_q40t_k64, 1, 4, 4)
+DEF_AGEMV_ATT(smith_agemv_att_q40t_k96, 1, 3, 8)
+DEF_AGEMV_ATT(smith_agemv_att_q40t_k128, 1, 4, 8)
+DEF_AGEMV_ATT(smith_agemv_att_q40t_k192, 1, 6, 8)
 
 #ifndef SMITH_NO_INSTANCES
 DEF_QGEMV3_FMT(q4s, FMT_Q4S)

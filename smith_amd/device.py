@@ -80,6 +80,8 @@ SYMBOLS = {
     "smith_linear_q4_0": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
     "smith_repack_q4_0_t_into": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32]),
     "smith_linear_q4_0_t": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
+    "smith_attention_parts": (_INT, [_P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _U32, _P]),
+    "smith_linear_q4_0_t_attn": (_INT, [_P, _P, _P, _U32, _P, _P, _P, _U32, _U32, _P, _U32, _P, _P]),
     "smith_linear_q4_0_t_act": (_INT, [_P, _P, ctypes.c_int, ctypes.c_float, _P, _P, _P, _U32, _U32, _P, _U32, _P,
                                        _P]),
     "smith_linear_q8": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),

@@ -15,9 +15,12 @@ graph and replayed.
 Single-row steps on Q4_0 models pass activations between kernels as "acts"
 (the vector already in the GEMV's MFMA operand form, with per-8-element sums
 and sums of squares; smith_linear_q4_0_t_act): every producer -- embedding,
-attention, o-proj, gate|up, down -- writes the act its consumer reads, with
-the next RMSNorm's gamma folded in, and the consumer applies the norm's rms
-as one scalar.  Prefill rows (M > 1) take the f32 path.
+o-proj, gate|up, down -- writes the act its consumer reads, with the next
+RMSNorm's gamma folded in, and the consumer applies the norm's rms as one
+scalar.  Attention leaves its key-split partials to the o-projection, which
+combines them while it builds its operand (smith_attention_parts +
+smith_linear_q4_0_t_attn; head_dim % 32 == 0, else attention writes an act).
+Prefill rows (M > 1) take the f32 path.
 """
 import os
 
@@ -82,6 +85,10 @@ class _Engine:
             return DeviceArray((K * 4 + K // 8 * 12,), np.uint8)
         if self.use_act:
             self.act_x, self.act_a, self.act_x2, self.act_h = act(dim), act(dim), act(dim), act(ffn)
+        # attention partials combined by the o-projection (hd % 32 == 0)
+        self.use_parts = self.use_act and hd % 32 == 0 and hd <= 128
+        if self.use_parts:
+            self.att_parts = DeviceArray((cfg["numHeads"] * 8 * 132,))
 
     def set_pos(self, p):
         device.check(device.lib.smith_set_i32(device.ops_ctx(), self.pos.ptr, int(p)), "set_pos")
@@ -115,11 +122,22 @@ class _Engine:
         blocks = model["blocks"]
         for li, (blk, cache) in enumerate(zip(blocks, caches)):
             blk["qkv"].act(ax, True, eps, qkv)
-            device.check(device.lib.smith_attention(
-                ctx, qkv, self.qkv_ld, self.pos.ptr, 1, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
-                rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, aa),
-                "attention")
-            blk["outProj"].act(aa, False, 0.0, x2, resid=x, epilogue=1, act_out=ax2, gamma_out=blk["ln2Gamma"].ptr)
+            if self.use_parts:
+                parts = self.att_parts.ptr
+                device.check(device.lib.smith_attention_parts(
+                    ctx, qkv, self.pos.ptr, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"], rope["cos"].ptr,
+                    rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], parts), "attention")
+                o = blk["outProj"]
+                device.check(device.lib.smith_linear_q4_0_t_attn(
+                    ctx, parts, self.pos.ptr, cfg["headDim"], o.a.ptr, o.b.ptr, x2, o.N, o.K, x, 1, ax2,
+                    blk["ln2Gamma"].ptr), "o-proj (attention partials)")
+            else:
+                device.check(device.lib.smith_attention(
+                    ctx, qkv, self.qkv_ld, self.pos.ptr, 1, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
+                    rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, aa),
+                    "attention")
+                blk["outProj"].act(aa, False, 0.0, x2, resid=x, epilogue=1, act_out=ax2,
+                                   gamma_out=blk["ln2Gamma"].ptr)
             blk["gateUp"].act(ax2, True, eps, None, epilogue=2, act_out=ah)
             last = li + 1 == len(blocks)
             blk["ffnDown"].act(ah, False, 0.0, x, resid=x2, epilogue=1, act_out=None if last else ax,

@@ -49,6 +49,7 @@ def test_code_object_has_kernels():
         need += ["smith_qprep_%s_hilo" % fmt, "smith_qprep_%s_plain" % fmt]
     need += ["smith_agemv_q40t_k%d" % k for k in (32, 48, 64, 72, 96, 128, 144, 192, 288)]
     need += ["smith_agemv_q40t_k%d_c2" % k for k in (96, 128, 144)]
+    need += ["smith_agemv_att_q40t_k%d" % k for k in (64, 96, 128, 192)]
     for fmt in ("q4s", "q8", "q40", "q40t"):
         need += ["smith_qgemv3_%s_m%d" % (fmt, m) for m in (4, 8, 16, 32)]
         need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 96, 128, 288)]
@@ -57,7 +58,8 @@ def test_code_object_has_kernels():
         assert re.search(r"\b%s\.kd\b" % k, out), k
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
-    for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_lmhead_q4_0_nb",
+    for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_attention_part", "smith_kv_append", "smith_attention_cached",
+              "smith_lmhead_q4_0_nb",
               "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
 

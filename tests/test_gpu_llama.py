@@ -72,7 +72,8 @@ def test_generate_greedy_graph_and_sync_paths(q4):
     assert out4 == out[:5 + gen.index(gen[4]) + 1]
 
 
-@pytest.mark.parametrize("kw", [dict(tie=True), dict(linear_type="q8_0"), dict(kv_heads=4)])
+@pytest.mark.parametrize("kw", [dict(tie=True), dict(linear_type="q8_0"), dict(kv_heads=4),
+                                dict(dim=288, heads=6, kv_heads=3)])  # head_dim 48: attention writes an act
 def test_variants(tmp_path_factory, kw):
     p = _files(tmp_path_factory, "v.gguf", **kw)
     m = loadGGUF(p)
@@ -111,3 +112,21 @@ def test_config5_dims_two_layers(tmp_path_factory):
         g = m.forwardDecode(t, 8 + i, caches)["logits"][0]
         assert normwise_rel_err(g, logits[i + 1]) <= TOL, i
     check_tokens(out[8:], logits)
+
+
+@pytest.mark.parametrize("n_prompt", [509, 1100])
+def test_long_context_decode_key_splits(tmp_path_factory, n_prompt):
+    """Single-row decode attention past 512 keys splits the keys across
+    workgroups (device-side split count): positions 509..512 cross the first
+    boundary (T = 512 -> 513), 1100.. run three splits."""
+    p = _files(tmp_path_factory, "long.gguf", context=8192)
+    m = loadGGUF(p)
+    ref = LO.LlamaOracle(p)
+    prompt = [int(x) for x in (np.arange(n_prompt) * 7919 % SMALL["vocab"])]
+    caches = m.createCache()
+    got = m.forwardPrefill(prompt, caches)["logits"][-1]
+    assert normwise_rel_err(got, ref.forward(prompt, 0)[-1]) <= TOL
+    for i, t in enumerate([5, 250, 17, 99]):
+        g = m.forwardDecode(t, n_prompt + i, caches)["logits"]
+        w = ref.forward([t], n_prompt + i)
+        assert normwise_rel_err(g, w) <= TOL, (n_prompt, i)
