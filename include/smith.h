@@ -206,9 +206,14 @@ int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_p
                              const void* nib, const void* d, float* out, uint32_t N, uint32_t K, const float* resid,
                              uint32_t epilogue, void* act_out, const float* gamma_out);
 /* LM head on a Q4_0 output.weight read as lmHead[K=dim][N=vocab] (blocks run
- * along the vocab axis, gguf_loader.js:240-259), optional fused final RMSNorm. */
-int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,
-                         uint32_t K, uint32_t N);
+ * along the vocab axis, gguf_loader.js:240-259): smith_repack_lmhead_q4_0
+ * splits the raw blocks into a nibble plane (K*N/2 bytes, block order) and a
+ * scale plane transposed to [N/32][K] (f16); smith_lmhead_q4_0_nb computes
+ * y = x . lmHead on those planes, optional fused final RMSNorm.
+ * K % 8 == 0, K <= 8192, N % 32 == 0. */
+int smith_repack_lmhead_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_t K, uint32_t N);
+int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
+                         const void* d, float* y, uint32_t K, uint32_t N);
 /* f32 GEMV, W [K][N] (w_is_nk = 0) or [N][K] (weight tying, 1). */
 int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,
                    uint32_t K, uint32_t N, int w_is_nk);

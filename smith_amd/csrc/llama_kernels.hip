@@ -401,74 +401,127 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
 // is read as lmHead[dim][vocab] (gguf_loader.js:240-259 never transposes a
 // path that does not end in ".weight"), so for Q4_0 the 32-weight blocks run
 // along the VOCAB axis: block (k, vb) at (k*(N/32) + vb)*18 covers
-// lmHead[k][32vb .. 32vb+31] = d*(nib - 8) (interleaved nibbles).
+// lmHead[k][32vb .. 32vb+31] = d*(nib - 8), element e in nibble e (byte
+// e/2, low nibble first).  smith_repack_lmhead_q4_0 splits the blocks into
+// a nibble plane in the same (k, vb) order (16 bytes per block) and a scale
+// plane transposed to [vb][k], so a lane reads one dword of nibbles per row
+// and the scales of 8 rows in one 16-byte load.
 // y[n] = sum_k x[k] * lmHead[k][n] for M = 1, optionally with the final
 // RMSNorm of x fused (gamma != null).
 // Lane (vb = lane/4, sub = lane%4) owns outputs 32vb + 8sub .. +7 of the 16
-// blocks a workgroup covers (one dword of nibbles per row k); per row:
-// c = x_k * d, 8 fma(c, nibble), and one -8c correction for the lane's 8
-// outputs.  8 waves split the workgroup's K range (LDS reduction); K splits
-// across workgroups (grid.y) are summed by the last-arriving workgroup.
+// blocks a workgroup covers; per row: c = x_k * d, 8 fma(c, nibble), and one
+// -8c correction for the lane's 8 outputs.  Rows go in batches of 16 with
+// the next batch's loads issued before the current one is used.  8 waves
+// split the workgroup's K range (LDS reduction); K splits across workgroups
+// (grid.y) are summed by the last-arriving workgroup.
 // ---------------------------------------------------------------------------
+extern "C" __global__ void smith_repack_lmhead_q4_0(const uint8_t* __restrict__ src, uint8_t* __restrict__ nib,
+                                                    uint16_t* __restrict__ dsc, uint32_t K, uint32_t NB) {
+  size_t total = (size_t)K * NB;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t k = (uint32_t)(idx / NB), vb = (uint32_t)(idx % NB);
+    const uint16_t* b = (const uint16_t*)(src + idx * 18);
+    dsc[(size_t)vb * K + k] = b[0];
+    uint16_t* dn = (uint16_t*)(nib + idx * 16);
+#pragma unroll
+    for (int i = 0; i < 8; i++) dn[i] = b[1 + i];
+  }
+}
+
+#define LMH_BATCH 16
+
 extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
-    const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ W,
-    float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws, uint32_t* __restrict__ counters) {
+    const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ nib,
+    const uint16_t* __restrict__ dsc, float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws,
+    uint32_t* __restrict__ counters) {
   __shared__ float xs[8192];
   __shared__ float part[8][512];
   __shared__ float red[8];
   __shared__ int s_last;
   const uint32_t NB = N / 32;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t vb = blockIdx.x * 16 + lane / 4, sub = lane & 3;
+  const uint32_t vb0 = blockIdx.x * 16 + lane / 4, sub = lane & 3;
+  const uint32_t vb = vb0 < NB ? vb0 : NB - 1;  // clamped; lanes past NB store nothing
   const uint32_t ksplit = gridDim.y;
-  const uint32_t kb = (K + ksplit - 1) / ksplit;
-  const uint32_t kb0 = blockIdx.y * kb, kb1 = kb0 + kb < K ? kb0 + kb : K;
-  float ss = 0.f;
-  for (uint32_t i = threadIdx.x; i < K; i += 512) {
-    float v = x[i];
-    xs[i] = v;
-    ss = __builtin_fmaf(v, v, ss);
+  // split and wave row counts are multiples of 8 (K % 8 == 0): aligned 16-byte scale loads
+  const uint32_t kb = ((K + ksplit - 1) / ksplit + 7) / 8 * 8;
+  const uint32_t kb0 = blockIdx.y * kb < K ? blockIdx.y * kb : K, kb1 = kb0 + kb < K ? kb0 + kb : K;
+  const uint32_t kper = ((kb1 - kb0 + 7) / 8 + 7) / 8 * 8;
+  const uint32_t k0 = kb0 + wave * kper < kb1 ? kb0 + wave * kper : kb1;
+  const uint32_t k1 = k0 + kper < kb1 ? k0 + kper : kb1;
+
+  // 1. x (and gamma) loads, then the first row batch in flight
+  float xv[16], gvv[16];
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const uint32_t i = threadIdx.x + 512 * q;
+    xv[q] = i < K ? x[i] : 0.f;
+    gvv[q] = gamma && i < K ? gamma[i] : 1.f;
   }
+  uint32_t wn[LMH_BATCH];
+  uint4 wd[LMH_BATCH / 8];
+  auto load_batch = [&](uint32_t kbase) {
+#pragma unroll
+    for (int r = 0; r < LMH_BATCH; r++) {
+      const uint32_t k = kbase + r < k1 ? kbase + r : (k1 > 0 ? k1 - 1 : 0);
+      wn[r] = *(const uint32_t*)(nib + ((size_t)k * NB + vb) * 16 + 4 * sub);
+    }
+#pragma unroll
+    for (int q = 0; q < LMH_BATCH / 8; q++) {
+      uint32_t k = kbase + 8 * q;
+      k = k < K ? k : K - 8;  // K % 8 == 0
+      wd[q] = *(const uint4*)(dsc + (size_t)vb * K + k);
+    }
+  };
+  if (k0 < k1) load_batch(k0);
+
+  // 2. RMSNorm of x into LDS
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; q++) ss = __builtin_fmaf(xv[q], xv[q], ss);
+  float rms = 1.f;
   if (gamma) {
     for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     float tot = 0.f;
     for (int w = 0; w < 8; w++) tot += red[w];
-    float rms = 1.0f / __builtin_sqrtf(tot / (float)K + eps);
-    for (uint32_t i = threadIdx.x; i < K; i += 512) xs[i] = xs[i] * rms * gamma[i];
+    rms = 1.0f / __builtin_sqrtf(tot / (float)K + eps);
+  }
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const uint32_t i = threadIdx.x + 512 * q;
+    if (i < K) xs[i] = gamma ? xv[q] * rms * gvv[q] : xv[q];
   }
   __syncthreads();
+
+  // 3. rows
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = 0.f;
   float corr = 0.f;
-  const uint32_t kper = (kb1 - kb0 + 7) / 8;
-  const uint32_t k0 = kb0 + wave * kper, k1 = k0 + kper < kb1 ? k0 + kper : kb1;
-  if (vb < NB) {
-    // 16 rows per batch: all of a batch's loads are issued before any use
-    for (uint32_t kb8 = k0; kb8 < k1; kb8 += 16) {
-      uint16_t dh[16], lo[16], hi[16];
+  for (uint32_t kb16 = k0; kb16 < k1; kb16 += LMH_BATCH) {
+    uint32_t cn[LMH_BATCH];
+    uint4 cd[LMH_BATCH / 8];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        uint32_t k = kb8 + r < k1 ? kb8 + r : k1 - 1;
-        const uint16_t* b = (const uint16_t*)(W + ((size_t)k * NB + vb) * 18);  // 2-byte aligned records
-        dh[r] = b[0];
-        lo[r] = b[1 + 2 * sub];
-        hi[r] = b[2 + 2 * sub];
-      }
+    for (int r = 0; r < LMH_BATCH; r++) cn[r] = wn[r];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        if (kb8 + r >= k1) break;
-        float c = xs[kb8 + r] * (float)__builtin_bit_cast(_Float16, dh[r]);
-        uint32_t w = (uint32_t)lo[r] | ((uint32_t)hi[r] << 16);
-        uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 2j / 2j+1 in byte j
-        corr += c;
+    for (int q = 0; q < LMH_BATCH / 8; q++) cd[q] = wd[q];
+    if (kb16 + LMH_BATCH < k1) load_batch(kb16 + LMH_BATCH);
 #pragma unroll
-        for (int jb = 0; jb < 4; jb++) {
-          acc[2 * jb] = __builtin_fmaf(c, (float)((ev >> (8 * jb)) & 0xFFu), acc[2 * jb]);
-          acc[2 * jb + 1] = __builtin_fmaf(c, (float)((od >> (8 * jb)) & 0xFFu), acc[2 * jb + 1]);
-        }
+    for (int r = 0; r < LMH_BATCH; r++) {
+      const uint32_t k = kb16 + r;
+      const uint32_t dw = (&cd[r / 8].x)[(r % 8) / 2];
+      const uint16_t dh = (uint16_t)((r & 1) ? dw >> 16 : dw & 0xFFFFu);
+      const float c = k < k1 ? xs[k] * (float)__builtin_bit_cast(_Float16, dh) : 0.f;
+      const uint32_t w = cn[r];
+      const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 2j / 2j+1 in byte j
+      corr += c;
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++) {
+        acc[2 * jb] = __builtin_fmaf(c, (float)((ev >> (8 * jb)) & 0xFFu), acc[2 * jb]);
+        acc[2 * jb + 1] = __builtin_fmaf(c, (float)((od >> (8 * jb)) & 0xFFu), acc[2 * jb + 1]);
       }
     }
   }
@@ -476,19 +529,17 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
   for (int e = 0; e < 8; e++) part[wave][lane * 8 + e] = __builtin_fmaf(-8.0f, corr, acc[e]);
   __syncthreads();
   const uint32_t nb0 = blockIdx.x * 512;
-  for (uint32_t o = threadIdx.x; o < 512; o += 512) {
-    float v = 0.f;
+  const uint32_t o = threadIdx.x, n = nb0 + o;
+  float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < 8; w++) v += part[w][o];
-    uint32_t n = nb0 + o;
-    if (n >= N) continue;
-    if (ksplit == 1)
-      y[n] = v;
-    else
-      __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
+  for (int w = 0; w < 8; w++) v += part[w][o];
+  if (ksplit == 1) {
+    if (n < N) y[n] = v;
+    return;
   }
-  if (ksplit == 1) return;
+  if (n < N)
+    __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -497,14 +548,12 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
   }
   __syncthreads();
   if (!s_last) return;
-  for (uint32_t o = threadIdx.x; o < 512; o += 512) {
-    uint32_t n = nb0 + o;
-    if (n >= N) continue;
-    float v = 0.f;
+  if (n < N) {
+    float t = 0.f;
     for (uint32_t sp = 0; sp < ksplit; sp++)
-      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n, 0u, __ATOMIC_RELAXED,
+      t += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n, 0u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT));
-    y[n] = v;
+    y[n] = t;
   }
   if (threadIdx.x == 0)
     __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -604,11 +653,22 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(const floa
   __shared__ int32_t s_tok;
   float best = -__builtin_inff();
   int32_t bidx = 0x7fffffff;
-  for (uint32_t i = threadIdx.x; i < N; i += 1024) {
-    float v = logits[i];
-    if (v > best) {  // strictly greater: earliest index within this thread
-      best = v;
-      bidx = (int32_t)i;
+  // thread t scans indices t, t + 1024, ... in increasing order, 8 loads in
+  // flight per batch
+  for (uint32_t i0 = threadIdx.x; i0 < N; i0 += 8 * 1024) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t i = i0 + 1024 * u;
+      v[u] = logits[i < N ? i : N - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t i = i0 + 1024 * u;
+      if (i < N && v[u] > best) {  // strictly greater: earliest index within this thread
+        best = v[u];
+        bidx = (int32_t)i;
+      }
     }
   }
   for (int d = 32; d >= 1; d >>= 1) {

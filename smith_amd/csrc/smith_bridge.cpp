@@ -1112,12 +1112,25 @@ int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_p
   return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
 }
 
-int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* W, float* y,
-                         uint32_t K, uint32_t N) {
+int smith_repack_lmhead_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (N % 32) return fail(c, "smith_repack_lmhead_q4_0: vocab %u is not a multiple of 32", N);
+  if (set_device(c)) return -1;
+  uint32_t NB = N / 32;
+  uint64_t total = (uint64_t)K * NB;
+  if (!total) return 0;
+  void* args[] = {&blocks, &nib, &d, &K, &NB};
+  return launch(c, "smith_repack_lmhead_q4_0", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
+                         const void* d, float* y, uint32_t K, uint32_t N) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
   if (N % 32) return fail(c, "smith_lmhead_q4_0_nb: vocab %u is not a multiple of 32", N);
-  if (K > 8192) return fail(c, "smith_lmhead_q4_0_nb: dim %u exceeds 8192", K);
+  if (K > 8192 || K % 8 || !K) return fail(c, "smith_lmhead_q4_0_nb: dim %u unsupported (8..8192, %% 8)", K);
   if (set_device(c)) return -1;
   uint32_t gx = (N / 32 + 15) / 16;
   // enough K splits that each of a workgroup's 8 waves has <= 32 rows
@@ -1128,7 +1141,7 @@ int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, flo
   }
   float* pws = c->ws;
   uint32_t* pcnt = c->counters;
-  void* args[] = {&x, &norm_gamma, &eps, &W, &y, &K, &N, &pws, &pcnt};
+  void* args[] = {&x, &norm_gamma, &eps, &nib, &d, &y, &K, &N, &pws, &pcnt};
   return launch(c, "smith_lmhead_q4_0_nb", dim3(gx, ksplit), dim3(512), args);
 }
 

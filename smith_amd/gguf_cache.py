@@ -154,7 +154,8 @@ class _Engine:
         cfg, ctx = self.cfg, device.ops_ctx()
         head, g, eps = model["lmHead"], model["lnFGamma"].ptr, model["normEps"]
         if head["kind"] == "q4_0_nb":
-            rc = device.lib.smith_lmhead_q4_0_nb(ctx, x_ptr, g, eps, head["w"].ptr, self.logits.ptr, cfg["dim"],
+            rc = device.lib.smith_lmhead_q4_0_nb(ctx, x_ptr, g, eps, head["nib"].ptr, head["d"].ptr, self.logits.ptr,
+                                                 cfg["dim"],
                                                  cfg["vocabSize"])
         elif head["kind"] == "f32_kn":
             rc = device.lib.smith_gemv_f32(ctx, x_ptr, g, eps, head["w"].ptr, self.logits.ptr, cfg["dim"],

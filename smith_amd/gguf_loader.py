@@ -217,8 +217,14 @@ def loadWeights(parsed, model):
     elif head["type"] == G.GGML_TYPE["Q4_0"]:
         if vocab % 32:
             raise NotImplementedError("Q4_0 output.weight needs vocab % 32 == 0")
-        model["lmHead"] = {"kind": "q4_0_nb", "w": DeviceArray.from_host(np.asarray(G.readTensorData(parsed, head)),
-                                                                          np.uint8)}
+        raw = DeviceArray.from_host(np.asarray(G.readTensorData(parsed, head)), np.uint8)
+        nibp = DeviceArray((dim * vocab // 2,), np.uint8)
+        dscp = DeviceArray((dim * vocab // 32,), np.uint16)
+        device.check(device.lib.smith_repack_lmhead_q4_0(device.ops_ctx(), raw.ptr, nibp.ptr, dscp.ptr, dim, vocab),
+                     "repack output.weight")
+        device.sync()
+        device.release_buffer(raw.ptr)
+        model["lmHead"] = {"kind": "q4_0_nb", "nib": nibp, "d": dscp}
     elif head["type"] in (G.GGML_TYPE["F32"], G.GGML_TYPE["F16"]):
         model["lmHead"] = {"kind": "f32_kn", "w": DeviceArray.from_host(G.dense_f32(parsed, head))}
     else:

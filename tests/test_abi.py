@@ -59,7 +59,7 @@ def test_code_object_has_kernels():
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_attention_part", "smith_kv_append", "smith_attention_cached",
-              "smith_lmhead_q4_0_nb",
+              "smith_lmhead_q4_0_nb", "smith_repack_lmhead_q4_0",
               "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
 

@@ -7,7 +7,7 @@ Bars: the repack is byte-exact; GEMV outputs are within normwise 2e-5 of the
 float64 reference (hi/lo f16 activations keep ~22 bits, the same bar as the
 f32-activation Q4_0 GEMV tests); a SwiGLU output silu(g)*u carries the
 relative errors of both of its GEMV columns and silu's slope (<= 1.1), so
-its bar is 3x that, 6e-5.
+its bar is 3x that, 6e-5.  The LM head is f32 FMA throughout (bar 2e-6).
 """
 import numpy as np
 import pytest
@@ -18,6 +18,7 @@ from smith_amd import device, prng
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-5
+TOL_F32 = 2e-6  # f32 FMA paths (no f16 operand)
 TOL_SWIGLU = 6e-5
 EPS = 1e-5
 
@@ -178,3 +179,25 @@ def test_act_gemv_rejects_bad_shapes():
                                               None) != 0
     assert device.lib.smith_linear_q4_0_t_act(ctx, dummy, 0, 0.0, dummy, dummy, dummy, 48, 256, None, 0, dummy,
                                               None) != 0
+
+
+@pytest.mark.parametrize("K,N", [(200, 96), (3072, 32000), (8192, 320)])
+def test_lmhead_planes_match_reference(K, N):
+    """Q4_0 output.weight read as lmHead[K][N] (blocks along N): planes from
+    smith_repack_lmhead_q4_0, y = rmsnorm(x) . lmHead, vs float64."""
+    w = prng.randn((K, N), 61, std=0.02)
+    blocks = O.quantize_rows(O.GGML_Q4_0, w)  # rows of N: blocks run along the vocab axis
+    wd = O.dequantize_tensor(O.GGML_Q4_0, blocks, K * N).reshape(K, N).astype(np.float64)
+    ctx = device.ops_ctx()
+    src = device.alloc(blocks.size)
+    device.upload(src, blocks)
+    nib = device.alloc(K * N // 2)
+    dsc = device.alloc(K * N // 16)
+    device.check(device.lib.smith_repack_lmhead_q4_0(ctx, src, nib, dsc, K, N))
+    x = prng.randn((K,), 62).astype(np.float64)
+    g = 1 + prng.randn((K,), 63, std=0.1).astype(np.float64)
+    xb, gb, yb = _buf(x), _buf(g), device.alloc(N * 4)
+    device.check(device.lib.smith_lmhead_q4_0_nb(ctx, xb, gb, EPS, nib, dsc, yb, K, N))
+    assert O.normwise_rel_err(_get(yb, N), _rms(x, g) @ wd) <= TOL_F32
+    device.check(device.lib.smith_lmhead_q4_0_nb(ctx, xb, None, 0.0, nib, dsc, yb, K, N))
+    assert O.normwise_rel_err(_get(yb, N), x @ wd) <= TOL_F32
