@@ -177,6 +177,40 @@ def cpu_baseline(K, N, budget_s):
                       "%.1f ms/call; host has %d cpus" % (reps, el, per * 1e3, os.cpu_count() or 0)}
 
 
+def cpu_baseline_e2e(reps=2):
+    """Config-5 decode on the CPU, the reference's path (weights dequantized to
+    f32 at load, gguf_loader.js:236; f32 GEMVs per token), 1 thread: one
+    layer's seven projections and the LM head timed with the oracle's f32
+    matmul, extrapolated to 32 layers (attention, norms and the sampler are
+    left out: < 1% of the work)."""
+    from oracle import oracle as O
+    from smith_amd import prng
+    c = dict(dim=3072, kv=1024, ffn=9216, vocab=32000, layers=32)
+    shapes = [(c["dim"], c["dim"]), (c["dim"], c["kv"]), (c["dim"], c["kv"]), (c["dim"], c["dim"]),
+              (c["dim"], c["ffn"]), (c["dim"], c["ffn"]), (c["ffn"], c["dim"])]
+    t_layer = 0.0
+    for i, (K, N) in enumerate(shapes):
+        w = prng.randn((K, N), 100 + i, std=0.02)
+        a = prng.randn((1, K), 0)
+        best = None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            O.matmul_f32(a, w)
+            el = time.perf_counter() - t0
+            best = el if best is None else min(best, el)
+        t_layer += best
+        del w
+    w = prng.randn((c["dim"], c["vocab"]), 200, std=0.02)
+    t0 = time.perf_counter()
+    O.matmul_f32(prng.randn((1, c["dim"]), 0), w)
+    t_head = time.perf_counter() - t0
+    del w
+    per_token = c["layers"] * t_layer + t_head
+    return {"value": round(1.0 / per_token, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": "oracle f32 GEMVs of one config-5 layer (%.1f ms) x 32 + LM head (%.1f ms), best of %d; "
+                      "extrapolated, attention/norms omitted" % (t_layer * 1e3, t_head * 1e3, reps)}
+
+
 def calibrate(D, steps):
     """Platform floor: per-launch duration of an empty kernel and of a plain
     128-bit streaming read of the config-1/3 weight sizes (HIP events over
@@ -328,6 +362,11 @@ def main():
     if not args.quick:
         cpu = cpu_baseline(K, N, args.cpu_seconds)
         log("cpu baseline:", cpu)
+        e2e = bench_e2e(D, args.gguf)
+        e2e["cpu_baseline"] = cpu_baseline_e2e()
+        e2e["bound_tok_s_at_hbm_peak"] = round(HBM_PEAK_GBS * 1e9 / (1981808640 + 55296000), 1)
+        configs["cfg5_e2e_llama_q4_0_decode"] = e2e
+        log("cfg5:", json.dumps(e2e))
 
     line = {
         "metric": "Q4 GEMV GB/s (% HBM peak) + Q4 decode tokens/sec, 1 MI355X",
