@@ -354,7 +354,8 @@ def main():
                 pre["M%d_N%d_K%d" % (M, Nn, Kk)] = {"TFLOPs_step": round(fl / msx / 1e9, 2),
                                                    "mfma_util_vs_f16_dense": round(fl / msx / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
                                                    "ms_step": round(msx, 3),
-                                                   "path": "GEMV in 32-row chunks (MFMA prefill GEMM not built yet)"}
+                                                   "path": "f16 activation prep + MFMA GEMM (Q4S dequantized "
+                                                           "to f16 in LDS, f32 accumulation)"}
         configs["cfg4_q4s_prefill"] = pre
         log("cfg4:", json.dumps(pre))
 

@@ -2,6 +2,7 @@
 
   smith_amd/lib/smith_kernels.hsaco   hipcc --offload-device-only --offload-arch=gfx950
   smith_amd/lib/smith_llama.hsaco     (the GGUF decode-path kernels, same flags)
+  smith_amd/lib/smith_gemm.hsaco      (the prefill MFMA GEMM, same flags)
   smith_amd/lib/libsmith.so           g++ host code against libamdhip64
 
 Run as `python -m smith_amd.build`; __graft_entry__.build() calls build().
@@ -16,6 +17,7 @@ LIBDIR = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HSACO = os.path.join(LIBDIR, "smith_kernels.hsaco")
 HSACO_LLAMA = os.path.join(LIBDIR, "smith_llama.hsaco")
+HSACO_GEMM = os.path.join(LIBDIR, "smith_gemm.hsaco")
 LIBSMITH = os.path.join(LIBDIR, "libsmith.so")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (unreliable on the pool).
@@ -33,7 +35,7 @@ def _run(cmd):
 def build_kernels():
     os.makedirs(LIBDIR, exist_ok=True)
     # a plain gfx950 ELF code object (no offload bundle) for hipModuleLoad
-    for src, dst in (("smith_kernels.hip", HSACO), ("llama_kernels.hip", HSACO_LLAMA)):
+    for src, dst in (("smith_kernels.hip", HSACO), ("llama_kernels.hip", HSACO_LLAMA), ("gemm_kernels.hip", HSACO_GEMM)):
         _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
               "-c", os.path.join(CSRC, src), "-o", dst])
 

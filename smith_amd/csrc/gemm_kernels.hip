@@ -1,0 +1,319 @@
+// gemm_kernels.hip -- gfx950 prefill GEMM for the quantized-weight path
+// (M >= 64 rows): C[M,N] = A[M,K] . W[K,N] with W in one of the packed
+// formats of smith_kernels.hip, dequantized tile by tile into LDS as f16 and
+// multiplied on v_mfma_f32_16x16x32_f16 with f32 accumulation.
+//
+//   smith_gemm_prep_a   A (f32, optional RMSNorm with gamma) -> A16 (f16)
+//   smith_gemm_<fmt>_m<BM>_n<BN>  the GEMM, fmt in {q4s, q8, q40, q40t}
+//
+// Workgroup tile BM x BN (128x64 .. 256x256), K in stages of BK=64 (two
+// 32-row quantization groups), double-buffered in LDS: while the MFMAs
+// consume stage s, the global loads of stage s+1 (A16 rows, weight records)
+// are in flight in registers; they are dequantized and stored after the
+// MFMAs.  Big tiles give each stage enough MFMA work (0.86 us for 256x256)
+// to cover the loads' latency.  A wave owns a 64x64 (64x32 for BN=64) part
+// of the tile as 16x16 MFMA tiles.  LDS rows hold 64 K values + 8 halves of
+// padding (144 B stride); LDS 288 * (BM + BN) bytes (147 KB at 256x256).
+// Dequantization (exact products, one f16 rounding per weight):
+//   Q4S   w = scale * (nib - zero)   record (g,n) 24 B  (shaders/matmul_q4.metal:24-28)
+//   Q8    w = f32(d) * int8          record (g,n) 34 B  (shaders/matmul_q8.metal:40-52)
+//   Q40T  w = d * (nib - 8)          tile-major planes  (src/gguf.js:187-197)
+//   Q40   same, planes in (g, n) record order
+// element k of a group is nibble k (byte k>>1, low nibble first) / byte k.
+// Epilogues: 0 store, 1 residual add, 2 SwiGLU on interleaved (gate, up)
+// columns: C[m][n/2] = silu(gate) * up.
+// Tiles are numbered so the tiles that share a weight tile run on one XCD
+// (workgroup id mod 8), keeping that weight tile in one L2.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define WF_Q4S 0
+#define WF_Q8 1
+#define WF_Q40T 2
+#define WF_Q40 3  // Q4_0 planes in (g, n) order (smith_repack_q4_0)
+
+#define GBK 64
+#define GLD 72  // halves per LDS row (64 + 8 pad)
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  _Float16 ha = (_Float16)a, hb = (_Float16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+// one weight record in registers
+struct WRec {
+  u32x4 q;         // Q4: 32 nibbles; Q8: int8 0..15
+  u32x4 q8b;       // Q8: int8 16..31 (with the 2-byte shift dword)
+  uint32_t q8c;
+  uint32_t sh;
+  float s, z;
+};
+
+template <int FMT>
+__device__ __forceinline__ WRec load_wrec(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
+                                          uint32_t N, uint32_t G, uint32_t g, uint32_t n) {
+  WRec r;
+  const bool ok = g < G && n < N;
+  const uint32_t gc = g < G ? g : G - 1, nc = n < N ? n : N - 1;
+  r.sh = 0;
+  r.z = 0.f;
+  if (FMT == WF_Q4S) {
+    const uint8_t* p = B + ((size_t)gc * N + nc) * 24;
+    r.q = *(const u32x4*)p;
+    const float2 sz = *(const float2*)(p + 16);
+    r.s = sz.x;
+    r.z = sz.y;
+  } else if (FMT == WF_Q40T || FMT == WF_Q40) {
+    const size_t rec = FMT == WF_Q40 ? (size_t)gc * N + nc : ((size_t)(nc >> 4) * G + gc) * 16 + (nc & 15);
+    r.q = *(const u32x4*)(B + rec * 16);
+    r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
+    r.z = 8.f;
+  } else {
+    const uint8_t* p = B + ((size_t)gc * N + nc) * 34;
+    r.s = (float)__builtin_bit_cast(_Float16, *(const uint16_t*)p);
+    const size_t a = (size_t)(p + 2);
+    const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
+    r.sh = (uint32_t)(a & 3);
+    r.q = (u32x4){w[0], w[1], w[2], w[3]};
+    r.q8b = (u32x4){w[4], w[5], w[6], w[7]};
+    r.q8c = w[8];
+  }
+  if (!ok) r.s = 0.f;
+  return r;
+}
+
+// the 32 dequantized weights of a record as 16 packed f16 pairs (k order)
+template <int FMT>
+__device__ __forceinline__ void dequant_wrec(const WRec& r, uint32_t (&o)[16]) {
+  if (FMT == WF_Q8) {
+    const uint32_t d[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t x = __builtin_amdgcn_alignbyte(d[i + 1], d[i], r.sh);  // int8 4i..4i+3
+      const float v0 = (float)(int8_t)(x & 0xFF), v1 = (float)(int8_t)((x >> 8) & 0xFF);
+      const float v2 = (float)(int8_t)((x >> 16) & 0xFF), v3 = (float)(int8_t)(x >> 24);
+      o[2 * i] = pack_h2(r.s * v0, r.s * v1);
+      o[2 * i + 1] = pack_h2(r.s * v2, r.s * v3);
+    }
+  } else {
+    const float c = -r.s * r.z;
+    const uint32_t d[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = d[i] & 0x0F0F0F0Fu, hi = (d[i] >> 4) & 0x0F0F0F0Fu;  // byte b: elements 2b / 2b+1
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const float ql = (float)((lo >> (8 * b)) & 0xFFu), qh = (float)((hi >> (8 * b)) & 0xFFu);
+        o[4 * i + b] = pack_h2(__builtin_fmaf(ql, r.s, c), __builtin_fmaf(qh, r.s, c));
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float silu_mul_g(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
+template <int FMT, int BM, int BN>
+__device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, const uint8_t* __restrict__ B,
+                                         const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t M,
+                                         uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,
+                                         float* __restrict__ ws, uint32_t sps) {
+  constexpr int WM = 64, WN = BN >= 128 ? 64 : 32;  // wave tile
+  constexpr int WAVES_N = BN / WN, NT = 64 * (BM / WM) * WAVES_N;
+  constexpr int TM = WM / 16, TN = WN / 16;          // 16x16 MFMA tiles per wave
+  constexpr int ACH = BM * GBK / 8;                  // 16-byte A chunks per stage
+  constexpr int APT = ACH / NT;                      // per thread
+  constexpr int NREC = BN * GBK / 32;                // weight records per stage
+  constexpr int RPT = (NREC + NT - 1) / NT;
+  static_assert(ACH % NT == 0, "A chunks must divide evenly");
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM][GLD];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN][GLD];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const uint32_t G = K / 32;
+  const uint32_t MB = (M + BM - 1) / BM, NBk = (N + BN - 1) / BN, T = MB * NBk;
+  // XCD-grouped tile order: XCD x (= id % 8) takes tiles [x*T/8, (x+1)*T/8),
+  // M-fastest, so its tiles share weight tiles
+  uint32_t t = blockIdx.x;
+  if (T % 8 == 0) t = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
+  const uint32_t nb = t / MB, mb = t % MB;
+  const uint32_t m0 = mb * BM, n0 = nb * BN;
+  // K split (gridDim.y > 1): this block runs stages [s0, s1) and writes its
+  // partial tile to ws[blockIdx.y]; smith_gemm_reduce finishes
+  const uint32_t Sall = (K + GBK - 1) / GBK;
+  const uint32_t s0 = blockIdx.y * sps < Sall ? blockIdx.y * sps : Sall;
+  const uint32_t s1 = s0 + sps < Sall ? s0 + sps : Sall;
+  const uint32_t S = s1 - s0;
+
+  u32x4 av[APT];
+  WRec wr[RPT];
+  auto load_stage = [&](uint32_t s) {
+    const uint32_t k0 = s * GBK;
+#pragma unroll
+    for (int q = 0; q < APT; q++) {
+      const uint32_t idx = tid + NT * q, row = idx >> 3, c8 = idx & 7;
+      const uint32_t m = m0 + row < M ? m0 + row : M - 1;
+      const uint32_t k = k0 + 8 * c8;
+      av[q] = k < K ? *(const u32x4*)(A16 + (size_t)m * K + k) : (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < RPT; q++) {
+      const uint32_t idx = tid + NT * q;
+      const uint32_t n = idx % BN, gi = idx / BN;
+      if (idx < NREC) wr[q] = load_wrec<FMT>(B, D, N, G, 2 * s + gi, n0 + n);
+    }
+  };
+  auto store_stage = [&](uint32_t buf) {
+#pragma unroll
+    for (int q = 0; q < APT; q++) {
+      const uint32_t idx = tid + NT * q, row = idx >> 3, c8 = idx & 7;
+      *(u32x4*)&As[buf][row][8 * c8] = av[q];
+    }
+#pragma unroll
+    for (int q = 0; q < RPT; q++) {
+      const uint32_t idx = tid + NT * q;
+      const uint32_t n = idx % BN, gi = idx / BN;
+      if (idx < NREC) {
+        uint32_t o[16];
+        dequant_wrec<FMT>(wr[q], o);
+        u32x4* dst = (u32x4*)&Bs[buf][n][32 * gi];
+#pragma unroll
+        for (int v = 0; v < 4; v++) dst[v] = (u32x4){o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]};
+      }
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  if (S > 0) {
+    load_stage(s0);
+    store_stage(0);
+  }
+  __syncthreads();
+  const uint32_t r16 = lane & 15, kq = lane >> 4;
+  for (uint32_t s = 0; s < S; s++) {
+    const uint32_t buf = s & 1;
+    if (s + 1 < S) load_stage(s0 + s + 1);
+#pragma unroll
+    for (int kk = 0; kk < GBK; kk += 32) {
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = *(const half8*)&As[buf][wm * WM + i * 16 + r16][kk + 8 * kq];
+#pragma unroll
+      for (int j = 0; j < TN; j++) bf[j] = *(const half8*)&Bs[buf][wn * WN + j * 16 + r16][kk + 8 * kq];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (s + 1 < S) store_stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane (c = lane % 16, kq) holds rows 4kq .. 4kq+3 of column c of each tile
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint32_t n = n0 + wn * WN + j * 16 + r16;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t m = m0 + wm * WM + i * 16 + 4 * kq + e;
+        float v = acc[i][j][e];
+        if (gridDim.y > 1) {
+          if (m < M && n < N) ws[((size_t)blockIdx.y * M + m) * N + n] = v;
+        } else if (epi == 2) {
+          const float u = __shfl_down(v, 1);  // column n+1 of the same row
+          if (m < M && n + 1 < N && (r16 & 1) == 0) C[(size_t)m * (N / 2) + n / 2] = silu_mul_g(v, u);
+        } else if (m < M && n < N) {
+          if (epi == 1) v += R[(size_t)m * N + n];
+          C[(size_t)m * N + n] = v;
+        }
+      }
+    }
+}
+
+#define DEF_GEMM(NAME, FMT, BM, BN)                                                                         \
+  extern "C" __global__ __launch_bounds__(64 * (BM / 64) * (BN / ((BN) >= 128 ? 64 : 32))) void NAME(      \
+      const _Float16* __restrict__ A16, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,       \
+      float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,   \
+      float* __restrict__ ws, uint32_t sps) {                                                                \
+    gemm_body<FMT, BM, BN>(A16, B, D, C, M, N, K, R, epi, ws, sps);                                          \
+  }
+
+// tiles BMxBN: m128_n64 (4 waves of 64x32), m128_n128 (4 waves), m256_n128 (8),
+// m256_n256 (16 waves); LDS (2 buffers of A and B rows) = 288 * (BM + BN) B
+#define DEF_GEMM_FMT(TAG, FMT)                                \
+  DEF_GEMM(smith_gemm_##TAG##_m128_n64, FMT, 128, 64)         \
+  DEF_GEMM(smith_gemm_##TAG##_m128_n128, FMT, 128, 128)       \
+  DEF_GEMM(smith_gemm_##TAG##_m256_n128, FMT, 256, 128)       \
+  DEF_GEMM(smith_gemm_##TAG##_m256_n256, FMT, 256, 256)
+
+DEF_GEMM_FMT(q4s, WF_Q4S)
+DEF_GEMM_FMT(q8, WF_Q8)
+DEF_GEMM_FMT(q40t, WF_Q40T)
+DEF_GEMM_FMT(q40, WF_Q40)
+
+// C = epilogue(sum over the ks K-split partials ws[0..ks) [M][N]), fixed
+// order; one thread per output (pair for SwiGLU).
+extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint32_t ks, float* __restrict__ C,
+                                             uint32_t M, uint32_t N, const float* __restrict__ R, uint32_t epi) {
+  const size_t MN = (size_t)M * N;
+  const size_t nout = epi == 2 ? MN / 2 : MN;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < nout; o += (size_t)gridDim.x * blockDim.x) {
+    if (epi == 2) {
+      const size_t i = 2 * o;  // (gate, up) at columns 2c, 2c+1 of one row
+      float g = 0.f, u = 0.f;
+      for (uint32_t y = 0; y < ks; y++) {
+        g += ws[y * MN + i];
+        u += ws[y * MN + i + 1];
+      }
+      C[o] = silu_mul_g(g, u);
+    } else {
+      float v = 0.f;
+      for (uint32_t y = 0; y < ks; y++) v += ws[y * MN + o];
+      C[o] = epi == 1 ? R[o] + v : v;
+    }
+  }
+}
+
+// A16[m][k] = f16(A[m][k] * rms_m * gamma[k]) (gamma != null: RMSNorm,
+// rmsnorm.metal:15-47) or f16(A[m][k]).  One workgroup per row, 256 threads.
+extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a(const float* __restrict__ A,
+                                                                   const float* __restrict__ gamma, float eps,
+                                                                   _Float16* __restrict__ A16, uint32_t K) {
+  __shared__ float red[4];
+  const uint32_t m = blockIdx.x, tid = threadIdx.x;
+  const float* a = A + (size_t)m * K;
+  float rms = 1.f;
+  if (gamma) {
+    float ss = 0.f;
+    for (uint32_t k = 4 * tid; k < K; k += 1024) {
+      const float4 v = *(const float4*)(a + k);
+      ss = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, ss))));
+    }
+    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    rms = 1.0f / __builtin_sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
+  }
+  for (uint32_t k = 4 * tid; k < K; k += 1024) {
+    float4 v = *(const float4*)(a + k);
+    if (gamma) {
+      const float4 g = *(const float4*)(gamma + k);
+      v = make_float4(v.x * rms * g.x, v.y * rms * g.y, v.z * rms * g.z, v.w * rms * g.w);
+    }
+    uint2 o;
+    o.x = pack_h2(v.x, v.y);
+    o.y = pack_h2(v.z, v.w);
+    *(uint2*)(A16 + (size_t)m * K + k) = o;
+  }
+}

@@ -56,6 +56,8 @@ struct Ctx {
   size_t counters_n = 0;
   void* normbuf = nullptr;
   size_t normbuf_bytes = 0;
+  void* a16 = nullptr;  // f16 activations of the GEMM path
+  size_t a16_bytes = 0;
   void* att_ws = nullptr;
   size_t att_ws_bytes = 0;
   uint32_t* att_cnt = nullptr;
@@ -302,11 +304,63 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
 }
 
+// M >= GEMM_MIN_M: f16 activations (RMSNorm fused into their conversion),
+// weights dequantized to f16 in LDS, MFMA GEMM with f32 accumulation.
+const uint32_t GEMM_MIN_M = 64;
+
+int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M, uint32_t N,
+         uint32_t K, const Epi& ep) {
+  if (ensure(c, &c->a16, &c->a16_bytes, (size_t)M * K * 2)) return -1;
+  {
+    const float* pa = a;
+    const float* pg = ep.gamma;
+    float pe = ep.eps;
+    void* pd = c->a16;
+    uint32_t pK = K;
+    void* args[] = {&pa, &pg, &pe, &pd, &pK};
+    if (launch(c, "smith_gemm_prep_a", dim3(M), dim3(256), args)) return -1;
+  }
+  // tile choice: the biggest tile that still gives about one tile per CU
+  // (bigger tiles carry more MFMA work per K stage to cover load latency);
+  // small grids split K across workgroups (partials reduced after)
+  auto ntiles = [&](uint32_t bm, uint32_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  uint32_t bm = 128, bn = 64;
+  if (ntiles(256, 256) >= 256) bm = 256, bn = 256;
+  else if (ntiles(256, 128) >= 200) bm = 256, bn = 128;
+  else if (ntiles(128, 128) >= 256) bm = 128, bn = 128;
+  const uint32_t tiles = ntiles(bm, bn);
+  const uint32_t S = (K + 63) / 64;
+  uint32_t ks = 1;
+  if (bm == 128 && bn == 64 && tiles < 512) ks = std::min<uint32_t>((512 + tiles - 1) / tiles, std::max<uint32_t>(1, S / 8));
+  const uint32_t sps = (S + ks - 1) / ks;
+  ks = (S + sps - 1) / sps;
+  if (ks > 1 && ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ks * M * N * sizeof(float))) return -1;
+  const uint32_t threads = 64 * (bm / 64) * (bn / (bn >= 128 ? 64 : 32));
+  char name[64];
+  snprintf(name, sizeof name, "smith_gemm_%s_m%u_n%u", fmt_tag(fmt), bm, bn);
+  const void* pA = c->a16;
+  const void* pB = B;
+  const void* pD = D;
+  float* pC = out;
+  uint32_t pM = M, pN = N, pK = K, pepi = ep.mode, psps = sps;
+  const float* pR = ep.resid;
+  float* pws = c->ws;
+  void* args[] = {&pA, &pB, &pD, &pC, &pM, &pN, &pK, &pR, &pepi, &pws, &psps};
+  if (launch(c, name, dim3(tiles, ks), dim3(threads), args)) return -1;
+  if (ks == 1) return 0;
+  const float* cws = c->ws;
+  uint32_t pks = ks;
+  void* rargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi};
+  size_t nout = (size_t)M * N / (ep.mode == 2 ? 2 : 1);
+  return launch(c, "smith_gemm_reduce", dim3((unsigned)std::min<size_t>((nout + 255) / 256, 65536)), dim3(256), rargs);
+}
+
 int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
             uint32_t N, uint32_t K, uint32_t G, const Epi& ep = Epi()) {
   if (set_device(c)) return -1;
   if (M == 0 || N == 0) return 0;
   if (ep.mode == 2 && N % 2) return fail(c, "smith: SwiGLU epilogue needs an even column count (got %u)", N);
+  if (M >= GEMM_MIN_M && K % 32 == 0) return gemm(c, fmt, a, B, D, out, M, N, K, ep);
   const uint32_t nout = ep.mode == 2 ? N / 2 : N;
   for (uint32_t m0 = 0; m0 < M; m0 += 32) {
     uint32_t mc = std::min<uint32_t>(32, M - m0);
@@ -373,6 +427,7 @@ void smith_destroy(void* ctx) {
   }
   if (c->prep) hipFree(c->prep);
   if (c->normbuf) hipFree(c->normbuf);
+  if (c->a16) hipFree(c->a16);
   if (c->att_ws) hipFree(c->att_ws);
   if (c->att_cnt) hipFree(c->att_cnt);
   if (c->ws) hipFree(c->ws);

@@ -14,6 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsmith.so")
 CODE_OBJECT_PATH = os.path.join(_HERE, "lib", "smith_kernels.hsaco")
 LLAMA_CODE_OBJECT_PATH = os.path.join(_HERE, "lib", "smith_llama.hsaco")
+GEMM_CODE_OBJECT_PATH = os.path.join(_HERE, "lib", "smith_gemm.hsaco")
 
 SHARED = 0
 PRIVATE = 1
@@ -164,9 +165,10 @@ def shader_lib():
             raise RuntimeError("smith: failed to load code object at %s: %s"
                                % (CODE_OBJECT_PATH, lib.smith_last_error(c).decode()))
         _library = lp
-        if not lib.smith_load_library(c, LLAMA_CODE_OBJECT_PATH.encode()):
-            raise RuntimeError("smith: failed to load code object at %s: %s"
-                               % (LLAMA_CODE_OBJECT_PATH, lib.smith_last_error(c).decode()))
+        for path in (LLAMA_CODE_OBJECT_PATH, GEMM_CODE_OBJECT_PATH):
+            if not lib.smith_load_library(c, path.encode()):
+                raise RuntimeError("smith: failed to load code object at %s: %s"
+                                   % (path, lib.smith_last_error(c).decode()))
     return _library
 
 

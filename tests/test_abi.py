@@ -56,6 +56,12 @@ def test_code_object_has_kernels():
         need += ["smith_qgemv1_%s_m1_k%d_c2" % (fmt, k) for k in (96, 128)]
     for k in need:
         assert re.search(r"\b%s\.kd\b" % k, out), k
+    out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.GEMM_CODE_OBJECT_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    for k in ["smith_gemm_prep_a", "smith_gemm_reduce"] + [
+            "smith_gemm_%s_m%d_n%d" % (f, m, n) for f in ("q4s", "q8", "q40", "q40t")
+            for (m, n) in ((128, 64), (128, 128), (256, 128), (256, 256))]:
+        assert re.search(r"\b%s\.kd\b" % k, out), k
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_attention_part", "smith_kv_append", "smith_attention_cached",

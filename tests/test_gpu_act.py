@@ -103,7 +103,7 @@ def test_tiles_repack_layout_and_interleave():
     assert device.lib.smith_repack_q4_0_t_into(ctx, src, nib, dsc, N, K, 0, 1, 40) != 0
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 17])
+@pytest.mark.parametrize("M", [1, 2, 3, 17, 70, 200])
 def test_linear_t_all_epilogues(M):
     N, K = 160, 320
     _, nib, dsc, wd = _q4_0(N, K, 11)
@@ -121,7 +121,7 @@ def test_linear_t_all_epilogues(M):
         if epi == 2:
             y = np.stack([_silu_mul(y[m]) for m in range(M)])
         got = _get(ob, y.size).reshape(y.shape)
-        tol = (TOL_SWIGLU if epi == 2 else TOL) if M <= 8 else 1e-3
+        tol = (TOL_SWIGLU if epi == 2 else TOL) if M <= 8 else (1e-3 if M < 64 else 1e-2)  # M >= 64: f16 MFMA GEMM
         assert O.normwise_rel_err(got, y) <= tol, (M, epi)
 
 
