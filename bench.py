@@ -74,22 +74,46 @@ class Weights:
         D.sync()
 
 
-def time_steps(D, step, steps, warmup):
+def time_steps(D, step, steps, warmup, rotation=1, graph=False):
     """ms per step over `steps` back-to-back calls, HIP events on the library
     stream around the whole timed region, and the number of kernel launches
-    one step makes (counted in a separate, untimed pass)."""
+    one step makes (counted in a separate, untimed pass).  graph=True: one
+    weight rotation of steps (`rotation` calls, each its own launches with
+    its own weight copy) is captured once as a HIP graph and the graph is
+    replayed until `steps` steps ran (launch-bound loops go through graphs)."""
     for i in range(warmup):
         step(i)
     D.sync()
+    g = None
+    if graph:
+        D.check(D.lib.smith_graph_begin(D.ops_ctx()), "graph begin")
+        try:
+            for i in range(rotation):
+                step(i)
+        finally:
+            g = D.lib.smith_graph_end(D.ops_ctx())
+        if not g:
+            D.check(-1, "graph end")
+        D.check(D.lib.smith_graph_launch(D.ops_ctx(), g), "graph launch")  # warm
+        D.sync()
     D.timer_start()
-    for i in range(steps):
-        step(i)
+    if g is not None:
+        reps = -(-steps // rotation)
+        for _ in range(reps):
+            D.check(D.lib.smith_graph_launch(D.ops_ctx(), g), "graph launch")
+        ran = reps * rotation
+    else:
+        for i in range(steps):
+            step(i)
+        ran = steps
     ms = D.timer_stop()
+    if g is not None:
+        D.lib.smith_graph_destroy(g)
     D.profile_kernels(True)
     step(0)
     _, launches = D.profile_read("")
     D.profile_kernels(False)
-    return ms / steps, {"launches_per_step": launches}
+    return ms / ran, {"launches_per_step": launches, "steps_timed": ran, "graph": g is not None}
 
 
 _Q4S_CACHE = {}
@@ -102,7 +126,7 @@ def q4s_weights(D, S, prng, K, N):
     return _Q4S_CACHE[(K, N)]
 
 
-def bench_q4s(D, S, prng, M, K, N, steps, warmup):
+def bench_q4s(D, S, prng, M, K, N, steps, warmup, graph=False):
     W = q4s_weights(D, S, prng, K, N)
     a = S.tensor(prng.randn((M, K), 0))
     out = S.create([M, N])
@@ -113,7 +137,7 @@ def bench_q4s(D, S, prng, M, K, N, steps, warmup):
     def step(i):
         D.lib.smith_matmul_q4(ctx, a.buffer, bufs[i % len(bufs)], out.buffer, M, N, K, G)
 
-    ms, kt = time_steps(D, step, steps, warmup)
+    ms, kt = time_steps(D, step, steps, warmup, rotation=len(bufs), graph=graph)
     return ms, kt, alg_bytes(q4s_bytes(K, N), M, K, N)
 
 
@@ -154,6 +178,37 @@ def bench_q40(D, S, prng, M, K, N, steps, warmup):
 
     ms, kt = time_steps(D, step, steps, warmup)
     return ms, kt, alg_bytes(q40_bytes(K, N), M, K, N)
+
+
+def bench_cfg4(D, S, prng, steps=5):
+    """Config 4: matmulQ4 at M in {512, 2048} on the MFMA GEMM path.  TFLOP/s
+    per step (activation prep + GEMM [+ K-split reduce]) and of the GEMM
+    kernel alone (per-launch HIP events of the smith_gemm_q4s_* launches)."""
+    pre = {}
+    for (Nn, Kk) in [(14336, 4096), (4096, 14336)]:
+        for M in (512, 2048):
+            msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, steps, 1)
+            fl = 2.0 * M * Nn * Kk
+            W = q4s_weights(D, S, prng, Kk, Nn)
+            a = S.tensor(prng.randn((M, Kk), 0))
+            out = S.create([M, Nn])
+            D.profile_kernels(True)
+            for i in range(steps):
+                D.lib.smith_matmul_q4(D.ops_ctx(), a.buffer, W.bufs[i % len(W.bufs)], out.buffer, M, Nn, Kk,
+                                      (Kk + 31) // 32)
+            kms, kn = D.profile_read("smith_gemm_q4s")
+            D.profile_read("")  # drop the other records (activation prep, reduce)
+            D.profile_kernels(False)
+            kus = kms * 1e3 / max(kn, 1)
+            pre["M%d_N%d_K%d" % (M, Nn, Kk)] = {
+                "TFLOPs_step": round(fl / msx / 1e9, 2),
+                "mfma_util_vs_f16_dense": round(fl / msx / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
+                "ms_step": round(msx, 3), "kernels_per_step": ktx["launches_per_step"],
+                "gemm_kernel_us": round(kus, 1), "gemm_kernel_TFLOPs": round(fl / kus / 1e6, 1),
+                "gemm_kernel_mfma_util": round(fl / kus / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
+                "path": "f16 activation prep + MFMA GEMM (Q4S dequantized to f16 in LDS, f32 accumulation)"}
+            log("cfg4 M=%d N=%d K=%d:" % (M, Nn, Kk), pre["M%d_N%d_K%d" % (M, Nn, Kk)])
+    return pre
 
 
 def cpu_baseline(K, N, budget_s):
@@ -234,10 +289,11 @@ def calibrate(D, steps):
                 D.lib.smith_set_bytes(enc, prm, 8, 1)
                 D.lib.smith_set_buffer(enc, out, 2)
                 D.lib.smith_dispatch(enc, 1024 * 256, 1, 1, 256, 1, 1)
-                D.lib.smith_wait(D.lib.smith_end_async(enc))
+                D.lib.smith_end_async(enc)  # back to back: no wait per launch
 
             for i in range(5):
                 launch(i)
+            D.sync()
             D.timer_start()
             for i in range(steps):
                 launch(i)
@@ -298,6 +354,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate", action="store_true", help="print the platform floor (empty kernel, streaming read)")
     ap.add_argument("--e2e-only", action="store_true", help="only the config-5 end-to-end decode")
+    ap.add_argument("--cfg4-only", action="store_true", help="only the config-4 prefill GEMMs")
     ap.add_argument("--gguf", default="/tmp/smith_config5.gguf", help="synthetic config-5 GGUF path (written if absent)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -317,14 +374,21 @@ def main():
     if args.e2e_only:
         print(json.dumps({"cfg5_e2e": bench_e2e(D, args.gguf)}), flush=True)
         return
+    if args.cfg4_only:
+        print(json.dumps({"cfg4_q4s_prefill": bench_cfg4(D, S, prng)}), flush=True)
+        return
     K = N = 4096
+    # back-to-back stream launches (the value); the same steps replayed from a
+    # captured HIP graph reported beside them
     ms, kt, nbytes = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup)
+    ms_graph, _, _ = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup, graph=True)
     assert kt["launches_per_step"] == 1, kt  # the M=1 path is one fused kernel
     value = nbytes / (ms * 1e-3) / 1e9
     # one kernel per step: the timed-region average is that kernel's average
-    # launch duration (including any gap between back-to-back launches)
+    # launch-to-launch duration (including the gap between back-to-back launches)
     achieved = value
-    log("cfg1 q4s M=1: %.2f us/step = %.0f GB/s (%d kernel/step)" % (ms * 1e3, value, kt["launches_per_step"]))
+    log("cfg1 q4s M=1: %.2f us/step = %.0f GB/s stream, %.2f us/step graph (%d kernel/step)"
+        % (ms * 1e3, value, ms_graph * 1e3, kt["launches_per_step"]))
 
     configs = {}
     if not args.quick:
@@ -346,16 +410,7 @@ def main():
                     "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
         configs["cfg3_q4s_batched_decode"] = sweep
         log("cfg3:", json.dumps(sweep))
-        pre = {}
-        for (Nn, Kk) in [(14336, 4096), (4096, 14336)]:
-            for M in (512, 2048):
-                msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, 3, 1)
-                fl = 2.0 * M * Nn * Kk
-                pre["M%d_N%d_K%d" % (M, Nn, Kk)] = {"TFLOPs_step": round(fl / msx / 1e9, 2),
-                                                   "mfma_util_vs_f16_dense": round(fl / msx / 1e9 / MFMA_F16_PEAK_TFLOPS, 4),
-                                                   "ms_step": round(msx, 3),
-                                                   "path": "f16 activation prep + MFMA GEMM (Q4S dequantized "
-                                                           "to f16 in LDS, f32 accumulation)"}
+        pre = bench_cfg4(D, S, prng)
         configs["cfg4_q4s_prefill"] = pre
         log("cfg4:", json.dumps(pre))
 
@@ -377,6 +432,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
+        "ms_per_step_graph_replay": round(ms_graph, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -384,7 +440,8 @@ def main():
         "data": "synthetic (SplitMix64/Box-Muller seeded: a~N(0,1) seed 0, W~N(0,0.02) seed 1)",
         "config": {"workload": "config 1: matmulQ4 GEMV M=1, Smith weight [K=4096, N=4096] quantizeQ4 (Q4S, "
                                "24 B/32 weights); weights rotated over >= 400 MB of copies",
-                   "M": 1, "K": K, "N": N, "format": "Q4S", "algorithmic_bytes_per_step": nbytes},
+                   "M": 1, "K": K, "N": N, "format": "Q4S", "algorithmic_bytes_per_step": nbytes,
+                   "timing": "HIP events around %d back-to-back stream launches" % kt["steps_timed"]},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1,
