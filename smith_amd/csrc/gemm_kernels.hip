@@ -12,8 +12,11 @@
 // are in flight in registers; they are dequantized and stored after the
 // MFMAs.  Big tiles give each stage enough MFMA work (0.86 us for 256x256)
 // to cover the loads' latency.  A wave owns a 64x64 (64x32 for BN=64) part
-// of the tile as 16x16 MFMA tiles.  LDS rows hold 64 K values + 8 halves of
-// padding (144 B stride); LDS 288 * (BM + BN) bytes (147 KB at 256x256).
+// of the tile as 16x16 MFMA tiles.  LDS rows hold 64 K values; their 16-byte
+// chunks are XOR-swizzled by the row (128 B stride, 256 * (BM + BN) bytes of
+// LDS) for the smaller tiles, and rows are padded by 8 halves instead (144 B
+// stride, 288 * (BM + BN) = 147 KB) at 256x256, where measured the swizzle
+// did not pay.
 // Dequantization (exact products, one f16 rounding per weight):
 //   Q4S   w = scale * (nib - zero)   record (g,n) 24 B  (shaders/matmul_q4.metal:24-28)
 //   Q8    w = f32(d) * int8          record (g,n) 34 B  (shaders/matmul_q8.metal:40-52)
@@ -114,14 +117,22 @@ __device__ __forceinline__ void dequant_wrec(const WRec& r, uint32_t (&o)[16]) {
   }
 }
 
+// 16-byte chunk position of chunk c (0..7) of LDS row r: with padded rows
+// (LD > 64) the identity; unpadded rows (LD == 64) XOR-swizzle the chunk by
+// the row so the 16-row MFMA operand reads and the row-wise stores spread
+// over the banks
+template <int LD>
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) {
+  return LD == 64 ? (c ^ (r & 7)) : c;
+}
+
 __device__ __forceinline__ float silu_mul_g(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
-template <int FMT, int BM, int BN>
+template <int FMT, int BM, int BN, int WM, int WN, int LD = GLD>
 __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, const uint8_t* __restrict__ B,
                                          const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t M,
                                          uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,
                                          float* __restrict__ ws, uint32_t sps) {
-  constexpr int WM = 64, WN = BN >= 128 ? 64 : 32;  // wave tile
   constexpr int WAVES_N = BN / WN, NT = 64 * (BM / WM) * WAVES_N;
   constexpr int TM = WM / 16, TN = WN / 16;          // 16x16 MFMA tiles per wave
   constexpr int ACH = BM * GBK / 8;                  // 16-byte A chunks per stage
@@ -129,8 +140,8 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
   constexpr int NREC = BN * GBK / 32;                // weight records per stage
   constexpr int RPT = (NREC + NT - 1) / NT;
   static_assert(ACH % NT == 0, "A chunks must divide evenly");
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM][GLD];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN][GLD];
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM][LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN][LD];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -149,29 +160,31 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
   const uint32_t s1 = s0 + sps < Sall ? s0 + sps : Sall;
   const uint32_t S = s1 - s0;
 
-  u32x4 av[APT];
-  WRec wr[RPT];
-  auto load_stage = [&](uint32_t s) {
+  struct Regs {
+    u32x4 av[APT];
+    WRec wr[RPT];
+  };
+  auto load_stage = [&](Regs& rg, uint32_t s) {
     const uint32_t k0 = s * GBK;
 #pragma unroll
     for (int q = 0; q < APT; q++) {
       const uint32_t idx = tid + NT * q, row = idx >> 3, c8 = idx & 7;
       const uint32_t m = m0 + row < M ? m0 + row : M - 1;
       const uint32_t k = k0 + 8 * c8;
-      av[q] = k < K ? *(const u32x4*)(A16 + (size_t)m * K + k) : (u32x4){0u, 0u, 0u, 0u};
+      rg.av[q] = k < K ? *(const u32x4*)(A16 + (size_t)m * K + k) : (u32x4){0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int q = 0; q < RPT; q++) {
       const uint32_t idx = tid + NT * q;
       const uint32_t n = idx % BN, gi = idx / BN;
-      if (idx < NREC) wr[q] = load_wrec<FMT>(B, D, N, G, 2 * s + gi, n0 + n);
+      if (idx < NREC) rg.wr[q] = load_wrec<FMT>(B, D, N, G, 2 * s + gi, n0 + n);
     }
   };
-  auto store_stage = [&](uint32_t buf) {
+  auto store_stage = [&](const Regs& rg, uint32_t buf) {
 #pragma unroll
     for (int q = 0; q < APT; q++) {
       const uint32_t idx = tid + NT * q, row = idx >> 3, c8 = idx & 7;
-      *(u32x4*)&As[buf][row][8 * c8] = av[q];
+      *(u32x4*)&As[buf][row][8 * swz<LD>(row, c8)] = rg.av[q];
     }
 #pragma unroll
     for (int q = 0; q < RPT; q++) {
@@ -179,10 +192,10 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
       const uint32_t n = idx % BN, gi = idx / BN;
       if (idx < NREC) {
         uint32_t o[16];
-        dequant_wrec<FMT>(wr[q], o);
-        u32x4* dst = (u32x4*)&Bs[buf][n][32 * gi];
+        dequant_wrec<FMT>(rg.wr[q], o);
 #pragma unroll
-        for (int v = 0; v < 4; v++) dst[v] = (u32x4){o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]};
+        for (int v = 0; v < 4; v++)
+          *(u32x4*)&Bs[buf][n][8 * swz<LD>(n, 4 * gi + v)] = (u32x4){o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]};
       }
     }
   };
@@ -193,28 +206,39 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  if (S > 0) {
-    load_stage(s0);
-    store_stage(0);
-  }
-  __syncthreads();
   const uint32_t r16 = lane & 15, kq = lane >> 4;
-  for (uint32_t s = 0; s < S; s++) {
-    const uint32_t buf = s & 1;
-    if (s + 1 < S) load_stage(s0 + s + 1);
+  auto mfma_stage = [&](uint32_t buf) {
 #pragma unroll
     for (int kk = 0; kk < GBK; kk += 32) {
       half8 af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; i++) af[i] = *(const half8*)&As[buf][wm * WM + i * 16 + r16][kk + 8 * kq];
+      for (int i = 0; i < TM; i++) {
+        const uint32_t row = wm * WM + i * 16 + r16;
+        af[i] = *(const half8*)&As[buf][row][8 * swz<LD>(row, kk / 8 + kq)];
+      }
 #pragma unroll
-      for (int j = 0; j < TN; j++) bf[j] = *(const half8*)&Bs[buf][wn * WN + j * 16 + r16][kk + 8 * kq];
+      for (int j = 0; j < TN; j++) {
+        const uint32_t row = wn * WN + j * 16 + r16;
+        bf[j] = *(const half8*)&Bs[buf][row][8 * swz<LD>(row, kk / 8 + kq)];
+      }
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (s + 1 < S) store_stage(buf ^ 1);
+  };
+
+  Regs r0;
+  if (S > 0) {
+    load_stage(r0, s0);
+    store_stage(r0, 0);
+  }
+  __syncthreads();
+  for (uint32_t s = 0; s < S; s++) {
+    const uint32_t buf = s & 1;
+    if (s + 1 < S) load_stage(r0, s0 + s + 1);
+    mfma_stage(buf);
+    if (s + 1 < S) store_stage(r0, buf ^ 1);
     __syncthreads();
   }
 
@@ -241,21 +265,21 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
     }
 }
 
-#define DEF_GEMM(NAME, FMT, BM, BN)                                                                         \
-  extern "C" __global__ __launch_bounds__(64 * (BM / 64) * (BN / ((BN) >= 128 ? 64 : 32))) void NAME(      \
+#define DEF_GEMM(NAME, FMT, BM, BN, WM, WN, ...)                                                        \
+  extern "C" __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void NAME(                            \
       const _Float16* __restrict__ A16, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,       \
       float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,   \
       float* __restrict__ ws, uint32_t sps) {                                                                \
-    gemm_body<FMT, BM, BN>(A16, B, D, C, M, N, K, R, epi, ws, sps);                                          \
+    gemm_body<FMT, BM, BN, WM, WN, ##__VA_ARGS__>(A16, B, D, C, M, N, K, R, epi, ws, sps);            \
   }
 
 // tiles BMxBN: m128_n64 (4 waves of 64x32), m128_n128 (4 waves), m256_n128 (8),
-// m256_n256 (16 waves); LDS (2 buffers of A and B rows) = 288 * (BM + BN) B
-#define DEF_GEMM_FMT(TAG, FMT)                                \
-  DEF_GEMM(smith_gemm_##TAG##_m128_n64, FMT, 128, 64)         \
-  DEF_GEMM(smith_gemm_##TAG##_m128_n128, FMT, 128, 128)       \
-  DEF_GEMM(smith_gemm_##TAG##_m256_n128, FMT, 256, 128)       \
-  DEF_GEMM(smith_gemm_##TAG##_m256_n256, FMT, 256, 256)
+// m256_n256 (16 waves); LDS holds 2 buffers of A and B rows
+#define DEF_GEMM_FMT(TAG, FMT)                                             \
+  DEF_GEMM(smith_gemm_##TAG##_m128_n64, FMT, 128, 64, 64, 32, 64)           \
+  DEF_GEMM(smith_gemm_##TAG##_m128_n128, FMT, 128, 128, 64, 64, 64)         \
+  DEF_GEMM(smith_gemm_##TAG##_m256_n128, FMT, 256, 128, 64, 64, 64)         \
+  DEF_GEMM(smith_gemm_##TAG##_m256_n256, FMT, 256, 256, 64, 64)
 
 DEF_GEMM_FMT(q4s, WF_Q4S)
 DEF_GEMM_FMT(q8, WF_Q8)
