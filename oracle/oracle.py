@@ -17,8 +17,18 @@ _lib = None
 Q4S_BYTES = 24
 Q8_BYTES = 34
 Q4_0_BYTES = 18
+GGML_F32 = 0
+GGML_F16 = 1
 GGML_Q4_0 = 2
+GGML_Q4_1 = 3
+GGML_Q5_0 = 6
 GGML_Q8_0 = 8
+GGML_Q4_K = 12
+GGML_Q6_K = 14
+GGML_BF16 = 30
+# (elements, bytes) per block, src/gguf.js:30-41
+BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_BF16: (1, 2), GGML_Q4_0: (32, 18), GGML_Q4_1: (32, 20),
+         GGML_Q5_0: (32, 22), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
 
 
 def build():
@@ -43,6 +53,10 @@ def lib():
             ("oracle_dequant_q8", [P, I, I, P], None),
             ("oracle_dequant_q4_0_block", [P, P], None),
             ("oracle_dequant_q8_0_block", [P, P], None),
+            ("oracle_dequant_q4_1_block", [P, P], None),
+            ("oracle_dequant_q5_0_block", [P, P], None),
+            ("oracle_dequant_q4_k_block", [P, P], None),
+            ("oracle_dequant_q6_k_block", [P, P], None),
             ("oracle_dequantize_tensor", [ctypes.c_int, P, I, P], ctypes.c_int),
             ("oracle_quantize_rows", [ctypes.c_int, P, I, I, P], ctypes.c_int),
             ("oracle_matmul_f64acc", [P, P, I, I, I, P], None),
@@ -132,8 +146,36 @@ def dequant_q8_0_block(blk):
     return out
 
 
+def _block(fn, n, blk):
+    blk = np.ascontiguousarray(blk, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    getattr(lib(), fn)(_p(blk), _p(out))
+    return out
+
+
+def dequant_q4_1_block(blk):
+    """dequantQ4_1, src/gguf.js:203-215."""
+    return _block("oracle_dequant_q4_1_block", 32, blk)
+
+
+def dequant_q5_0_block(blk):
+    """dequantQ5_0, src/gguf.js:238-259."""
+    return _block("oracle_dequant_q5_0_block", 32, blk)
+
+
+def dequant_q4_k_block(blk):
+    """dequantQ4_K, src/gguf.js:264-305."""
+    return _block("oracle_dequant_q4_k_block", 256, blk)
+
+
+def dequant_q6_k_block(blk):
+    """dequantQ6_K, src/gguf.js:309-339."""
+    return _block("oracle_dequant_q6_k_block", 256, blk)
+
+
 def dequantize_tensor(ggml_type, data, numel):
-    """dequantizeTensor, src/gguf.js:343-394 (Q4_0 / Q8_0)."""
+    """dequantizeTensor, src/gguf.js:343-394 (F32, F16, BF16, Q4_0, Q4_1,
+    Q5_0, Q8_0, Q4_K, Q6_K)."""
     data = np.ascontiguousarray(data, dtype=np.uint8)
     out = np.empty(numel, dtype=np.float32)
     if lib().oracle_dequantize_tensor(ggml_type, _p(data), numel, _p(out)):
@@ -142,11 +184,13 @@ def dequantize_tensor(ggml_type, data, numel):
 
 
 def quantize_rows(ggml_type, x):
-    """GGUF Q4_0/Q8_0 encoder (ggml reference rounding, interleaved nibbles)."""
+    """GGUF block encoder for this build's synthetic files, row by row
+    (Q4_0/Q8_0/Q4_1/Q5_0: ggml reference rounding; Q4_K/Q6_K: this build's
+    rounding), packed in the order the reference's decoders read."""
     x = _f32(x)
     rows, cols = x.shape
-    bpb = Q4_0_BYTES if ggml_type == GGML_Q4_0 else Q8_BYTES
-    out = np.zeros(rows * ((cols + 31) // 32) * bpb, dtype=np.uint8)
+    be, bpb = BLOCK[ggml_type]
+    out = np.zeros(rows * ((cols + be - 1) // be) * bpb, dtype=np.uint8)
     if lib().oracle_quantize_rows(ggml_type, _p(x), rows, cols, _p(out)):
         raise ValueError("unsupported type %d" % ggml_type)
     return out

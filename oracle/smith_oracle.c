@@ -250,21 +250,131 @@ void oracle_dequant_q8_0_block(const uint8_t* blk, float* out32) {
   }
 }
 
-/* dequantizeTensor, src/gguf.js:343-394, for Q4_0 (type 2) and Q8_0 (type 8):
- * blocks in storage order along the flat tensor; the last block is cut at
- * numElements. */
+/* dequantQ4_1, src/gguf.js:203-215: f16 d, f16 m, 16 nibble bytes
+ * (interleaved order as Q4_0); value = d * nibble + m in f64, stored f32. */
+void oracle_dequant_q4_1_block(const uint8_t* blk, float* out32) {
+  double d = oracle_from_f16((uint16_t)(blk[0] | (blk[1] << 8)));
+  double m = oracle_from_f16((uint16_t)(blk[2] | (blk[3] << 8)));
+  for (int i = 0; i < 32; i++) {
+    uint8_t b = blk[4 + (i >> 1)];
+    int nib = (i & 1) ? (b >> 4) : (b & 0x0f);
+    out32[i] = (float)(d * (double)nib + m);
+  }
+}
+
+/* dequantQ5_0, src/gguf.js:238-259: f16 d, a 32-bit little-endian word of
+ * fifth bits (bit i for element i), 16 nibble bytes (interleaved order);
+ * value = d * ((nibble | bit << 4) - 16) in f64, stored f32. */
+void oracle_dequant_q5_0_block(const uint8_t* blk, float* out32) {
+  double d = oracle_from_f16((uint16_t)(blk[0] | (blk[1] << 8)));
+  uint32_t hb = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+  for (int i = 0; i < 32; i++) {
+    uint8_t b = blk[6 + (i >> 1)];
+    int nib = (i & 1) ? (b >> 4) : (b & 0x0f);
+    int q = nib | (int)(((hb >> i) & 1u) << 4);
+    out32[i] = (float)(d * (double)(q - 16));
+  }
+}
+
+/* The 6-bit (scale, min) pair of sub-block i of a Q4_K super-block as the
+ * reference unpacks it (src/gguf.js:281-291): i < 4: low 6 bits of bytes i
+ * and i+4; i >= 4: scale = (byte[i-4] >> 6) | (low nibble of byte[i+4]) << 2,
+ * min = (byte[i] >> 6) | (high nibble of byte[i+4]) << 2.  (The bit order of
+ * the i >= 4 case differs from llama.cpp's get_scale_min_k4; the reference's
+ * is the one restated.) */
+void oracle_q4_k_scale_min(const uint8_t* sc12, int i, int* sc, int* mn) {
+  if (i < 4) {
+    *sc = sc12[i] & 0x3f;
+    *mn = sc12[4 + i] & 0x3f;
+  } else {
+    *sc = (sc12[i - 4] >> 6) | ((sc12[i + 4] & 0x0f) << 2);
+    *mn = (sc12[i] >> 6) | ((sc12[i + 4] >> 4) << 2);
+  }
+}
+
+/* dequantQ4_K, src/gguf.js:264-305: 256 elements; f16 d, f16 dmin, 12 bytes
+ * of packed 6-bit scales/mins, 128 nibble bytes with element j in byte j>>1
+ * (low nibble if j even).  sc = f32(d * scale), mn = f32(dmin * min)
+ * (Float32Array stores); value = sc * nibble - mn in f64, stored f32. */
+void oracle_dequant_q4_k_block(const uint8_t* blk, float* out256) {
+  double d = oracle_from_f16((uint16_t)(blk[0] | (blk[1] << 8)));
+  double dmin = oracle_from_f16((uint16_t)(blk[2] | (blk[3] << 8)));
+  float sc[8], mn[8];
+  for (int i = 0; i < 8; i++) {
+    int s, m;
+    oracle_q4_k_scale_min(blk + 4, i, &s, &m);
+    sc[i] = (float)(d * s);
+    mn[i] = (float)(dmin * m);
+  }
+  for (int j = 0; j < 256; j++) {
+    uint8_t b = blk[16 + (j >> 1)];
+    int nib = (j & 1) ? (b >> 4) : (b & 0x0f);
+    out256[j] = (float)((double)sc[j >> 5] * nib - (double)mn[j >> 5]);
+  }
+}
+
+/* dequantQ6_K, src/gguf.js:309-339: 256 elements; ql[128] (element j: nibble
+ * of byte j>>1, low if j even), qh[64] (element j: bits (j&3)*2.. of byte
+ * j>>2), int8 scales[16] (one per 16 elements), f16 d at byte 208;
+ * value = d * scale * (q - 32) evaluated left to right in f64, stored f32. */
+void oracle_dequant_q6_k_block(const uint8_t* blk, float* out256) {
+  double d = oracle_from_f16((uint16_t)(blk[208] | (blk[209] << 8)));
+  for (int j = 0; j < 256; j++) {
+    uint8_t lb = blk[j >> 1];
+    int ql = (j & 1) ? (lb >> 4) : (lb & 0x0f);
+    int qh = (blk[128 + (j >> 2)] >> ((j & 3) * 2)) & 3;
+    int q = ql | (qh << 4);
+    int sc = (int8_t)blk[192 + (j >> 4)];
+    out256[j] = (float)(d * (double)sc * (double)(q - 32));
+  }
+}
+
+/* GGML type numbers (src/gguf.js:15-25) and block geometry (:30-41). */
+int oracle_block_geometry(int type, int* elems, int* bytes) {
+  switch (type) {
+    case 0: *elems = 1; *bytes = 4; return 0;     /* F32 */
+    case 1: *elems = 1; *bytes = 2; return 0;     /* F16 */
+    case 30: *elems = 1; *bytes = 2; return 0;    /* BF16 */
+    case 2: *elems = 32; *bytes = 18; return 0;   /* Q4_0 */
+    case 3: *elems = 32; *bytes = 20; return 0;   /* Q4_1 */
+    case 6: *elems = 32; *bytes = 22; return 0;   /* Q5_0 */
+    case 8: *elems = 32; *bytes = 34; return 0;   /* Q8_0 */
+    case 12: *elems = 256; *bytes = 144; return 0; /* Q4_K */
+    case 14: *elems = 256; *bytes = 210; return 0; /* Q6_K */
+    default: return -1;
+  }
+}
+
+/* dequantizeTensor, src/gguf.js:343-394: F32 as stored, F16 by fromFloat16,
+ * BF16 by a 16-bit shift, block types block by block in storage order along
+ * the flat tensor with the last block cut at numElements. */
 int oracle_dequantize_tensor(int type, const uint8_t* data, int64_t numel, float* out) {
-  int bpb;
-  void (*fn)(const uint8_t*, float*);
-  if (type == 2) { bpb = Q4_0_BYTES; fn = oracle_dequant_q4_0_block; }
-  else if (type == 8) { bpb = Q8_BYTES; fn = oracle_dequant_q8_0_block; }
-  else return -1;
-  int64_t blocks = (numel + 31) / 32;
-  float tmp[32];
+  int be, bb;
+  if (oracle_block_geometry(type, &be, &bb)) return -1;
+  if (type == 0) { memcpy(out, data, (size_t)numel * 4); return 0; }
+  if (type == 1 || type == 30) {
+    for (int64_t i = 0; i < numel; i++) {
+      uint16_t h = (uint16_t)(data[2 * i] | (data[2 * i + 1] << 8));
+      if (type == 1) out[i] = (float)oracle_from_f16(h);
+      else { uint32_t u = (uint32_t)h << 16; memcpy(out + i, &u, 4); }
+    }
+    return 0;
+  }
+  void (*fn)(const uint8_t*, float*) = 0;
+  switch (type) {
+    case 2: fn = oracle_dequant_q4_0_block; break;
+    case 3: fn = oracle_dequant_q4_1_block; break;
+    case 6: fn = oracle_dequant_q5_0_block; break;
+    case 8: fn = oracle_dequant_q8_0_block; break;
+    case 12: fn = oracle_dequant_q4_k_block; break;
+    case 14: fn = oracle_dequant_q6_k_block; break;
+  }
+  int64_t blocks = (numel + be - 1) / be;
+  float tmp[256];
   for (int64_t b = 0; b < blocks; b++) {
-    fn(data + b * bpb, tmp);
-    int64_t cnt = numel - b * 32 < 32 ? numel - b * 32 : 32;
-    memcpy(out + b * 32, tmp, (size_t)cnt * 4);
+    fn(data + b * bb, tmp);
+    int64_t cnt = numel - b * be < be ? numel - b * be : be;
+    memcpy(out + b * be, tmp, (size_t)cnt * 4);
   }
   return 0;
 }
@@ -311,22 +421,154 @@ void oracle_quantize_q8_0_block(const float* x, uint8_t* blk) {
   for (int i = 0; i < 32; i++) blk[2 + i] = (uint8_t)(int8_t)roundf(x[i] * id);
 }
 
-/* Quantize a [rows, cols] f32 matrix row by row into GGUF blocks
- * (type 2 = Q4_0, 8 = Q8_0); cols is padded up to a multiple of 32 with 0. */
+/* Encoders for the other block types, written for this build's synthetic
+ * files (the reference has none).  Each packs in the layout the reference's
+ * decoder above reads; the rounding choices are this build's. */
+
+static void put_f16(uint8_t* p, float v) {
+  uint16_t h = oracle_f32_to_f16_rne(v);
+  p[0] = (uint8_t)(h & 0xff);
+  p[1] = (uint8_t)(h >> 8);
+}
+static void put_nib(uint8_t* qs, int i, int q) { qs[i >> 1] |= (uint8_t)((i & 1) ? (q << 4) : q); }
+static int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* Q4_1 as ggml's quantize_row_q4_1_ref: d = (max - min) / 15, m = min,
+ * q = min(15, (int8)((x - min) / d + 0.5f)). */
+void oracle_quantize_q4_1_block(const float* x, uint8_t* blk) {
+  float mn = x[0], mx = x[0];
+  for (int i = 1; i < 32; i++) { if (x[i] < mn) mn = x[i]; if (x[i] > mx) mx = x[i]; }
+  float d = (mx - mn) / 15.0f;
+  float id = d != 0.0f ? 1.0f / d : 0.0f;
+  put_f16(blk, d);
+  put_f16(blk + 2, mn);
+  memset(blk + 4, 0, 16);
+  for (int i = 0; i < 32; i++) {
+    int8_t qi = (int8_t)((x[i] - mn) * id + 0.5f);
+    put_nib(blk + 4, i, qi < 15 ? qi : 15);
+  }
+}
+
+/* Q5_0 as ggml's quantize_row_q5_0_ref: signed extreme max, d = max / -16,
+ * q = min(31, (int8)(x / d + 16.5f)); nibble and fifth bit of element i in
+ * the reference's order. */
+void oracle_quantize_q5_0_block(const float* x, uint8_t* blk) {
+  float amax = 0.0f, mx = 0.0f;
+  for (int i = 0; i < 32; i++) if (amax < fabsf(x[i])) { amax = fabsf(x[i]); mx = x[i]; }
+  float d = mx / -16.0f;
+  float id = d != 0.0f ? 1.0f / d : 0.0f;
+  put_f16(blk, d);
+  uint32_t hb = 0;
+  memset(blk + 6, 0, 16);
+  for (int i = 0; i < 32; i++) {
+    int8_t qi = (int8_t)(x[i] * id + 16.5f);
+    int q = qi < 31 ? qi : 31;
+    put_nib(blk + 6, i, q & 15);
+    hb |= (uint32_t)(q >> 4) << i;
+  }
+  for (int k = 0; k < 4; k++) blk[2 + k] = (uint8_t)(hb >> (8 * k));
+}
+
+/* Q4_K: per 32-element sub-block, step = (max - min) / 15 and offset = -min
+ * (min clamped to <= 0); d = max step / 63, dmin = max offset / 63 (f16);
+ * 6-bit ints round(step / d), round(offset / dmin); then
+ * q = clamp(round((x + dmin*m) / (d*s)), 0, 15) with the stored values. */
+void oracle_quantize_q4_k_block(const float* x, uint8_t* blk) {
+  float step[8], offs[8], smax = 0.0f, omax = 0.0f;
+  for (int i = 0; i < 8; i++) {
+    float mn = 0.0f, mx = 0.0f;
+    for (int k = 0; k < 32; k++) {
+      float v = x[32 * i + k];
+      if (k == 0 || v < mn) mn = v;
+      if (k == 0 || v > mx) mx = v;
+    }
+    if (mn > 0.0f) mn = 0.0f;
+    step[i] = (mx - mn) / 15.0f;
+    offs[i] = -mn;
+    if (step[i] > smax) smax = step[i];
+    if (offs[i] > omax) omax = offs[i];
+  }
+  put_f16(blk, smax / 63.0f);
+  put_f16(blk + 2, omax / 63.0f);
+  float d = (float)oracle_from_f16((uint16_t)(blk[0] | (blk[1] << 8)));
+  float dmin = (float)oracle_from_f16((uint16_t)(blk[2] | (blk[3] << 8)));
+  uint8_t* s12 = blk + 4;
+  memset(s12, 0, 12);
+  int S[8], Mi[8];
+  for (int i = 0; i < 8; i++) {
+    S[i] = d > 0.0f ? clampi((int)roundf(step[i] / d), 0, 63) : 0;
+    Mi[i] = dmin > 0.0f ? clampi((int)roundf(offs[i] / dmin), 0, 63) : 0;
+    if (i < 4) {
+      s12[i] |= (uint8_t)S[i];
+      s12[4 + i] |= (uint8_t)Mi[i];
+    } else {
+      s12[i - 4] |= (uint8_t)((S[i] & 3) << 6);
+      s12[i + 4] |= (uint8_t)((S[i] >> 2) | ((Mi[i] >> 2) << 4));
+      s12[i] |= (uint8_t)((Mi[i] & 3) << 6);
+    }
+  }
+  memset(blk + 16, 0, 128);
+  for (int j = 0; j < 256; j++) {
+    float sc = d * (float)S[j >> 5], mn = dmin * (float)Mi[j >> 5];
+    int q = sc > 0.0f ? clampi((int)roundf((x[j] + mn) / sc), 0, 15) : 0;
+    put_nib(blk + 16, j, q);
+  }
+}
+
+/* Q6_K: per 16-element sub-block the signed extreme max, scale = max / -32;
+ * d = (largest |scale|) / 127 (f16); int8 s = clamp(round(scale / d));
+ * q = clamp(round(x / (d*s)), -32, 31) + 32 in the reference's ql/qh order. */
+void oracle_quantize_q6_k_block(const float* x, uint8_t* blk) {
+  float scl[16], amx = 0.0f;
+  for (int i = 0; i < 16; i++) {
+    float am = 0.0f, mx = 0.0f;
+    for (int k = 0; k < 16; k++) {
+      float v = x[16 * i + k];
+      if (am < fabsf(v)) { am = fabsf(v); mx = v; }
+    }
+    scl[i] = mx / -32.0f;
+    if (fabsf(scl[i]) > amx) amx = fabsf(scl[i]);
+  }
+  memset(blk, 0, 210);
+  put_f16(blk + 208, amx / 127.0f);
+  float d = (float)oracle_from_f16((uint16_t)(blk[208] | (blk[209] << 8)));
+  for (int i = 0; i < 16; i++) {
+    int s = d > 0.0f ? clampi((int)roundf(scl[i] / d), -128, 127) : 0;
+    blk[192 + i] = (uint8_t)(int8_t)s;
+    float step = d * (float)s;
+    for (int k = 0; k < 16; k++) {
+      int j = 16 * i + k;
+      int q = step != 0.0f ? clampi((int)roundf(x[j] / step), -32, 31) + 32 : 32;
+      put_nib(blk, j, q & 15);
+      blk[128 + (j >> 2)] |= (uint8_t)((q >> 4) << ((j & 3) * 2));
+    }
+  }
+}
+
+/* Quantize a [rows, cols] f32 matrix row by row into GGUF blocks of any of
+ * the block types above; cols is padded up to a multiple of the block size
+ * with 0. */
 int oracle_quantize_rows(int type, const float* x, int64_t rows, int64_t cols, uint8_t* out) {
-  int bpb = type == 2 ? Q4_0_BYTES : (type == 8 ? Q8_BYTES : 0);
-  if (!bpb) return -1;
-  int64_t bpr = (cols + 31) / 32;
-  float tmp[32];
+  int be, bb;
+  if (oracle_block_geometry(type, &be, &bb) || be == 1) return -1;
+  void (*fn)(const float*, uint8_t*) = 0;
+  switch (type) {
+    case 2: fn = oracle_quantize_q4_0_block; break;
+    case 3: fn = oracle_quantize_q4_1_block; break;
+    case 6: fn = oracle_quantize_q5_0_block; break;
+    case 8: fn = oracle_quantize_q8_0_block; break;
+    case 12: fn = oracle_quantize_q4_k_block; break;
+    case 14: fn = oracle_quantize_q6_k_block; break;
+  }
+  int64_t bpr = (cols + be - 1) / be;
+  float tmp[256];
   for (int64_t r = 0; r < rows; r++) {
     for (int64_t b = 0; b < bpr; b++) {
-      for (int i = 0; i < 32; i++) {
-        int64_t c = b * 32 + i;
+      for (int i = 0; i < be; i++) {
+        int64_t c = b * be + i;
         tmp[i] = c < cols ? x[r * cols + c] : 0.0f;
       }
-      uint8_t* blk = out + (r * bpr + b) * bpb;
-      if (type == 2) oracle_quantize_q4_0_block(tmp, blk);
-      else oracle_quantize_q8_0_block(tmp, blk);
+      fn(tmp, out + (r * bpr + b) * bb);
     }
   }
   return 0;
@@ -386,11 +628,12 @@ void oracle_matmul_q8(const float* a, const uint8_t* q, int64_t M, int64_t N, in
  * row): y[M,N] = A[M,K] . W^T, the transpose gguf_loader.js:243-253 applies
  * for a [out,in] listing.  f64 accumulation. */
 int oracle_matmul_gguf(int type, const float* a, const uint8_t* q, int64_t M, int64_t N, int64_t K, float* c) {
-  int64_t kp = (K + 31) / 32 * 32;
+  int be, bb;
+  if (oracle_block_geometry(type, &be, &bb) || be == 1) return -1;
+  int64_t kp = (K + be - 1) / be * be;
   float* wt = (float*)malloc((size_t)(N * kp) * 4);
-  int bpb = type == 2 ? Q4_0_BYTES : Q8_BYTES;
   for (int64_t n = 0; n < N; n++) {
-    if (oracle_dequantize_tensor(type, q + n * (kp / 32) * bpb, kp, wt + n * kp)) { free(wt); return -1; }
+    if (oracle_dequantize_tensor(type, q + n * (kp / be) * bb, kp, wt + n * kp)) { free(wt); return -1; }
   }
   for (int64_t m = 0; m < M; m++) {
     for (int64_t n = 0; n < N; n++) {
