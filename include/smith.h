@@ -65,6 +65,11 @@ int smith_copy_h2d(void* ctx, void* dst_buffer, uint64_t dst_offset, const void*
 int smith_copy_d2h(void* ctx, void* dst, const void* src_buffer, uint64_t src_offset, uint64_t bytes);
 int smith_copy_d2d(void* ctx, void* dst_buffer, uint64_t dst_offset, const void* src_buffer,
                    uint64_t src_offset, uint64_t bytes);
+/* rows x width bytes between pitched device regions (no reference
+ * counterpart: used to place the column ranges of mixed-type q|k|v
+ * projections into one row-major output). */
+int smith_copy_2d(void* ctx, void* dst, uint64_t dpitch, const void* src, uint64_t spitch, uint64_t width,
+                  uint64_t rows);
 int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes); /* enqueued fill kernel */
 int smith_sync(void* ctx);
 void smith_free(void* p); /* strings and SmithTiming returned by this library */
@@ -205,6 +210,37 @@ int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, u
 int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_ptr, uint32_t head_dim,
                              const void* nib, const void* d, float* out, uint32_t N, uint32_t K, const float* resid,
                              uint32_t epilogue, void* act_out, const float* gamma_out);
+/* Other GGUF block types on the quantized path (src/gguf.js:203-339 decode
+ * them to f32 at load; here the blocks stay quantized).  A weight listed
+ * [out=N, in=K] of GGML type Q4_0 (2), Q4_1 (3), Q5_0 (6), Q4_K (12) or
+ * Q6_K (14) is moved into one "tile plane" buffer of
+ * smith_gguf_tiles_bytes(type, N_total, K) bytes (0: shape or type not
+ * supported; N % 16 == 0, K % 32 == 0, K % 256 == 0 for Q4_K / Q6_K):
+ * nibbles, high bits, per-32 scales, per-256 scales, each in 16-column tiles.
+ * smith_repack_gguf_tiles_into places the N rows of `blocks` at columns
+ * n_off + n * n_stride of an N_total-column buffer (fused q|k|v, interleaved
+ * gate/up), as smith_repack_q4_0_t_into does.
+ * smith_linear_gguf_tiles: y = x . W^T for M rows with the fused RMSNorm /
+ * residual / SwiGLU of smith_linear_q4_0_t (Q4_0 runs exactly that; the
+ * other types run the MFMA GEMM, f16 weights, for every M).
+ * smith_linear_gguf_tiles_act / _attn: the single-row act GEMVs of
+ * smith_linear_q4_0_t_act / _attn on these planes (exact weights). */
+uint64_t smith_gguf_tiles_bytes(uint32_t ggml_type, uint32_t N, uint32_t K);
+int smith_repack_gguf_tiles_into(void* ctx, uint32_t ggml_type, const void* blocks, void* planes, uint32_t N,
+                                 uint32_t K, uint32_t n_off, uint32_t n_stride, uint32_t N_total);
+int smith_linear_gguf_tiles(void* ctx, uint32_t ggml_type, const float* x, const void* planes, float* out,
+                            uint32_t M, uint32_t N, uint32_t K, const float* norm_gamma, float eps, const float* resid,
+                            uint32_t epilogue);
+int smith_linear_gguf_tiles_act(void* ctx, uint32_t ggml_type, const void* act_in, int norm, float eps,
+                                const void* planes, float* out, uint32_t N, uint32_t K, const float* resid,
+                                uint32_t epilogue, void* act_out, const float* gamma_out);
+int smith_linear_gguf_tiles_attn(void* ctx, uint32_t ggml_type, const float* parts, const int32_t* pos_ptr,
+                                 uint32_t head_dim, const void* planes, float* out, uint32_t N, uint32_t K,
+                                 const float* resid, uint32_t epilogue, void* act_out, const float* gamma_out);
+/* dequantizeTensor (src/gguf.js:343-394) on the device: numel elements of a
+ * flat GGUF tensor of type F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q8_0, Q4_K or
+ * Q6_K to f32, bit-identical to the reference's Float32Array. */
+int smith_dequantize_gguf(void* ctx, uint32_t ggml_type, const void* src, float* dst, uint64_t numel);
 /* LM head on a Q4_0 output.weight read as lmHead[K=dim][N=vocab] (blocks run
  * along the vocab axis, gguf_loader.js:240-259): smith_repack_lmhead_q4_0
  * splits the raw blocks into a nibble plane (K*N/2 bytes, block order) and a

@@ -15,7 +15,7 @@ import numpy as np
 from . import oracle as O
 
 F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
-_BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34)}
+_BLOCK = O.BLOCK
 
 
 def read_gguf(path):

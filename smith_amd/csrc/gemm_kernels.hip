@@ -33,6 +33,7 @@
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#include "gguf_tiles_dev.h"
 
 #define WF_Q4S 0
 #define WF_Q8 1
@@ -54,6 +55,7 @@ struct WRec {
   uint32_t q8c;
   uint32_t sh;
   float s, z;
+  uint32_t h0, h1, p, sp;  // GGUF tile planes (FMT >= GT_Q41): hb words, prm, sup
 };
 
 template <int FMT>
@@ -64,6 +66,19 @@ __device__ __forceinline__ WRec load_wrec(const uint8_t* __restrict__ B, const u
   const uint32_t gc = g < G ? g : G - 1, nc = n < N ? n : N - 1;
   r.sh = 0;
   r.z = 0.f;
+  if (FMT >= GT_Q41) {
+    // GGUF tile planes (gguf_tiles.h); a zero prm / sup makes the record 0
+    GtW<FMT> w;
+    const size_t rec = ((size_t)(nc >> 4) * G + gc) * 16 + (nc & 15);
+    gt_load<FMT>(w, B, gt_planes(FMT, N, G), rec, ((size_t)(nc >> 4) * (G / 8) + gc / 8) * 16 + (nc & 15));
+    r.q = w.q;
+    r.h0 = w.h0;
+    r.h1 = w.h1;
+    r.p = ok ? w.p : 0u;
+    r.sp = ok ? w.sp : 0u;
+    r.s = 1.f;
+    return r;
+  }
   if (FMT == WF_Q4S) {
     const uint8_t* p = B + ((size_t)gc * N + nc) * 24;
     r.q = *(const u32x4*)p;
@@ -92,6 +107,22 @@ __device__ __forceinline__ WRec load_wrec(const uint8_t* __restrict__ B, const u
 // the 32 dequantized weights of a record as 16 packed f16 pairs (k order)
 template <int FMT>
 __device__ __forceinline__ void dequant_wrec(const WRec& r, uint32_t (&o)[16]) {
+  if constexpr (FMT >= GT_Q41) {
+    GtW<FMT> w;
+    w.q = r.q;
+    w.h0 = r.h0;
+    w.h1 = r.h1;
+    w.p = r.p;
+    w.sp = r.sp;
+    float s0, c0, s1, c1;
+    gt_affine<FMT>(w, s0, c0, s1, c1);
+#pragma unroll
+    for (int e = 0; e < 32; e += 2) {
+      const float s = e < 16 ? s0 : s1, c = e < 16 ? c0 : c1;
+      o[e / 2] = pack_h2(__builtin_fmaf((float)gt_q<FMT>(w, e), s, c), __builtin_fmaf((float)gt_q<FMT>(w, e + 1), s, c));
+    }
+    return;
+  }
   if (FMT == WF_Q8) {
     const uint32_t d[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
 #pragma unroll
@@ -285,6 +316,10 @@ DEF_GEMM_FMT(q4s, WF_Q4S)
 DEF_GEMM_FMT(q8, WF_Q8)
 DEF_GEMM_FMT(q40t, WF_Q40T)
 DEF_GEMM_FMT(q40, WF_Q40)
+DEF_GEMM_FMT(q41t, GT_Q41)
+DEF_GEMM_FMT(q50t, GT_Q50)
+DEF_GEMM_FMT(q4kt, GT_Q4K)
+DEF_GEMM_FMT(q6kt, GT_Q6K)
 
 // C = epilogue(sum over the ks K-split partials ws[0..ks) [M][N]), fixed
 // order; one thread per output (pair for SwiGLU).

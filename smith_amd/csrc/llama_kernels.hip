@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #include "act_frag.h"
+#include "gguf_tiles.h"
 
 // ---------------------------------------------------------------------------
 // RMSNorm rows: y = x * rsqrt(mean(x^2) + eps) * gamma
@@ -739,3 +740,159 @@ extern "C" __global__ void smith_randn_f32(float* __restrict__ out, uint64_t n, 
     if (2 * pi + 1 < n) out[2 * pi + 1] = (float)(r * sin(th) * (double)stdv + (double)mean);
   }
 }
+
+// ---------------------------------------------------------------------------
+// GGUF weights [out=N rows, in=K] of Q4_0 / Q4_1 / Q5_0 / Q4_K / Q6_K blocks
+// -> the tile planes of gguf_tiles.h.  Values are moved, never changed: the
+// same integers, f16 fields and 6-bit / int8 scales the reference's decoders
+// read (src/gguf.js:187-339), at the record of column n_off + n * n_stride of
+// an N_total-column buffer (q|k|v side by side, gate/up interleaved).
+// One thread per (row, 32-element group).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+template <int F>
+__device__ __forceinline__ void repack_gguf_tiles(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                  uint32_t N, uint32_t G, uint32_t n_off, uint32_t n_stride,
+                                                  uint32_t N_total) {
+  const GtPlanes P = gt_planes(F, N_total, G);
+  const size_t total = (size_t)N * G;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t n = (uint32_t)(idx / G), g = (uint32_t)(idx % G);
+    const uint32_t col = n_off + n * n_stride;
+    const size_t rec = ((size_t)(col >> 4) * G + g) * 16 + (col & 15);
+    const uint32_t sb = g >> 3, i8 = g & 7;  // super-block and sub-block (Q4_K / Q6_K)
+    const uint8_t* blk;
+    const uint8_t* qs;
+    if (F == GT_Q41) blk = src + idx * 20, qs = blk + 4;
+    else if (F == GT_Q50) blk = src + idx * 22, qs = blk + 6;
+    else if (F == GT_Q4K) blk = src + ((size_t)n * (G / 8) + sb) * 144, qs = blk + 16 + 16 * i8;
+    else if (F == GT_Q6K) blk = src + ((size_t)n * (G / 8) + sb) * 210, qs = blk + 16 * i8;
+    else blk = src + idx * 18, qs = blk + 2;
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+      w[d] = (uint32_t)qs[4 * d] | ((uint32_t)qs[4 * d + 1] << 8) | ((uint32_t)qs[4 * d + 2] << 16) |
+             ((uint32_t)qs[4 * d + 3] << 24);
+    *(uint4*)(dst + rec * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (F == GT_Q50) {
+      const uint32_t hb = ld_u16(blk + 2) | (ld_u16(blk + 4) << 16);  // bit e: element e
+      uint32_t W = 0;
+#pragma unroll
+      for (int e = 0; e < 32; e++) {
+        const int i = e >> 3, k = e & 7;
+        W |= ((hb >> e) & 1u) << (4 * i + (k & 3) + 16 * (k >> 2));
+      }
+      *(uint32_t*)(dst + P.hb + rec * 4) = W;
+    }
+    if (F == GT_Q6K) {
+      const uint8_t* qh = blk + 128 + 8 * i8;  // elements 32*i8 .. +31: 2 bits each, 4 per byte
+      uint32_t W0 = 0, W1 = 0;
+#pragma unroll
+      for (int e = 0; e < 32; e++) {
+        const int i = e >> 3, k = e & 7;
+        const uint32_t v = (qh[e >> 2] >> (2 * (e & 3))) & 3u;
+        const uint32_t pos = 2 * (4 * (i & 1) + (k & 3)) + 16 * (k >> 2);
+        if (i < 2) W0 |= v << pos;
+        else W1 |= v << pos;
+      }
+      *(uint2*)(dst + P.hb + rec * 8) = make_uint2(W0, W1);
+    }
+    if (F == GT_Q41) {
+      *(uint32_t*)(dst + P.prm + rec * 4) = ld_u16(blk) | (ld_u16(blk + 2) << 16);
+    } else if (F == GT_Q4K) {
+      // 6-bit (scale, min) of sub-block i8 as src/gguf.js:281-291 unpacks them
+      const uint8_t* s12 = blk + 4;
+      uint32_t sc, mn;
+      if (i8 < 4) {
+        sc = s12[i8] & 0x3Fu;
+        mn = s12[4 + i8] & 0x3Fu;
+      } else {
+        sc = (uint32_t)(s12[i8 - 4] >> 6) | ((uint32_t)(s12[i8 + 4] & 0x0F) << 2);
+        mn = (uint32_t)(s12[i8] >> 6) | ((uint32_t)(s12[i8 + 4] >> 4) << 2);
+      }
+      *(uint16_t*)(dst + P.prm + rec * 2) = (uint16_t)(sc | (mn << 8));
+    } else if (F == GT_Q6K) {
+      *(uint16_t*)(dst + P.prm + rec * 2) = (uint16_t)ld_u16(blk + 192 + 2 * i8);
+    } else {
+      *(uint16_t*)(dst + P.prm + rec * 2) = (uint16_t)ld_u16(blk);
+    }
+    if (gt_super(F) && i8 == 0) {
+      const size_t srec = ((size_t)(col >> 4) * (G / 8) + sb) * 16 + (col & 15);
+      if (F == GT_Q4K) *(uint32_t*)(dst + P.sup + srec * 4) = ld_u16(blk) | (ld_u16(blk + 2) << 16);
+      else *(uint16_t*)(dst + P.sup + srec * 2) = (uint16_t)ld_u16(blk + 208);
+    }
+  }
+}
+
+#define DEF_REPACK_GT(NAME, F)                                                                                  \
+  extern "C" __global__ void NAME(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint32_t N,      \
+                                  uint32_t G, uint32_t n_off, uint32_t n_stride, uint32_t N_total) {           \
+    repack_gguf_tiles<F>(src, dst, N, G, n_off, n_stride, N_total);                                           \
+  }
+DEF_REPACK_GT(smith_repack_gt_q40, GT_Q40)
+DEF_REPACK_GT(smith_repack_gt_q41, GT_Q41)
+DEF_REPACK_GT(smith_repack_gt_q50, GT_Q50)
+DEF_REPACK_GT(smith_repack_gt_q4k, GT_Q4K)
+DEF_REPACK_GT(smith_repack_gt_q6k, GT_Q6K)
+
+// ---------------------------------------------------------------------------
+// dequantizeTensor (src/gguf.js:343-394) on the device: element idx of a flat
+// tensor from its block, evaluated as the reference does -- f64 products
+// and sums of the exactly decoded f16 fields and integers, one rounding to
+// f32 (Float32Array store).  F16 by exact conversion, BF16 by a 16-bit shift
+// (F32 needs no kernel).  One thread per element.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double f16_to_f64(uint32_t h) { return (double)(float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+template <int T>
+__device__ __forceinline__ float dequant_elem(const uint8_t* __restrict__ src, size_t idx) {
+  if (T == 1) return (float)__builtin_bit_cast(_Float16, (uint16_t)ld_u16(src + 2 * idx));
+  if (T == 30) return __uint_as_float(ld_u16(src + 2 * idx) << 16);
+  const uint32_t be = (T == 12 || T == 14) ? 256 : 32;
+  const uint32_t bb = T == 2 ? 18 : (T == 3 ? 20 : (T == 6 ? 22 : (T == 8 ? 34 : (T == 12 ? 144 : 210))));
+  const uint8_t* blk = src + (idx / be) * bb;
+  const uint32_t j = (uint32_t)(idx % be);
+  auto nib = [&](const uint8_t* qs) { const uint8_t b = qs[j >> 1]; return (int)((j & 1) ? (b >> 4) : (b & 15)); };
+  if (T == 2) return (float)(f16_to_f64(ld_u16(blk)) * (double)(nib(blk + 2) - 8));
+  if (T == 3) return (float)(f16_to_f64(ld_u16(blk)) * (double)nib(blk + 4) + f16_to_f64(ld_u16(blk + 2)));
+  if (T == 6) {
+    const uint32_t hb = ld_u16(blk + 2) | (ld_u16(blk + 4) << 16);
+    return (float)(f16_to_f64(ld_u16(blk)) * (double)((nib(blk + 6) | (int)(((hb >> j) & 1u) << 4)) - 16));
+  }
+  if (T == 8) return (float)(f16_to_f64(ld_u16(blk)) * (double)(int8_t)blk[2 + j]);
+  if (T == 12) {
+    const uint32_t i = j >> 5;
+    const uint8_t* s12 = blk + 4;
+    uint32_t sc, mn;
+    if (i < 4) {
+      sc = s12[i] & 0x3Fu;
+      mn = s12[4 + i] & 0x3Fu;
+    } else {
+      sc = (uint32_t)(s12[i - 4] >> 6) | ((uint32_t)(s12[i + 4] & 0x0F) << 2);
+      mn = (uint32_t)(s12[i] >> 6) | ((uint32_t)(s12[i + 4] >> 4) << 2);
+    }
+    const float scf = (float)(f16_to_f64(ld_u16(blk)) * (double)sc);
+    const float mnf = (float)(f16_to_f64(ld_u16(blk + 2)) * (double)mn);
+    return (float)((double)scf * (double)nib(blk + 16) - (double)mnf);
+  }
+  // Q6_K
+  const int q = nib(blk) | (int)(((blk[128 + (j >> 2)] >> (2 * (j & 3))) & 3u) << 4);
+  return (float)(f16_to_f64(ld_u16(blk + 208)) * (double)(int8_t)blk[192 + (j >> 4)] * (double)(q - 32));
+}
+
+#define DEF_DEQUANT(NAME, T)                                                                                   \
+  extern "C" __global__ void NAME(const uint8_t* __restrict__ src, float* __restrict__ dst, uint64_t numel) { \
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < numel;                              \
+         idx += (size_t)gridDim.x * blockDim.x)                                                               \
+      dst[idx] = dequant_elem<T>(src, idx);                                                                    \
+  }
+DEF_DEQUANT(smith_dequantize_f16, 1)
+DEF_DEQUANT(smith_dequantize_bf16, 30)
+DEF_DEQUANT(smith_dequantize_q4_0, 2)
+DEF_DEQUANT(smith_dequantize_q4_1, 3)
+DEF_DEQUANT(smith_dequantize_q5_0, 6)
+DEF_DEQUANT(smith_dequantize_q8_0, 8)
+DEF_DEQUANT(smith_dequantize_q4_k, 12)
+DEF_DEQUANT(smith_dequantize_q6_k, 14)

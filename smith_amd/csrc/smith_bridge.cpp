@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "../../include/smith.h"
+#include "gguf_tiles.h"
 
 namespace {
 
@@ -203,9 +204,12 @@ int ensure_counters(Ctx* c, size_t n) {
   return 0;
 }
 
-enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2, FQ40T = 3 };
+enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2, FQ40T = 3, FQ41T = 4, FQ50T = 5, FQ4KT = 6, FQ6KT = 7 };
 
-const char* fmt_tag(Fmt f) { return f == FQ4S ? "q4s" : (f == FQ8 ? "q8" : (f == FQ40 ? "q40" : "q40t")); }
+const char* fmt_tag(Fmt f) {
+  static const char* tags[] = {"q4s", "q8", "q40", "q40t", "q41t", "q50t", "q4kt", "q6kt"};
+  return tags[f];
+}
 
 // M > 2: prepare the activations once (smith_qprep_*), then the 16-row
 // MFMA GEMV (smith_qgemv3_*).  Buckets must match DEF_QGEMV3_FMT.
@@ -588,6 +592,17 @@ int smith_copy_d2d(void* ctx, void* dst, uint64_t doff, const void* src, uint64_
   if (set_device(c)) return -1;
   if (!bytes) return 0;
   HIPCHK(c, hipMemcpyAsync((char*)dst + doff, (const char*)src + soff, bytes, hipMemcpyDeviceToDevice, c->stream));
+  return 0;
+}
+
+int smith_copy_2d(void* ctx, void* dst, uint64_t dpitch, const void* src, uint64_t spitch, uint64_t width,
+                  uint64_t rows) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!rows || !width) return 0;
+  if (!dst || !src || width > dpitch || width > spitch) return fail(c, "smith_copy_2d: bad pitches or buffers");
+  if (set_device(c)) return -1;
+  HIPCHK(c, hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDeviceToDevice, c->stream));
   return 0;
 }
 
@@ -992,18 +1007,20 @@ int smith_linear_q4_0_t(void* ctx, const float* x, const void* nib, const void* 
   return qmatmul(c, FQ40T, x, nib, d, out, M, N, K, K / 32, e);
 }
 
-int smith_linear_q4_0_t_act(void* ctx, const void* act_in, int norm, float eps, const void* nib, const void* d,
-                            float* out, uint32_t N, uint32_t K, const float* resid, uint32_t epilogue,
-                            void* act_out, const float* gamma_out) {
-  Ctx* c = (Ctx*)ctx;
-  if (!c) return -1;
-  if (!act_in) return fail(c, "smith_linear_q4_0_t_act: no input act");
-  if (K % 32 || !K) return fail(c, "smith_linear_q4_0_t_act: K %u is not a positive multiple of 32", K);
-  if (N % 16 || !N) return fail(c, "smith_linear_q4_0_t_act: N %u is not a positive multiple of 16", N);
-  if (epilogue > 2) return fail(c, "smith_linear_q4_0_t_act: unknown epilogue %u", epilogue);
-  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q4_0_t_act: residual epilogue without a residual buffer");
+namespace {
+
+// single-row GEMV on an act (smith_agemv_<fmt>_k*); B/D as the format takes
+// them (Q4_0: nib and d planes; other tile formats: the plane buffer twice)
+int act_gemv(Ctx* c, const char* fn, Fmt fmt, const void* act_in, int norm, float eps, const void* B, const void* D,
+             float* out, uint32_t N, uint32_t K, const float* resid, uint32_t epilogue, void* act_out,
+             const float* gamma_out) {
+  if (!act_in) return fail(c, "%s: no input act", fn);
+  if (K % 32 || !K) return fail(c, "%s: K %u is not a positive multiple of 32", fn, K);
+  if (N % 16 || !N) return fail(c, "%s: N %u is not a positive multiple of 16", fn, N);
+  if (epilogue > 2) return fail(c, "%s: unknown epilogue %u", fn, epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "%s: residual epilogue without a residual buffer", fn);
   const uint32_t nout = epilogue == 2 ? N / 2 : N;
-  if (act_out && nout % 32) return fail(c, "smith_linear_q4_0_t_act: act output needs %u %% 32 == 0", nout);
+  if (act_out && nout % 32) return fail(c, "%s: act output needs %u %% 32 == 0", fn, nout);
   if (set_device(c)) return -1;
   // smallest block K coverage that holds all K groups (no split), else 288
   // groups per block and a K split across blocks
@@ -1023,13 +1040,80 @@ int smith_linear_q4_0_t_act(void* ctx, const void* act_in, int norm, float eps, 
     if (ensure_counters(c, gx)) return -1;
   }
   char name[64];
-  snprintf(name, sizeof name, "smith_agemv_q40t_k%u", kb);
+  snprintf(name, sizeof name, "smith_agemv_%s_k%u", fmt_tag(fmt), kb);
   float* pws = c->ws;
   uint32_t* pcnt = c->counters;
   uint32_t pN = N, pK = K, pnorm = norm ? 1u : 0u, pepi = epilogue;
   const float* pR = epilogue == 1 ? resid : nullptr;
-  void* args[] = {&act_in, &nib, &d, &out, &pN, &pK, &pnorm, &eps, &pR, &pepi, &act_out, &gamma_out, &pws, &pcnt};
+  void* args[] = {&act_in, &B, &D, &out, &pN, &pK, &pnorm, &eps, &pR, &pepi, &act_out, &gamma_out, &pws, &pcnt};
   return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
+}
+
+// o-projection on attention split partials (smith_agemv_att_<fmt>_k*)
+int attn_gemv(Ctx* c, const char* fn, Fmt fmt, const float* parts, const int32_t* pos_ptr, uint32_t head_dim,
+              const void* B, const void* D, float* out, uint32_t N, uint32_t K, const float* resid,
+              uint32_t epilogue, void* act_out, const float* gamma_out) {
+  if (!parts || !pos_ptr) return fail(c, "%s: no attention partials", fn);
+  if (!head_dim || head_dim > 128 || head_dim % 32 || K % head_dim)
+    return fail(c, "%s: head_dim %u unsupported for K %u", fn, head_dim, K);
+  if (K % 32 || !K) return fail(c, "%s: K %u is not a positive multiple of 32", fn, K);
+  if (N % 16 || !N) return fail(c, "%s: N %u is not a positive multiple of 16", fn, N);
+  if (epilogue > 2) return fail(c, "%s: unknown epilogue %u", fn, epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "%s: residual epilogue without a residual buffer", fn);
+  const uint32_t nout = epilogue == 2 ? N / 2 : N;
+  if (act_out && nout % 32) return fail(c, "%s: act output needs %u %% 32 == 0", fn, nout);
+  if (set_device(c)) return -1;
+  static const uint32_t kbs[] = {64, 96, 128, 192};
+  const uint32_t G = K / 32;
+  uint32_t kb = 192;
+  for (uint32_t v : kbs)
+    if (v >= G) {
+      kb = v;
+      break;
+    }
+  const uint32_t ksplit = (G + kb - 1) / kb;
+  const uint32_t threads = kb == 64 ? 256 : 512;
+  const uint32_t gx = N / 16;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_agemv_att_%s_k%u", fmt_tag(fmt), kb);
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pN = N, pK = K, phd = head_dim, pepi = epilogue;
+  const float* pR = epilogue == 1 ? resid : nullptr;
+  void* args[] = {&parts, &pos_ptr, &phd, &B, &D, &out, &pN, &pK, &pR, &pepi, &act_out, &gamma_out, &pws, &pcnt};
+  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
+}
+
+// GGML type -> tile format, with the shape rules of the tile planes
+int tiles_fmt(Ctx* c, const char* fn, uint32_t type, uint32_t N, uint32_t K, Fmt* fmt) {
+  const int f = gt_of_ggml((int)type);
+  if (f < 0) return fail(c, "%s: GGML type %u has no tile layout (Q4_0, Q4_1, Q5_0, Q4_K, Q6_K)", fn, type);
+  const uint32_t kq = gt_super(f) ? 256 : 32;
+  if (!K || K % kq) return fail(c, "%s: K %u is not a positive multiple of %u for GGML type %u", fn, K, kq, type);
+  if (!N || N % 16) return fail(c, "%s: N %u is not a positive multiple of 16", fn, N);
+  *fmt = (Fmt)f;
+  return 0;
+}
+
+// (B, D) kernel arguments of a tile-plane buffer
+void tiles_bd(Fmt fmt, const void* planes, uint32_t N, uint32_t K, const void** B, const void** D) {
+  *B = planes;
+  *D = fmt == FQ40T ? (const void*)((const char*)planes + gt_planes(GT_Q40, N, K / 32).prm) : planes;
+}
+
+}  // namespace
+
+int smith_linear_q4_0_t_act(void* ctx, const void* act_in, int norm, float eps, const void* nib, const void* d,
+                            float* out, uint32_t N, uint32_t K, const float* resid, uint32_t epilogue,
+                            void* act_out, const float* gamma_out) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  return act_gemv(c, "smith_linear_q4_0_t_act", FQ40T, act_in, norm, eps, nib, d, out, N, K, resid, epilogue,
+                  act_out, gamma_out);
 }
 
 int smith_linear_q8(void* ctx, const float* x, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,
@@ -1132,39 +1216,111 @@ int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_p
                              uint32_t epilogue, void* act_out, const float* gamma_out) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
-  if (!parts || !pos_ptr) return fail(c, "smith_linear_q4_0_t_attn: no attention partials");
-  if (!head_dim || head_dim > 128 || head_dim % 32 || K % head_dim)
-    return fail(c, "smith_linear_q4_0_t_attn: head_dim %u unsupported for K %u", head_dim, K);
-  if (K % 32 || !K) return fail(c, "smith_linear_q4_0_t_attn: K %u is not a positive multiple of 32", K);
-  if (N % 16 || !N) return fail(c, "smith_linear_q4_0_t_attn: N %u is not a positive multiple of 16", N);
-  if (epilogue > 2) return fail(c, "smith_linear_q4_0_t_attn: unknown epilogue %u", epilogue);
-  if (epilogue == 1 && !resid) return fail(c, "smith_linear_q4_0_t_attn: residual epilogue without a residual buffer");
-  const uint32_t nout = epilogue == 2 ? N / 2 : N;
-  if (act_out && nout % 32) return fail(c, "smith_linear_q4_0_t_attn: act output needs %u %% 32 == 0", nout);
+  return attn_gemv(c, "smith_linear_q4_0_t_attn", FQ40T, parts, pos_ptr, head_dim, nib, d, out, N, K, resid,
+                   epilogue, act_out, gamma_out);
+}
+
+uint64_t smith_gguf_tiles_bytes(uint32_t ggml_type, uint32_t N, uint32_t K) {
+  const int f = gt_of_ggml((int)ggml_type);
+  if (f < 0 || !N || N % 16 || !K || K % (gt_super(f) ? 256u : 32u)) return 0;
+  return gt_planes(f, N, K / 32).total;
+}
+
+int smith_repack_gguf_tiles_into(void* ctx, uint32_t ggml_type, const void* blocks, void* planes, uint32_t N,
+                                 uint32_t K, uint32_t n_off, uint32_t n_stride, uint32_t N_total) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  Fmt fmt;
+  if (tiles_fmt(c, "smith_repack_gguf_tiles_into", ggml_type, N_total, K, &fmt)) return -1;
+  if (!blocks || !planes) return fail(c, "smith_repack_gguf_tiles_into: null buffer");
+  if (N && (uint64_t)n_off + (uint64_t)(N - 1) * n_stride >= N_total)
+    return fail(c, "smith_repack_gguf_tiles_into: columns exceed N_total=%u", N_total);
   if (set_device(c)) return -1;
-  static const uint32_t kbs[] = {64, 96, 128, 192};
   const uint32_t G = K / 32;
-  uint32_t kb = 192;
-  for (uint32_t v : kbs)
-    if (v >= G) {
-      kb = v;
-      break;
-    }
-  const uint32_t ksplit = (G + kb - 1) / kb;
-  const uint32_t threads = kb == 64 ? 256 : 512;
-  const uint32_t gx = N / 16;
-  if (ksplit > 1) {
-    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
-    if (ensure_counters(c, gx)) return -1;
+  const uint64_t total = (uint64_t)N * G;
+  if (!total) return 0;
+  static const char* names[] = {"", "", "", "smith_repack_gt_q40", "smith_repack_gt_q41", "smith_repack_gt_q50",
+                                "smith_repack_gt_q4k", "smith_repack_gt_q6k"};
+  uint32_t pN = N, pG = G, po = n_off, ps = n_stride, pT = N_total;
+  void* args[] = {&blocks, &planes, &pN, &pG, &po, &ps, &pT};
+  return launch(c, names[fmt], dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)), dim3(256), args);
+}
+
+int smith_linear_gguf_tiles(void* ctx, uint32_t ggml_type, const float* x, const void* planes, float* out,
+                            uint32_t M, uint32_t N, uint32_t K, const float* norm_gamma, float eps, const float* resid,
+                            uint32_t epilogue) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  Fmt fmt;
+  if (tiles_fmt(c, "smith_linear_gguf_tiles", ggml_type, N, K, &fmt)) return -1;
+  if (epilogue > 2) return fail(c, "smith_linear_gguf_tiles: unknown epilogue %u", epilogue);
+  if (epilogue == 1 && !resid) return fail(c, "smith_linear_gguf_tiles: residual epilogue without a residual buffer");
+  const void *B, *D;
+  tiles_bd(fmt, planes, N, K, &B, &D);
+  Epi e;
+  e.gamma = norm_gamma;
+  e.eps = eps;
+  e.resid = epilogue == 1 ? resid : nullptr;
+  e.mode = epilogue;
+  if (fmt == FQ40T) return qmatmul(c, FQ40T, x, B, D, out, M, N, K, K / 32, e);
+  // the other tile formats: every row count on the MFMA GEMM (single rows
+  // of the decode step take the act path, smith_linear_gguf_tiles_act)
+  if (set_device(c)) return -1;
+  if (M == 0) return 0;
+  return gemm(c, fmt, x, B, D, out, M, N, K, e);
+}
+
+int smith_linear_gguf_tiles_act(void* ctx, uint32_t ggml_type, const void* act_in, int norm, float eps,
+                                const void* planes, float* out, uint32_t N, uint32_t K, const float* resid,
+                                uint32_t epilogue, void* act_out, const float* gamma_out) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  Fmt fmt;
+  if (tiles_fmt(c, "smith_linear_gguf_tiles_act", ggml_type, N, K, &fmt)) return -1;
+  const void *B, *D;
+  tiles_bd(fmt, planes, N, K, &B, &D);
+  return act_gemv(c, "smith_linear_gguf_tiles_act", fmt, act_in, norm, eps, B, D, out, N, K, resid, epilogue,
+                  act_out, gamma_out);
+}
+
+int smith_linear_gguf_tiles_attn(void* ctx, uint32_t ggml_type, const float* parts, const int32_t* pos_ptr,
+                                 uint32_t head_dim, const void* planes, float* out, uint32_t N, uint32_t K,
+                                 const float* resid, uint32_t epilogue, void* act_out, const float* gamma_out) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  Fmt fmt;
+  if (tiles_fmt(c, "smith_linear_gguf_tiles_attn", ggml_type, N, K, &fmt)) return -1;
+  const void *B, *D;
+  tiles_bd(fmt, planes, N, K, &B, &D);
+  return attn_gemv(c, "smith_linear_gguf_tiles_attn", fmt, parts, pos_ptr, head_dim, B, D, out, N, K, resid,
+                   epilogue, act_out, gamma_out);
+}
+
+int smith_dequantize_gguf(void* ctx, uint32_t ggml_type, const void* src, float* dst, uint64_t numel) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!numel) return 0;
+  if (!src || !dst) return fail(c, "smith_dequantize_gguf: null buffer");
+  if (set_device(c)) return -1;
+  if (ggml_type == 0) {
+    HIPCHK(c, hipMemcpyAsync(dst, src, numel * 4, hipMemcpyDeviceToDevice, c->stream));
+    return 0;
   }
-  char name[64];
-  snprintf(name, sizeof name, "smith_agemv_att_q40t_k%u", kb);
-  float* pws = c->ws;
-  uint32_t* pcnt = c->counters;
-  uint32_t pN = N, pK = K, phd = head_dim, pepi = epilogue;
-  const float* pR = epilogue == 1 ? resid : nullptr;
-  void* args[] = {&parts, &pos_ptr, &phd, &nib, &d, &out, &pN, &pK, &pR, &pepi, &act_out, &gamma_out, &pws, &pcnt};
-  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
+  const char* name = nullptr;
+  switch (ggml_type) {
+    case 1: name = "smith_dequantize_f16"; break;
+    case 30: name = "smith_dequantize_bf16"; break;
+    case 2: name = "smith_dequantize_q4_0"; break;
+    case 3: name = "smith_dequantize_q4_1"; break;
+    case 6: name = "smith_dequantize_q5_0"; break;
+    case 8: name = "smith_dequantize_q8_0"; break;
+    case 12: name = "smith_dequantize_q4_k"; break;
+    case 14: name = "smith_dequantize_q6_k"; break;
+    default: return fail(c, "smith_dequantize_gguf: GGML type %u cannot be dequantized", ggml_type);
+  }
+  uint64_t pn = numel;
+  void* args[] = {&src, &dst, &pn};
+  return launch(c, name, dim3((unsigned)std::min<uint64_t>((numel + 255) / 256, 1 << 20)), dim3(256), args);
 }
 
 int smith_repack_lmhead_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_t K, uint32_t N) {

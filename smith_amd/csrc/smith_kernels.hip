@@ -42,6 +42,7 @@
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#include "gguf_tiles_dev.h"
 
 #define FMT_Q4S 0
 #define FMT_Q8 1
@@ -509,13 +510,12 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
   return r;
 }
 
-// (x & mask) | (base & ~mask) in one v_bfi_b32: the and/or pair the compiler
-// would emit costs two VALU slots per converted dword (VOP3 takes no literal,
-// so the mask goes in an SGPR and the base in a VGPR, both loop invariant).
+// (x & mask) | (base & ~mask).  Plain C on purpose: the compiler's hazard
+// recognizer does not see VALU work inside inline asm, and a v_bfi_b32
+// written by asm into a dead lane of an in-flight MFMA's result was
+// overwritten when the MFMA retired.
 __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t base) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(base));
-  return r;
+  return (x & mask) | (base & ~mask);
 }
 
 // B operand of MFMA i (K elements 8i..8i+7 of the record).
@@ -1046,7 +1046,7 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 #define ATTP_MAXSPLIT 8  // as llama_kernels.hip
 #define ATTP_ROWS 32
 #define ATTP_STRIDE 132
-template <int CT, int S, int WK, int SRC>
+template <int F, int CT, int S, int WK, int SRC>
 __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, const uint8_t* __restrict__ B,
                                            const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t N,
                                            uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,
@@ -1059,7 +1059,10 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   constexpr int GMAX = 4 * S * WK;
   __shared__ u32x4 fragL[8 * GMAX + 4];  // [g][hi/lo][slice] + one zero fragment
   __shared__ float red[WK][BC];
+  constexpr bool NEED_S = F != FMT_Q40T;  // the affine term needs the group sums S
+  constexpr bool HALVES = F == GT_Q6K;    // separate scales for elements 0-15 / 16-31
   __shared__ float c1L[SRC == 1 ? 4 * GMAX : 1];                 // per-part C1 (SRC 1)
+  __shared__ float sL[SRC == 1 && NEED_S ? 4 * GMAX : 1];         // per-part S (SRC 1)
   __shared__ float coefL[SRC == 1 ? GMAX : 1][ATTP_MAXSPLIT];    // per-head split weights (SRC 1)
   const uint32_t G = K / 32, T = K / 8;
   const uint32_t lane = threadIdx.x & 63;
@@ -1080,7 +1083,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   constexpr int CPT = (8 * GMAX + NT - 1) / NT;   // frag words per thread (this block's groups)
   constexpr int SPL = (4 * GMAX + 63) / 64;       // part sums of squares per lane
   u32x4 fv[CPT];
-  float c1[S];
+  float c1[S], c1b[S], sg[S], sgb[S];  // (C1, S) of the group, or of its halves (HALVES)
   float ssv[SPL];
   // SRC 1: split partials of this block's parts (part = 8 elements)
   constexpr int PPT = SRC == 1 ? (4 * GMAX + NT - 1) / NT : 1;
@@ -1098,7 +1101,21 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       const uint32_t g = gw + 4 * st + j;
       const uint32_t gc = g < G ? g : G - 1;
       const float4 cc = *(const float4*)(c1p + 4 * gc);
-      c1[st] = (cc.x + cc.y) + (cc.z + cc.w);
+      if (HALVES) {
+        c1[st] = cc.x + cc.y;
+        c1b[st] = cc.z + cc.w;
+      } else {
+        c1[st] = (cc.x + cc.y) + (cc.z + cc.w);
+      }
+      if (NEED_S) {
+        const float4 sv = *(const float4*)(c1p + T + 4 * gc);
+        if (HALVES) {
+          sg[st] = sv.x + sv.y;
+          sgb[st] = sv.z + sv.w;
+        } else {
+          sg[st] = (sv.x + sv.y) + (sv.z + sv.w);
+        }
+      }
     }
     // sums of squares for the RMSNorm (one block covers K; with a K split the
     // finishing block reads them at the end)
@@ -1155,16 +1172,23 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   // read clamped and get scale 0.
   u32x4 wq[S][CT];
   uint16_t wd[S][CT];
+  GtW<F> gw_[S][CT];
   {
     const uint32_t nt = n0 >> 4, ntl = (N - 1) >> 4;
+    const GtPlanes P = gt_planes(F, N, G);
 #pragma unroll
     for (int st = 0; st < S; st++)
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) {
         const uint32_t g = gw + 4 * st + j, t = nt + ct;
-        const size_t rec = ((size_t)(t < ntl ? t : ntl) * G + (g < G ? g : G - 1)) * 16 + c;
-        wq[st][ct] = *(const u32x4*)(B + rec * 16);
-        wd[st][ct] = D[rec];
+        const uint32_t tc = t < ntl ? t : ntl, gc = g < G ? g : G - 1;
+        const size_t rec = ((size_t)tc * G + gc) * 16 + c;
+        if (F == FMT_Q40T) {
+          wq[st][ct] = *(const u32x4*)(B + rec * 16);
+          wd[st][ct] = D[rec];
+        } else {
+          gt_load<F>(gw_[st][ct], B, P, rec, ((size_t)tc * (G / 8) + gc / 8) * 16 + c);
+        }
       }
   }
   if (threadIdx.x < 4) fragL[8 * GMAX + threadIdx.x] = (u32x4){0u, 0u, 0u, 0u};
@@ -1245,6 +1269,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         fragL[(gl * 2 + 0) * 4 + sl] = hp;
         fragL[(gl * 2 + 1) * 4 + sl] = lp;
         c1L[pl] = __builtin_fmaf(8.0f, sp_, c1p_);
+        if (NEED_S) sL[pl] = sp_;
       }
     }
   }
@@ -1254,7 +1279,15 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     for (int st = 0; st < S; st++) {
       const uint32_t g = gw + 4 * st + j;
       const uint32_t gl = (g < G ? g : G - 1) - gb;
-      c1[st] = (c1L[4 * gl] + c1L[4 * gl + 1]) + (c1L[4 * gl + 2] + c1L[4 * gl + 3]);
+      if (HALVES) {
+        c1[st] = c1L[4 * gl] + c1L[4 * gl + 1];
+        c1b[st] = c1L[4 * gl + 2] + c1L[4 * gl + 3];
+        sg[st] = sL[4 * gl] + sL[4 * gl + 1];
+        sgb[st] = sL[4 * gl + 2] + sL[4 * gl + 3];
+      } else {
+        c1[st] = (c1L[4 * gl] + c1L[4 * gl + 1]) + (c1L[4 * gl + 2] + c1L[4 * gl + 3]);
+        if (NEED_S) sg[st] = (sL[4 * gl] + sL[4 * gl + 1]) + (sL[4 * gl + 2] + sL[4 * gl + 3]);
+      }
     }
   }
 
@@ -1272,17 +1305,47 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   for (int st = 0; st < S; st++) {
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
-      f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
-      Rec<FMT_Q40T> rr;
-      rr.q = wq[st][ct];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fragL[abase[st] + i]),
-                                                   rec_to_f16<FMT_Q40T>(rr, i), p, 0, 0, 0);
       const uint32_t g = gw + 4 * st + j, n = n0 + 16 * ct + c;
-      const float sc = g < G && n < N ? (float)__builtin_bit_cast(_Float16, wd[st][ct]) : 0.f;
-      const float t = __builtin_fmaf(p[1], 1.0f / 2048.0f, p[0]) - c1[st];
-      acc[ct] = __builtin_fmaf(sc, t, acc[ct]);
+      const bool in = g < G && n < N;
+      if constexpr (F == FMT_Q40T) {
+        f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
+        Rec<FMT_Q40T> rr;
+        rr.q = wq[st][ct];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fragL[abase[st] + i]),
+                                                     rec_to_f16<FMT_Q40T>(rr, i), p, 0, 0, 0);
+        const float sc = in ? (float)__builtin_bit_cast(_Float16, wd[st][ct]) : 0.f;
+        const float t = __builtin_fmaf(p[1], 1.0f / 2048.0f, p[0]) - c1[st];
+        acc[ct] = __builtin_fmaf(sc, t, acc[ct]);
+      } else {
+        // sum of a*(s*q + c) = s*X + (8s + c)*S with X = P - C1 (C1 carries
+        // the +8S of the act): per group, or per 16-element half (Q6_K)
+        const GtW<F>& w = gw_[st][ct];
+        const u32x4* fa = fragL + abase[st];
+        f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f}, p2 = (f32x4){0.f, 0.f, 0.f, 0.f};
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[0]), gt_to_f16<F, 0>(w), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[1]), gt_to_f16<F, 1>(w), p, 0, 0, 0);
+        if (HALVES) {
+          p2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[2]), gt_to_f16<F, 2>(w), p2, 0, 0, 0);
+          p2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[3]), gt_to_f16<F, 3>(w), p2, 0, 0, 0);
+        } else {
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[2]), gt_to_f16<F, 2>(w), p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[3]), gt_to_f16<F, 3>(w), p, 0, 0, 0);
+        }
+        float s0, a0, s1, a1;
+        gt_affine<F>(w, s0, a0, s1, a1);
+        s0 = in ? s0 : 0.f;
+        a0 = in ? a0 : 0.f;
+        const float t = __builtin_fmaf(p[1], 1.0f / 2048.0f, p[0]) - c1[st];
+        acc[ct] = __builtin_fmaf(s0, t, __builtin_fmaf(__builtin_fmaf(8.0f, s0, a0), sg[st], acc[ct]));
+        if (HALVES) {
+          s1 = in ? s1 : 0.f;
+          a1 = in ? a1 : 0.f;
+          const float t2 = __builtin_fmaf(p2[1], 1.0f / 2048.0f, p2[0]) - c1b[st];
+          acc[ct] = __builtin_fmaf(s1, t2, __builtin_fmaf(__builtin_fmaf(8.0f, s1, a1), sgb[st], acc[ct]));
+        }
+      }
     }
   }
 
@@ -1349,45 +1412,48 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   }
 }
 
-#define DEF_AGEMV(NAME, CT, S, WK)                                                                           \
+#define DEF_AGEMV(NAME, F, CT, S, WK)                                                                         \
   extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                                \
       const uint8_t* __restrict__ act, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,        \
       float* __restrict__ C, uint32_t N, uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,   \
       uint32_t epi, uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out, float* __restrict__ ws, \
       uint32_t* __restrict__ counters) {                                                                     \
-    agemv_body<CT, S, WK, 0>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters,        \
-                             nullptr, 0);                                                                    \
+    agemv_body<F, CT, S, WK, 0>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters,     \
+                                nullptr, 0);                                                                 \
   }
 
 // o-projection on attention split partials (SRC 1); parts in place of the act
-#define DEF_AGEMV_ATT(NAME, CT, S, WK)                                                                       \
+#define DEF_AGEMV_ATT(NAME, F, CT, S, WK)                                                                     \
   extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                                \
       const float* __restrict__ parts, const int32_t* __restrict__ pos_ptr, uint32_t hd,                     \
       const uint8_t* __restrict__ B, const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t N,       \
       uint32_t K, const float* __restrict__ R, uint32_t epi, uint8_t* __restrict__ act_out,                   \
       const float* __restrict__ gamma_out, float* __restrict__ ws, uint32_t* __restrict__ counters) {        \
-    agemv_body<CT, S, WK, 1>((const uint8_t*)parts, B, D, C, N, K, 0u, 0.f, R, epi, act_out, gamma_out, ws,  \
+    agemv_body<F, CT, S, WK, 1>((const uint8_t*)parts, B, D, C, N, K, 0u, 0.f, R, epi, act_out, gamma_out, ws, \
                              counters, pos_ptr, hd);                                                         \
   }
 
 // named by the groups one block covers (4*S*WK) and the column tiles per wave;
 // a K longer than one block is split over gridDim.y blocks
-DEF_AGEMV(smith_agemv_q40t_k32, 1, 2, 4)
-DEF_AGEMV(smith_agemv_q40t_k48, 1, 3, 4)
-DEF_AGEMV(smith_agemv_q40t_k64, 1, 4, 4)
-DEF_AGEMV(smith_agemv_q40t_k72, 1, 3, 6)
-DEF_AGEMV(smith_agemv_q40t_k96, 1, 3, 8)
-DEF_AGEMV(smith_agemv_q40t_k128, 1, 4, 8)
-DEF_AGEMV(smith_agemv_q40t_k144, 1, 3, 12)
-DEF_AGEMV(smith_agemv_q40t_k192, 1, 6, 8)
-DEF_AGEMV(smith_agemv_q40t_k288, 1, 9, 8)
-DEF_AGEMV(smith_agemv_q40t_k96_c2, 2, 3, 8)
-DEF_AGEMV(smith_agemv_q40t_k128_c2, 2, 4, 8)
-DEF_AGEMV(smith_agemv_q40t_k144_c2, 2, 3, 12)
-DEF_AGEMV_ATT(smith_agemv_att_q40t_k64, 1, 4, 4)
-DEF_AGEMV_ATT(smith_agemv_att_q40t_k96, 1, 3, 8)
-DEF_AGEMV_ATT(smith_agemv_att_q40t_k128, 1, 4, 8)
-DEF_AGEMV_ATT(smith_agemv_att_q40t_k192, 1, 6, 8)
+#define DEF_AGEMV_FMT(TAG, F)                                 \
+  DEF_AGEMV(smith_agemv_##TAG##_k32, F, 1, 2, 4)              \
+  DEF_AGEMV(smith_agemv_##TAG##_k48, F, 1, 3, 4)              \
+  DEF_AGEMV(smith_agemv_##TAG##_k64, F, 1, 4, 4)              \
+  DEF_AGEMV(smith_agemv_##TAG##_k72, F, 1, 3, 6)              \
+  DEF_AGEMV(smith_agemv_##TAG##_k96, F, 1, 3, 8)              \
+  DEF_AGEMV(smith_agemv_##TAG##_k128, F, 1, 4, 8)             \
+  DEF_AGEMV(smith_agemv_##TAG##_k144, F, 1, 3, 12)            \
+  DEF_AGEMV(smith_agemv_##TAG##_k192, F, 1, 6, 8)             \
+  DEF_AGEMV(smith_agemv_##TAG##_k288, F, 1, 9, 8)             \
+  DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k64, F, 1, 4, 4)      \
+  DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k96, F, 1, 3, 8)      \
+  DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k128, F, 1, 4, 8)     \
+  DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k192, F, 1, 6, 8)
+DEF_AGEMV_FMT(q40t, FMT_Q40T)
+DEF_AGEMV_FMT(q41t, GT_Q41)
+DEF_AGEMV_FMT(q50t, GT_Q50)
+DEF_AGEMV_FMT(q4kt, GT_Q4K)
+DEF_AGEMV_FMT(q6kt, GT_Q6K)
 
 #ifndef SMITH_NO_INSTANCES
 DEF_QGEMV3_FMT(q4s, FMT_Q4S)

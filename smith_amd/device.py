@@ -85,6 +85,14 @@ SYMBOLS = {
     "smith_linear_q4_0_t_attn": (_INT, [_P, _P, _P, _U32, _P, _P, _P, _U32, _U32, _P, _U32, _P, _P]),
     "smith_linear_q4_0_t_act": (_INT, [_P, _P, ctypes.c_int, ctypes.c_float, _P, _P, _P, _U32, _U32, _P, _U32, _P,
                                        _P]),
+    "smith_gguf_tiles_bytes": (_U64, [_U32, _U32, _U32]),
+    "smith_copy_2d": (_INT, [_P, _P, _U64, _P, _U64, _U64, _U64]),
+    "smith_repack_gguf_tiles_into": (_INT, [_P, _U32, _P, _P, _U32, _U32, _U32, _U32, _U32]),
+    "smith_linear_gguf_tiles": (_INT, [_P, _U32, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
+    "smith_linear_gguf_tiles_act": (_INT, [_P, _U32, _P, ctypes.c_int, ctypes.c_float, _P, _P, _U32, _U32, _P,
+                                           _U32, _P, _P]),
+    "smith_linear_gguf_tiles_attn": (_INT, [_P, _U32, _P, _P, _U32, _P, _P, _U32, _U32, _P, _U32, _P, _P]),
+    "smith_dequantize_gguf": (_INT, [_P, _U32, _P, _P, _U64]),
     "smith_linear_q8": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
     "smith_rmsnorm": (_INT, [_P, _P, _P, _P, _U32, _U32, ctypes.c_float]),
     "smith_embed": (_INT, [_P, _P, _P, _P, _U32, _U32, _P, _P]),

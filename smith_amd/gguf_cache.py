@@ -12,14 +12,15 @@ then the LM head (final RMSNorm fused) and a device-side greedy step
 lives in device memory, so the greedy decode step is captured once as a HIP
 graph and replayed.
 
-Single-row steps on Q4_0 models pass activations between kernels as "acts"
-(the vector already in the GEMV's MFMA operand form, with per-8-element sums
-and sums of squares; smith_linear_q4_0_t_act): every producer -- embedding,
+Single-row steps on models whose linears have tile layouts (Q4_0, Q4_1,
+Q5_0, Q4_K, Q6_K) pass activations between kernels as "acts" (the vector
+already in the GEMV's MFMA operand form, with per-8-element sums and sums of
+squares; smith_linear_q4_0_t_act / smith_linear_gguf_tiles_act): every producer -- embedding,
 o-proj, gate|up, down -- writes the act its consumer reads, with the next
 RMSNorm's gamma folded in, and the consumer applies the norm's rms as one
 scalar.  Attention leaves its key-split partials to the o-projection, which
 combines them while it builds its operand (smith_attention_parts +
-smith_linear_q4_0_t_attn; head_dim % 32 == 0, else attention writes an act).
+smith_linear_*_attn; head_dim % 32 == 0, else attention writes an act).
 Prefill rows (M > 1) take the f32 path.
 """
 import os
@@ -77,8 +78,7 @@ class _Engine:
         self.graph = None
         self.graph_caches = None
         hd = cfg["headDim"]
-        self.use_act = (all(b[k].kind == "q4_0t" for b in model["blocks"] for k in ("qkv", "outProj", "gateUp",
-                                                                                   "ffnDown"))
+        self.use_act = (all(b[k].has_act for b in model["blocks"] for k in ("qkv", "outProj", "gateUp", "ffnDown"))
                         and dim % 32 == 0 and ffn % 32 == 0 and hd % 8 == 0 and cfg["numHeads"] * hd == dim)
 
         def act(K):
@@ -127,10 +127,7 @@ class _Engine:
                 device.check(device.lib.smith_attention_parts(
                     ctx, qkv, self.pos.ptr, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"], rope["cos"].ptr,
                     rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], parts), "attention")
-                o = blk["outProj"]
-                device.check(device.lib.smith_linear_q4_0_t_attn(
-                    ctx, parts, self.pos.ptr, cfg["headDim"], o.a.ptr, o.b.ptr, x2, o.N, o.K, x, 1, ax2,
-                    blk["ln2Gamma"].ptr), "o-proj (attention partials)")
+                blk["outProj"].attn(parts, self.pos.ptr, cfg["headDim"], x2, x, 1, ax2, blk["ln2Gamma"].ptr)
             else:
                 device.check(device.lib.smith_attention(
                     ctx, qkv, self.qkv_ld, self.pos.ptr, 1, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],

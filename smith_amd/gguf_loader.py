@@ -2,16 +2,20 @@
 
 Differences from the reference, all on purpose: the
 reference dequantizes every tensor to f32 at load (gguf_loader.js:236) and
-runs f32 GEMMs; here Q4_0 / Q8_0 linear weights stay quantized on the device
-and `linear` runs the quantized GEMV.  The blocks are only moved (never
-changed) into the kernels' layouts:
-  * q|k|v of a layer side by side in one buffer (one GEMV per layer),
+runs f32 GEMMs; here Q4_0 / Q4_1 / Q5_0 / Q8_0 / Q4_K / Q6_K linear weights
+stay quantized on the device and `linear` runs the quantized GEMV.  The
+blocks are only moved (never changed) into the kernels' layouts:
+  * q|k|v of a layer side by side in one buffer (one GEMV per layer) when
+    they share a block type, else three GEMVs writing the column ranges of
+    the same q|k|v rows (Q4_K_M files keep attn_v in Q6_K),
   * gate/up interleaved column by column (the SwiGLU epilogue pairs them),
   * output.weight kept as stored: the reference reads its flat data as
     lmHead[dim][vocab] (gguf_loader.js:240-259 only transposes paths ending
     in ".weight"), so its Q4_0 blocks run along the vocab axis and it gets
     its own GEMV (smith_lmhead_q4_0_nb).
-Norms and the token embedding are f32 on the device.
+Norms and the token embedding are f32 on the device (a quantized
+token_embd, or an output.weight of a type without its own GEMV, is decoded
+on the device by smith_dequantize_gguf, bit-identical to dequantizeTensor).
 """
 import numpy as np
 
@@ -84,52 +88,132 @@ class DeviceArray:
         return device.download(self.ptr, self.nbytes, self.dtype).reshape(self.shape)
 
 
+GT_TYPES = {G.GGML_TYPE[t] for t in ("Q4_1", "Q5_0", "Q4_K", "Q6_K")}
+
+
 class QLinear:
     """A quantized linear weight on the device: y = x . W with W [in=K, out=N].
-    kind 'q4_0t': tile-major nib/d planes; kind 'q8': matmulQ8 records."""
+    kind 'q4_0t': tile-major nib/d planes; kind 'q8': matmulQ8 records;
+    kind 'gt': the tile planes of another GGUF block type (ggml_type)."""
 
-    def __init__(self, kind, K, N, a, b=None):
-        self.kind, self.K, self.N, self.a, self.b = kind, K, N, a, b
+    def __init__(self, kind, K, N, a, b=None, ggml_type=None):
+        self.kind, self.K, self.N, self.a, self.b, self.ggml_type = kind, K, N, a, b, ggml_type
 
     def __call__(self, x_ptr, out_ptr, M, gamma=None, eps=0.0, resid=None, epilogue=0):
         ctx = device.ops_ctx()
         if self.kind == "q4_0t":
             rc = device.lib.smith_linear_q4_0_t(ctx, x_ptr, self.a.ptr, self.b.ptr, out_ptr, M, self.N, self.K,
                                                 gamma, eps, resid, epilogue)
+        elif self.kind == "gt":
+            rc = device.lib.smith_linear_gguf_tiles(ctx, self.ggml_type, x_ptr, self.a.ptr, out_ptr, M, self.N,
+                                                    self.K, gamma, eps, resid, epilogue)
         else:
             rc = device.lib.smith_linear_q8(ctx, x_ptr, self.a.ptr, out_ptr, M, self.N, self.K, gamma, eps,
                                             resid, epilogue)
         device.check(rc, "linear")
 
+    @property
+    def has_act(self):
+        return self.kind in ("q4_0t", "gt")
+
     def act(self, act_in, norm, eps, out_ptr, resid=None, epilogue=0, act_out=None, gamma_out=None):
-        """Single-row linear on a prepared activation (smith_linear_q4_0_t_act)."""
-        rc = device.lib.smith_linear_q4_0_t_act(device.ops_ctx(), act_in, 1 if norm else 0, eps, self.a.ptr,
-                                                self.b.ptr, out_ptr, self.N, self.K, resid, epilogue, act_out,
-                                                gamma_out)
+        """Single-row linear on a prepared activation (smith_linear_*_act)."""
+        if self.kind == "q4_0t":
+            rc = device.lib.smith_linear_q4_0_t_act(device.ops_ctx(), act_in, 1 if norm else 0, eps, self.a.ptr,
+                                                    self.b.ptr, out_ptr, self.N, self.K, resid, epilogue, act_out,
+                                                    gamma_out)
+        else:
+            rc = device.lib.smith_linear_gguf_tiles_act(device.ops_ctx(), self.ggml_type, act_in, 1 if norm else 0,
+                                                        eps, self.a.ptr, out_ptr, self.N, self.K, resid, epilogue,
+                                                        act_out, gamma_out)
         device.check(rc, "linear (act)")
+
+    def attn(self, parts, pos_ptr, head_dim, out_ptr, resid, epilogue, act_out, gamma_out):
+        """Single-row linear on attention split partials (smith_linear_*_attn)."""
+        ctx = device.ops_ctx()
+        if self.kind == "q4_0t":
+            rc = device.lib.smith_linear_q4_0_t_attn(ctx, parts, pos_ptr, head_dim, self.a.ptr, self.b.ptr, out_ptr,
+                                                     self.N, self.K, resid, epilogue, act_out, gamma_out)
+        else:
+            rc = device.lib.smith_linear_gguf_tiles_attn(ctx, self.ggml_type, parts, pos_ptr, head_dim, self.a.ptr,
+                                                         out_ptr, self.N, self.K, resid, epilogue, act_out, gamma_out)
+        device.check(rc, "o-proj (attention partials)")
+
+
+class QGroup:
+    """Linears of different block types sharing one input and writing the
+    column ranges [off, off + N_i) of one [M, N] output (q|k|v)."""
+
+    def __init__(self, parts):
+        self.parts = parts  # [(QLinear, column offset)]
+        self.K = parts[0][0].K
+        self.N = sum(q.N for q, _ in parts)
+        self.kind = "group"
+        self._tmp = None
+
+    @property
+    def has_act(self):
+        return all(q.has_act for q, _ in self.parts)
+
+    def __call__(self, x_ptr, out_ptr, M, gamma=None, eps=0.0, resid=None, epilogue=0):
+        if resid is not None or epilogue:
+            raise NotImplementedError("epilogues on a mixed-type linear group")
+        if M == 1:
+            for q, off in self.parts:
+                q(x_ptr, out_ptr + off * 4, 1, gamma, eps)
+            return
+        need = M * max(q.N for q, _ in self.parts) * 4
+        if self._tmp is None or self._tmp.nbytes < need:
+            self._tmp = DeviceArray((need // 4,))
+        ctx = device.ops_ctx()
+        for q, off in self.parts:
+            q(x_ptr, self._tmp.ptr, M, gamma, eps)
+            device.check(device.lib.smith_copy_2d(ctx, out_ptr + off * 4, self.N * 4, self._tmp.ptr, q.N * 4, q.N * 4,
+                                                  M), "group copy")
+
+    def act(self, act_in, norm, eps, out_ptr, resid=None, epilogue=0, act_out=None, gamma_out=None):
+        if resid is not None or epilogue or act_out is not None:
+            raise NotImplementedError("epilogues on a mixed-type linear group")
+        for q, off in self.parts:
+            q.act(act_in, norm, eps, out_ptr + off * 4)
 
 
 def _pack_group(parsed, infos, K, cols, interleave):
-    """Repack one or more [out, in] Q4_0 / Q8_0 weights into one device
-    buffer: side by side (interleave=False) or column-interleaved."""
-    types = {i["type"] for i in infos}
-    if len(types) != 1:
-        raise ValueError("fused weights must share one GGML type, got %s" % sorted(types))
-    t = types.pop()
+    """Repack one or more [out, in] quantized weights into one device buffer:
+    side by side (interleave=False) or column-interleaved.  Weights of
+    different block types side by side become a QGroup."""
+    types = [i["type"] for i in infos]
+    if len(set(types)) != 1:
+        if interleave:
+            raise NotImplementedError("interleaved weights of different GGML types (%s)"
+                                      % ", ".join(G.GGML_TYPE_NAME.get(t, str(t)) for t in types))
+        parts, off = [], 0
+        for info, n in zip(infos, cols):
+            parts.append((_pack_group(parsed, [info], K, [n], False), off))
+            off += n
+        return QGroup(parts)
+    t = types[0]
     Ntot = sum(cols)
     Gk = K // 32
     ctx = device.ops_ctx()
+    dsc = None
     if t == G.GGML_TYPE["Q4_0"]:
         nib = DeviceArray((Gk * Ntot * 16,), np.uint8)
         dsc = DeviceArray((Gk * Ntot,), np.uint16)
         kind = "q4_0t"
     elif t == G.GGML_TYPE["Q8_0"]:
         nib = DeviceArray((Gk * Ntot * 34,), np.uint8)
-        dsc = None
         kind = "q8"
+    elif t in GT_TYPES:
+        nbytes = int(device.lib.smith_gguf_tiles_bytes(t, Ntot, K))
+        if not nbytes:
+            raise NotImplementedError("%s weight [%d, %d]: needs out %% 16 == 0 and in %% %d == 0"
+                                      % (G.GGML_TYPE_NAME[t], Ntot, K, 256 if t in (12, 14) else 32))
+        nib = DeviceArray((nbytes,), np.uint8)
+        kind = "gt"
     else:
-        raise NotImplementedError("linear weight type %s is not on the quantized path (Q4_0, Q8_0 only)"
-                                  % G.GGML_TYPE_NAME.get(t, t))
+        raise NotImplementedError("linear weight type %s is not on the quantized path "
+                                  "(Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q6_K)" % G.GGML_TYPE_NAME.get(t, t))
     off = 0
     for j, (info, n) in enumerate(zip(infos, cols)):
         raw = G.readTensorData(parsed, info)
@@ -137,13 +221,28 @@ def _pack_group(parsed, infos, K, cols, interleave):
         n_off, stride = (j, len(infos)) if interleave else (off, 1)
         if kind == "q4_0t":
             rc = device.lib.smith_repack_q4_0_t_into(ctx, src.ptr, nib.ptr, dsc.ptr, n, K, n_off, stride, Ntot)
+        elif kind == "gt":
+            rc = device.lib.smith_repack_gguf_tiles_into(ctx, t, src.ptr, nib.ptr, n, K, n_off, stride, Ntot)
         else:
             rc = device.lib.smith_repack_q8_0_into(ctx, src.ptr, nib.ptr, n, K, n_off, stride, Ntot)
         device.check(rc, "repack %s" % info["name"])
         device.sync()
         device.release_buffer(src.ptr)
         off += n
-    return QLinear(kind, K, Ntot, nib, dsc)
+    return QLinear(kind, K, Ntot, nib, dsc, ggml_type=t)
+
+
+def device_f32(parsed, info):
+    """Any dequantizable tensor as an f32 device array (dequantizeTensor,
+    src/gguf.js:343-394, on the device)."""
+    numel = int(np.prod(info["shape"]))
+    out = DeviceArray((numel,))
+    raw = DeviceArray.from_host(np.asarray(G.readTensorData(parsed, info)), np.uint8)
+    device.check(device.lib.smith_dequantize_gguf(device.ops_ctx(), info["type"], raw.ptr, out.ptr, numel),
+                 "dequantize %s" % info["name"])
+    device.sync()
+    device.release_buffer(raw.ptr)
+    return out
 
 
 def createGGUFModel(config):
@@ -193,7 +292,10 @@ def loadWeights(parsed, model):
     E = by_path.get("embedding.tokenWeight")
     if E is None:
         raise ValueError("token_embd.weight missing")
-    model["embedding"] = DeviceArray.from_host(G.dense_f32(parsed, E).reshape(vocab, dim))
+    if E["type"] in (G.GGML_TYPE["F32"], G.GGML_TYPE["F16"]):
+        model["embedding"] = DeviceArray.from_host(G.dense_f32(parsed, E).reshape(vocab, dim))
+    else:
+        model["embedding"] = device_f32(parsed, E)
     for L, blk in enumerate(model["blocks"]):
         p = "blocks.%d." % L
         q, k, v = (by_path[p + "mha.%sProj.weight" % n] for n in ("q", "k", "v"))
@@ -228,7 +330,9 @@ def loadWeights(parsed, model):
     elif head["type"] in (G.GGML_TYPE["F32"], G.GGML_TYPE["F16"]):
         model["lmHead"] = {"kind": "f32_kn", "w": DeviceArray.from_host(G.dense_f32(parsed, head))}
     else:
-        raise NotImplementedError("output.weight type %s" % G.GGML_TYPE_NAME.get(head["type"], head["type"]))
+        # other block types: decoded once to the f32 [dim][vocab] the reference
+        # builds (its blocks run along vocab, so no K-blocked GEMV applies)
+        model["lmHead"] = {"kind": "f32_kn", "w": device_f32(parsed, head)}
     device.sync()
     return {"loaded": loaded, "skipped": skipped}
 

@@ -1,5 +1,9 @@
-"""Tiny Llama GGUF files written on the CPU (numpy + the oracle's Q4_0 / Q8_0
-encoders), with the same layout choices as smith_amd.synthetic_gguf."""
+"""Tiny Llama GGUF files written on the CPU (numpy + the oracle's block
+encoders), with the same layout choices as smith_amd.synthetic_gguf.
+
+linear_type sets every linear weight's block type; `types` overrides it per
+linear ({"attn_v": "q6_k", ...}); embd_type / head_type set token_embd's and
+output.weight's types (f32 / q4_0 by default)."""
 import numpy as np
 
 from oracle import oracle as O
@@ -8,7 +12,8 @@ from smith_amd import prng
 
 
 def write_tiny_llama(path, dim=64, layers=2, heads=4, kv_heads=2, ffn=96, vocab=96, context=512, seed=3,
-                     linear_type="q4_0", tie=False, kv_override=None, head_f32=None, std=0.05):
+                     linear_type="q4_0", tie=False, kv_override=None, head_f32=None, std=0.05, types=None,
+                     embd_type="f32", head_type="q4_0"):
     hd = dim // heads
     kvd = kv_heads * hd
     T = G.GGUF_TYPE
@@ -24,8 +29,10 @@ def write_tiny_llama(path, dim=64, layers=2, heads=4, kv_heads=2, ffn=96, vocab=
         "llama.attention.layer_norm_rms_epsilon": (T["FLOAT32"], 1e-5),
         "llama.vocab_size": (T["UINT32"], vocab),
     }
-    gt = G.GGML_TYPE["Q4_0"] if linear_type == "q4_0" else G.GGML_TYPE["Q8_0"]
-    bpb = 18 if linear_type == "q4_0" else 34
+    types = dict(types or {})
+
+    def ttype(name):
+        return G.GGML_TYPE[name.upper()]
     s = [seed * 7919]
 
     def nxt():
@@ -38,12 +45,17 @@ def write_tiny_llama(path, dim=64, layers=2, heads=4, kv_heads=2, ffn=96, vocab=
 
     def lin(name, out_, in_, arr=None):
         w = prng.randn((out_, in_), nxt(), std=std) if arr is None else arr
-        q = O.quantize_rows(gt, w)
-        return (name, [out_, in_], gt, q.size, lambda q=q: q)
+        t = ttype(types.get(name.split(".")[2], linear_type))
+        q = O.quantize_rows(t, w)
+        return (name, [out_, in_], t, q.size, lambda q=q: q)
 
     tensors = []
     E = prng.randn((vocab, dim), nxt(), std=std)
-    tensors.append(f32("token_embd.weight", (vocab, dim), arr=E))
+    if embd_type == "f32":
+        tensors.append(f32("token_embd.weight", (vocab, dim), arr=E))
+    else:
+        qe = O.quantize_rows(ttype(embd_type), E)
+        tensors.append(("token_embd.weight", [vocab, dim], ttype(embd_type), qe.size, lambda q=qe: q))
     for L in range(layers):
         p = "blk.%d." % L
         tensors.append(f32(p + "attn_norm.weight", (dim,), 0.02, 1.0))
@@ -66,7 +78,7 @@ def write_tiny_llama(path, dim=64, layers=2, heads=4, kv_heads=2, ffn=96, vocab=
     elif not tie:
         # flat data = lmHead[dim][vocab], quantized along vocab
         w = prng.randn((dim, vocab), nxt(), std=std)
-        q = O.quantize_rows(G.GGML_TYPE["Q4_0"], w)
-        tensors.append(("output.weight", [dim, vocab], G.GGML_TYPE["Q4_0"], q.size, lambda q=q: q))
+        q = O.quantize_rows(ttype(head_type), w)
+        tensors.append(("output.weight", [dim, vocab], ttype(head_type), q.size, lambda q=q: q))
     G.write_gguf(path, meta, tensors)
     return E

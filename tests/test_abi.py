@@ -47,9 +47,9 @@ def test_code_object_has_kernels():
             "smith_repack_q4_0_cols", "smith_repack_q8_0_cols", "smith_repack_q4_0_tiles", "smith_zero_u32"]
     for fmt in ("q4", "q8", "q40"):
         need += ["smith_qprep_%s_hilo" % fmt, "smith_qprep_%s_plain" % fmt]
-    need += ["smith_agemv_q40t_k%d" % k for k in (32, 48, 64, 72, 96, 128, 144, 192, 288)]
-    need += ["smith_agemv_q40t_k%d_c2" % k for k in (96, 128, 144)]
-    need += ["smith_agemv_att_q40t_k%d" % k for k in (64, 96, 128, 192)]
+    for fmt in ("q40t", "q41t", "q50t", "q4kt", "q6kt"):
+        need += ["smith_agemv_%s_k%d" % (fmt, k) for k in (32, 48, 64, 72, 96, 128, 144, 192, 288)]
+        need += ["smith_agemv_att_%s_k%d" % (fmt, k) for k in (64, 96, 128, 192)]
     for fmt in ("q4s", "q8", "q40", "q40t"):
         need += ["smith_qgemv3_%s_m%d" % (fmt, m) for m in (4, 8, 16, 32)]
         need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 96, 128, 288)]
@@ -59,14 +59,16 @@ def test_code_object_has_kernels():
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.GEMM_CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     for k in ["smith_gemm_prep_a", "smith_gemm_reduce"] + [
-            "smith_gemm_%s_m%d_n%d" % (f, m, n) for f in ("q4s", "q8", "q40", "q40t")
+            "smith_gemm_%s_m%d_n%d" % (f, m, n) for f in ("q4s", "q8", "q40", "q40t", "q41t", "q50t", "q4kt", "q6kt")
             for (m, n) in ((128, 64), (128, 128), (256, 128), (256, 256))]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_attention_part", "smith_kv_append", "smith_attention_cached",
               "smith_lmhead_q4_0_nb", "smith_repack_lmhead_q4_0",
-              "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"]:
+              "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"] + [
+              "smith_repack_gt_%s" % f for f in ("q40", "q41", "q50", "q4k", "q6k")] + [
+              "smith_dequantize_%s" % t for t in ("f16", "bf16", "q4_0", "q4_1", "q5_0", "q8_0", "q4_k", "q6_k")]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
 
 

@@ -1,0 +1,308 @@
+"""GPU parity of the other GGUF block types (Q4_1, Q5_0, Q4_K, Q6_K; Q4_0
+and Q8_0 alongside where the entry point takes them):
+
+  * smith_dequantize_gguf vs the oracle's dequantizeTensor: bit-exact, also
+    on random block bytes (finite f16 fields) and a ragged element count;
+  * smith_repack_gguf_tiles_into: the planes decoded on the host by the
+    documented layout (nib / permuted high bits / prm / sup in 16-column
+    tiles) reproduce the oracle's f32 weights exactly, for side-by-side and
+    interleaved placement;
+  * smith_linear_gguf_tiles_act / _attn (exact weights): normwise 5e-5 of
+    the float64 product with the oracle's weights (SwiGLU 1.5e-4).  The
+    exponent-bias operand (f16 1024 + q) makes each group's f32 MFMA sum
+    about 1024 * sum|a| before the offset is taken off, so a group carries
+    ~2^-24 * 1024 * sum|a| of rounding: normwise ~1e-5 .. 2.5e-5 at
+    K = 3072 (Q4_0 seeds included), hence 5e-5;
+  * smith_linear_gguf_tiles (MFMA GEMM, f16 weights and activations):
+    normwise 1e-2, the GEMM bar of the Q4_0 tests;
+  * loadGGUF(...).generate on a tiny model with the Q4_K_M mix (Q4_K
+    q/k/o/gate/up, Q6_K v/down, Q6_K output.weight, Q4_K token_embd) and on
+    Q4_1 / Q5_0 / Q6_K models, against the Llama oracle (as test_gpu_llama).
+"""
+import numpy as np
+import pytest
+
+from oracle import llama_oracle as LO
+from oracle import oracle as O
+from oracle.oracle import normwise_rel_err
+from smith_amd import device, prng
+from tests.llama_fixtures import write_tiny_llama
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-5
+TOL_SWIGLU = 1.5e-4
+TOL_GEMM = 1e-2
+EPS = 1e-5
+KQ = [O.GGML_Q4_1, O.GGML_Q5_0, O.GGML_Q4_K, O.GGML_Q6_K]
+ALL_TILE = [O.GGML_Q4_0] + KQ
+
+
+def _buf(a):
+    a = np.ascontiguousarray(a)
+    b = device.alloc(max(a.nbytes, 4))
+    device.upload(b, a)
+    return b
+
+
+def _get(b, n, dt=np.float32):
+    device.sync()
+    return device.download(b, n * np.dtype(dt).itemsize, dt)
+
+
+def _rms(x, g):
+    return x / np.sqrt(np.mean(x * x) + EPS) * g
+
+
+def _silu_mul(y):
+    g, u = y[0::2], y[1::2]
+    return g / (1 + np.exp(-g)) * u
+
+
+def _weights(t, N, K, seed):
+    w = prng.randn((N, K), seed, std=0.02)
+    blocks = O.quantize_rows(t, w)
+    wd = O.dequantize_tensor(t, blocks, N * K).reshape(N, K)
+    return blocks, wd
+
+
+def _planes(t, blocks, N, K, parts=None):
+    nbytes = int(device.lib.smith_gguf_tiles_bytes(t, N, K))
+    assert nbytes
+    pl = device.alloc(nbytes)
+    ctx = device.ops_ctx()
+    for (b, n, off, stride) in parts or [(blocks, N, 0, 1)]:
+        src = _buf(b)
+        device.check(device.lib.smith_repack_gguf_tiles_into(ctx, t, src, pl, n, K, off, stride, N))
+        device.sync()
+        device.release_buffer(src)
+    return pl, nbytes
+
+
+# ---------------- dequantizeTensor ----------------
+
+@pytest.mark.parametrize("t", [O.GGML_F16, O.GGML_BF16, O.GGML_Q4_0, O.GGML_Q8_0] + KQ)
+def test_dequantize_bit_exact(t):
+    be, bb = O.BLOCK[t]
+    ctx = device.ops_ctx()
+    rng = np.random.default_rng(t)
+    if be == 1:
+        raw = rng.integers(0, 1 << 16, 4099, dtype=np.uint16)
+        if t == O.GGML_F16:
+            raw[(raw & 0x7C00) == 0x7C00] &= 0xBFFF  # finite halves
+        raw = raw.view(np.uint8)
+        numel = 4099
+    else:
+        enc = O.quantize_rows(t, prng.randn((6, 4 * be), 90 + t, std=0.05))
+        rnd = rng.integers(0, 256, 40 * bb, dtype=np.uint8).reshape(40, bb)
+        # finite f16 fields in the random blocks
+        f16_at = {O.GGML_Q4_0: [0], O.GGML_Q8_0: [0], O.GGML_Q4_1: [0, 2], O.GGML_Q5_0: [0],
+                  O.GGML_Q4_K: [0, 2], O.GGML_Q6_K: [208]}[t]
+        for o in f16_at:
+            rnd[:, o + 1] &= 0x3B  # exponent < 31, magnitude < 1
+        raw = np.concatenate([enc, rnd.ravel()])
+        numel = (raw.size // bb) * be - 5  # ragged tail
+    src, dst = _buf(raw), device.alloc(numel * 4)
+    device.check(device.lib.smith_dequantize_gguf(ctx, t, src, dst, numel))
+    got = _get(dst, numel)
+    want = O.dequantize_tensor(t, raw, numel)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------- tile planes ----------------
+
+def _decode_planes(t, data, N, K):
+    """Host decoder of the tile planes (layout of gguf_tiles.h) -> [N, K]."""
+    G = K // 32
+    R = N * G
+    al = lambda x: (x + 255) & ~255
+    hbB = {O.GGML_Q5_0: 4, O.GGML_Q6_K: 8}.get(t, 0)
+    pB = 4 if t == O.GGML_Q4_1 else 2
+    supB = {O.GGML_Q4_K: 4, O.GGML_Q6_K: 2}.get(t, 0)
+    o_hb = al(R * 16)
+    o_p = al(o_hb + R * hbB)
+    o_s = al(o_p + R * pB)
+    h16 = lambda u: float(np.array([u & 0xFFFF], np.uint16).view(np.float16)[0])
+    out = np.zeros((N, K), np.float64)
+    for n in range(N):
+        for g in range(G):
+            rec = ((n // 16) * G + g) * 16 + n % 16
+            nb = data[rec * 16:rec * 16 + 16]
+            q = np.array([(nb[e // 2] >> (4 * (e % 2))) & 15 for e in range(32)], np.int64)
+            if hbB:
+                words = data[o_hb + rec * hbB:o_hb + rec * hbB + hbB].view(np.uint32)
+                for e in range(32):
+                    i, k = e >> 3, e & 7
+                    if t == O.GGML_Q5_0:
+                        q[e] |= ((int(words[0]) >> (4 * i + (k & 3) + 16 * (k >> 2))) & 1) << 4
+                    else:
+                        pos = 2 * (4 * (i & 1) + (k & 3)) + 16 * (k >> 2)
+                        q[e] |= ((int(words[i >> 1]) >> pos) & 3) << 4
+            p = int(data[o_p + rec * pB:o_p + rec * pB + pB].view(np.uint32 if pB == 4 else np.uint16)[0])
+            srec = ((n // 16) * (G // 8) + g // 8) * 16 + n % 16
+            sp = int(data[o_s + srec * supB:o_s + srec * supB + supB].view(np.uint32 if supB == 4 else np.uint16)[0]) \
+                if supB else 0
+            if t == O.GGML_Q4_0:
+                v = h16(p) * (q - 8)
+            elif t == O.GGML_Q5_0:
+                v = h16(p) * (q - 16)
+            elif t == O.GGML_Q4_1:
+                v = h16(p) * q + h16(p >> 16)
+            elif t == O.GGML_Q4_K:
+                v = np.float32(h16(sp) * (p & 63)) * q - np.float32(h16(sp >> 16) * ((p >> 8) & 63))
+            else:
+                sc = np.array([p & 0xFF, (p >> 8) & 0xFF], np.uint8).view(np.int8).astype(np.float64)
+                v = h16(sp) * np.repeat(sc, 16) * (q - 32)
+            out[n, 32 * g:32 * g + 32] = v
+    return out.astype(np.float32)
+
+
+@pytest.mark.parametrize("t", ALL_TILE)
+def test_repack_planes_decode_to_oracle_weights(t):
+    K = 512
+    b1, w1 = _weights(t, 32, K, 11 + t)
+    b2, w2 = _weights(t, 16, K, 12 + t)
+    pl, nb = _planes(t, None, 48, K, parts=[(b1, 32, 0, 1), (b2, 16, 32, 1)])
+    got = _decode_planes(t, _get(pl, nb, np.uint8), 48, K)
+    assert np.array_equal(got, np.concatenate([w1, w2]))
+    # interleaved (gate/up) placement
+    pl, nb = _planes(t, None, 64, K, parts=[(b1, 32, 0, 2), (b1, 32, 1, 2)])
+    got = _decode_planes(t, _get(pl, nb, np.uint8), 64, K)
+    assert np.array_equal(got[0::2], w1) and np.array_equal(got[1::2], w1)
+
+
+def test_tiles_rejects_bad_shapes():
+    assert device.lib.smith_gguf_tiles_bytes(O.GGML_Q4_K, 64, 288) == 0  # K % 256
+    assert device.lib.smith_gguf_tiles_bytes(O.GGML_Q5_0, 40, 288) == 0  # N % 16
+    assert device.lib.smith_gguf_tiles_bytes(O.GGML_Q8_0, 64, 256) == 0  # no tile layout
+    assert device.lib.smith_gguf_tiles_bytes(O.GGML_Q5_0, 64, 288) > 0
+    ctx = device.ops_ctx()
+    d = device.alloc(4096)
+    assert device.lib.smith_linear_gguf_tiles_act(ctx, O.GGML_Q6_K, d, 0, 0.0, d, d, 64, 288, None, 0, None,
+                                                  None) != 0
+
+
+# ---------------- act GEMV (exact weights) ----------------
+
+def _act_of(x, gamma):
+    K = x.size
+    E = _buf(np.asarray(x, np.float32))
+    tok = _buf(np.zeros(1, np.int32))
+    out = device.alloc(K * 4)
+    act = device.alloc(K * 4 + K // 8 * 12)
+    g = _buf(np.asarray(gamma, np.float32)) if gamma is not None else None
+    device.check(device.lib.smith_embed(device.ops_ctx(), E, tok, out, 1, K, act, g))
+    return act
+
+
+@pytest.mark.parametrize("t", ALL_TILE)
+@pytest.mark.parametrize("N,K", [(64, 256), (3072, 3072), (96, 9216), (48, 768)])
+def test_act_gemv_all_types(t, N, K):
+    blocks, wd = _weights(t, N, K, 21 + N + t)
+    pl, _ = _planes(t, blocks, N, K)
+    x = prng.randn((K,), 22).astype(np.float64)
+    g = 1 + prng.randn((K,), 23, std=0.1).astype(np.float64)
+    out = device.alloc(N * 4)
+    ctx = device.ops_ctx()
+    for norm in (0, 1):
+        act = _act_of(x, g if norm else None)
+        device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act, norm, EPS, pl, out, N, K, None, 0, None,
+                                                            None))
+        xn = _rms(x, g) if norm else x
+        assert normwise_rel_err(_get(out, N), wd.astype(np.float64) @ xn) <= TOL, norm
+
+
+@pytest.mark.parametrize("t", KQ)
+def test_act_gemv_epilogues_and_act_output(t):
+    """residual + act output -> SwiGLU -> residual chain on one type."""
+    D, F = 256, 512
+    ctx = device.ops_ctx()
+    b_o, wo = _weights(t, D, D, 31)
+    b_gu, wgu = _weights(t, 2 * F, D, 32)
+    b_dn, wdn = _weights(t, D, F, 33)
+    p_o, _ = _planes(t, b_o, D, D)
+    p_gu, _ = _planes(t, b_gu, 2 * F, D)
+    p_dn, _ = _planes(t, b_dn, D, F)
+    wo, wgu, wdn = (w.astype(np.float64) for w in (wo, wgu, wdn))
+    a_in = prng.randn((D,), 34).astype(np.float64)
+    x = prng.randn((D,), 35).astype(np.float64)
+    g2 = 1 + prng.randn((D,), 36, std=0.1).astype(np.float64)
+    act_a = _act_of(a_in, None)
+    xb, g2b = _buf(x.astype(np.float32)), _buf(g2.astype(np.float32))
+    x2b, act_x2 = device.alloc(D * 4), device.alloc(D * 4 + D // 8 * 12)
+    device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act_a, 0, 0.0, p_o, x2b, D, D, xb, 1, act_x2, g2b))
+    x2 = _get(x2b, D).astype(np.float64)
+    assert normwise_rel_err(x2, x + wo @ a_in) <= TOL
+    hb, act_h = device.alloc(F * 4), device.alloc(F * 4 + F // 8 * 12)
+    device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act_x2, 1, EPS, p_gu, hb, 2 * F, D, None, 2, act_h,
+                                                        None))
+    h = _get(hb, F).astype(np.float64)
+    assert normwise_rel_err(h, _silu_mul(wgu @ _rms(x2, g2))) <= TOL_SWIGLU
+    outb = device.alloc(D * 4)
+    device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act_h, 0, 0.0, p_dn, outb, D, F, x2b, 1, None, None))
+    assert normwise_rel_err(_get(outb, D), x2 + wdn @ h) <= TOL
+
+
+# ---------------- M-row linear (GEMM) ----------------
+
+@pytest.mark.parametrize("t", KQ)
+@pytest.mark.parametrize("M", [1, 5, 70, 200])
+def test_linear_gemm_all_epilogues(t, M):
+    N, K = 160, 512
+    blocks, wd = _weights(t, N, K, 41 + t)
+    pl, _ = _planes(t, blocks, N, K)
+    x = prng.randn((M, K), 42)
+    g = 1 + prng.randn((K,), 43, std=0.1)
+    r = prng.randn((M, N), 44)
+    ctx = device.ops_ctx()
+    xb, gb, rb, ob = _buf(x), _buf(g), _buf(r), device.alloc(M * N * 4)
+    xn = np.stack([_rms(x[m].astype(np.float64), g) for m in range(M)])
+    for epi in (0, 1, 2):
+        device.check(device.lib.smith_linear_gguf_tiles(ctx, t, xb, pl, ob, M, N, K, gb, EPS, rb, epi))
+        y = xn @ wd.astype(np.float64).T
+        if epi == 1:
+            y = y + r
+        if epi == 2:
+            y = np.stack([_silu_mul(y[m]) for m in range(M)])
+        got = _get(ob, y.size).reshape(y.shape)
+        assert normwise_rel_err(got, y) <= TOL_GEMM, (M, epi)
+
+
+# ---------------- end to end ----------------
+
+SMALL = dict(dim=256, layers=2, heads=4, kv_heads=2, ffn=512, vocab=320, context=2048)
+Q4_K_M = dict(linear_type="q4_k", types={"attn_v": "q6_k", "ffn_down": "q6_k"}, embd_type="q4_k", head_type="q6_k")
+
+
+def check_tokens(gpu_tokens, ref_logits):
+    for i, (tk, lg) in enumerate(zip(gpu_tokens, ref_logits)):
+        top2 = np.sort(lg)[-2:]
+        if tk != int(np.argmax(lg)):
+            assert top2[1] - top2[0] < 1e-4 * max(1.0, abs(top2[1])), (i, tk, int(np.argmax(lg)))
+
+
+@pytest.mark.parametrize("kw", [Q4_K_M, dict(linear_type="q4_1"), dict(linear_type="q5_0", head_type="q8_0"),
+                                dict(linear_type="q5_0", dim=288, heads=6, kv_heads=3, ffn=768),  # head_dim 48
+                                dict(linear_type="q6_k", tie=True)])
+def test_generate_mixed_formats(tmp_path_factory, kw):
+    from smith_amd.gguf_loader import loadGGUF
+    p = str(tmp_path_factory.mktemp("ggufk") / "m.gguf")
+    write_tiny_llama(p, **dict(SMALL, **kw))
+    m = loadGGUF(p)
+    ref = LO.LlamaOracle(p)
+    prompt = [3, 77, 150, 9, 210]
+    caches = m.createCache()
+    assert normwise_rel_err(m.forwardPrefill(prompt, caches)["logits"], ref.forward(prompt, 0)) <= 1e-2
+    out = m.generate(prompt, {"maxTokens": 8, "temperature": 0})
+    gen = out[len(prompt):]
+    ref.reset()
+    _, logits = ref.generate_greedy(prompt, 8, teacher=gen)
+    check_tokens(gen, logits)
+    caches = m.createCache()
+    m.forwardPrefill(prompt, caches)
+    ref.reset()
+    ref.forward(prompt, 0)
+    for i, tk in enumerate([5, 250, 17]):
+        g = m.forwardDecode(tk, len(prompt) + i, caches)["logits"]
+        w = ref.forward([tk], len(prompt) + i)
+        assert normwise_rel_err(g, w) <= 1e-3, i
