@@ -304,11 +304,23 @@ def calibrate(D, steps):
     return res
 
 
-def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3):
-    """Config 5: seeded synthetic Llama GGUF (Q4_0 linears), loadGGUF, then
-    generate(prompt of 128 seeded ids, maxTokens 128, temperature 0).
-    Decode tok/s = decode steps / decode time (HIP events around the greedy
-    graph replays); prefill reported separately."""
+def e2e_weight_bytes(mix):
+    """HBM bytes of weights one decode token streams at config 5."""
+    c = __import__("smith_amd.synthetic_gguf", fromlist=["CONFIG5"]).CONFIG5
+    d, f, v, L = c["dim"], c["ffn"], c["vocab"], c["layers"]
+    kv = c["kv_heads"] * d // c["heads"]
+    if mix == "q4_0":
+        return 1981808640 + 55296000  # Q4_0 linears + Q4_0 LM head
+    q4k = L * (2 * d * d + d * kv + 2 * d * f)  # q, o, k, gate, up
+    q6k = L * (d * kv + f * d)                  # v, down
+    return q4k * 144 // 256 + q6k * 210 // 256 + d * v * 4  # + the f32 LM head
+
+
+def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3, mix="q4_0"):
+    """Config 5: seeded synthetic Llama GGUF (Q4_0 linears, or the Q4_K_M
+    mix), loadGGUF, then generate(prompt of 128 seeded ids, maxTokens 128,
+    temperature 0).  Decode tok/s = decode steps / decode time (HIP events
+    around the greedy graph replays); prefill reported separately."""
     from smith_amd import prng
     from smith_amd.gguf_loader import loadGGUF
     from smith_amd.synthetic_gguf import CONFIG5, build_llama_gguf
@@ -316,7 +328,7 @@ def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3):
     if not os.path.exists(path):
         c = CONFIG5
         build_llama_gguf(path, dim=c["dim"], layers=c["layers"], heads=c["heads"], kv_heads=c["kv_heads"],
-                         ffn=c["ffn"], vocab=c["vocab"], context=c["context"], seed=1)
+                         ffn=c["ffn"], vocab=c["vocab"], context=c["context"], seed=1, mix=mix)
     t_write = time.perf_counter() - t0
     t0 = time.perf_counter()
     m = loadGGUF(path)
@@ -337,8 +349,8 @@ def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3):
              "generate_ms": round(t_all, 3)}
         if best is None or r["decode_tok_s"] > best["decode_tok_s"]:
             best = r
-    gb_per_token = 1981808640 + 55296000  # Q4_0 linears + Q4_0 LM head of config 5
-    best.update({"weights_GB_per_token": round(gb_per_token / 1e9, 3),
+    gb_per_token = e2e_weight_bytes(mix)
+    best.update({"mix": mix, "weights_GB_per_token": round(gb_per_token / 1e9, 3),
                  "weight_stream_GBps": round(gb_per_token / (best["decode_ms_per_token"] * 1e-3) / 1e9, 1),
                  "tokens_generated": len(out) - prompt_len, "gguf_write_s": round(t_write, 1),
                  "load_s": round(t_load, 1), "first_tokens": out[prompt_len:prompt_len + 8]})
@@ -356,6 +368,7 @@ def main():
     ap.add_argument("--e2e-only", action="store_true", help="only the config-5 end-to-end decode")
     ap.add_argument("--cfg4-only", action="store_true", help="only the config-4 prefill GEMMs")
     ap.add_argument("--gguf", default="/tmp/smith_config5.gguf", help="synthetic config-5 GGUF path (written if absent)")
+    ap.add_argument("--mix", default="q4_0", choices=["q4_0", "q4_k_m"], help="config-5 weight types for --e2e-only")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (--gpus %d requested); multi-GPU "
@@ -372,7 +385,8 @@ def main():
         print(json.dumps({"calibration": calibrate(D, args.steps)}), flush=True)
         return
     if args.e2e_only:
-        print(json.dumps({"cfg5_e2e": bench_e2e(D, args.gguf)}), flush=True)
+        path = args.gguf if args.mix == "q4_0" else args.gguf.replace(".gguf", "_%s.gguf" % args.mix)
+        print(json.dumps({"cfg5_e2e": bench_e2e(D, path, mix=args.mix)}), flush=True)
         return
     if args.cfg4_only:
         print(json.dumps({"cfg4_q4s_prefill": bench_cfg4(D, S, prng)}), flush=True)
@@ -423,6 +437,10 @@ def main():
         e2e["bound_tok_s_at_hbm_peak"] = round(HBM_PEAK_GBS * 1e9 / (1981808640 + 55296000), 1)
         configs["cfg5_e2e_llama_q4_0_decode"] = e2e
         log("cfg5:", json.dumps(e2e))
+        km = bench_e2e(D, args.gguf.replace(".gguf", "_q4_k_m.gguf"), mix="q4_k_m", reps=2)
+        km["bound_tok_s_at_hbm_peak"] = round(HBM_PEAK_GBS * 1e9 / e2e_weight_bytes("q4_k_m"), 1)
+        configs["cfg5_e2e_llama_q4_k_m_decode"] = km
+        log("cfg5 q4_k_m:", json.dumps(km))
 
     line = {
         "metric": "Q4 GEMV GB/s (% HBM peak) + Q4 decode tokens/sec, 1 MI355X",

@@ -237,6 +237,15 @@ int smith_linear_gguf_tiles_act(void* ctx, uint32_t ggml_type, const void* act_i
 int smith_linear_gguf_tiles_attn(void* ctx, uint32_t ggml_type, const float* parts, const int32_t* pos_ptr,
                                  uint32_t head_dim, const void* planes, float* out, uint32_t N, uint32_t K,
                                  const float* resid, uint32_t epilogue, void* act_out, const float* gamma_out);
+/* One launch for a q|k|v whose weights differ in block type: output columns
+ * [0, N1) from planes1 (type1, e.g. q|k in Q4_K), [N1, N1 + N2) from planes2
+ * (type2, e.g. v in Q6_K), both on the same act (optional RMSNorm scale);
+ * plain stores.  smith_gguf_tiles_pair_ok tells which pairs have a kernel
+ * (Q4_K+Q6_K, Q4_K+Q5_0, Q5_0+Q6_K, Q4_0+Q6_K, Q4_K+Q4_0). */
+int smith_gguf_tiles_pair_ok(uint32_t type1, uint32_t type2);
+int smith_linear_gguf_tiles_pair_act(void* ctx, uint32_t type1, const void* planes1, uint32_t N1, uint32_t type2,
+                                     const void* planes2, uint32_t N2, const void* act_in, int norm, float eps,
+                                     float* out, uint32_t K);
 /* dequantizeTensor (src/gguf.js:343-394) on the device: numel elements of a
  * flat GGUF tensor of type F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q8_0, Q4_K or
  * Q6_K to f32, bit-identical to the reference's Float32Array. */

@@ -1296,6 +1296,58 @@ int smith_linear_gguf_tiles_attn(void* ctx, uint32_t ggml_type, const float* par
                    epilogue, act_out, gamma_out);
 }
 
+namespace {
+const char* pair_tag(Fmt f1, Fmt f2) {
+  static const struct { Fmt a, b; const char* tag; } pairs[] = {
+      {FQ4KT, FQ6KT, "q4kt_q6kt"}, {FQ4KT, FQ50T, "q4kt_q50t"}, {FQ50T, FQ6KT, "q50t_q6kt"},
+      {FQ40T, FQ6KT, "q40t_q6kt"}, {FQ4KT, FQ40T, "q4kt_q40t"}};
+  for (const auto& p : pairs)
+    if (p.a == f1 && p.b == f2) return p.tag;
+  return nullptr;
+}
+}  // namespace
+
+int smith_gguf_tiles_pair_ok(uint32_t type1, uint32_t type2) {
+  const int f1 = gt_of_ggml((int)type1), f2 = gt_of_ggml((int)type2);
+  return f1 >= 0 && f2 >= 0 && pair_tag((Fmt)f1, (Fmt)f2) ? 1 : 0;
+}
+
+int smith_linear_gguf_tiles_pair_act(void* ctx, uint32_t type1, const void* planes1, uint32_t N1, uint32_t type2,
+                                     const void* planes2, uint32_t N2, const void* act_in, int norm, float eps,
+                                     float* out, uint32_t K) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  const char* fn = "smith_linear_gguf_tiles_pair_act";
+  Fmt f1, f2;
+  if (tiles_fmt(c, fn, type1, N1, K, &f1) || tiles_fmt(c, fn, type2, N2, K, &f2)) return -1;
+  const char* tag = pair_tag(f1, f2);
+  if (!tag) return fail(c, "%s: no kernel for the GGML type pair (%u, %u)", fn, type1, type2);
+  if (!act_in || !planes1 || !planes2 || !out) return fail(c, "%s: null buffer", fn);
+  if (set_device(c)) return -1;
+  static const uint32_t kbs[] = {32, 48, 64, 72, 96, 128, 144, 192, 288};
+  const uint32_t G = K / 32, N = N1 + N2;
+  uint32_t kb = 288;
+  for (uint32_t v : kbs)
+    if (v >= G) {
+      kb = v;
+      break;
+    }
+  const uint32_t ksplit = (G + kb - 1) / kb;
+  const uint32_t threads = kb == 32 || kb == 48 || kb == 64 ? 256 : (kb == 72 ? 384 : (kb == 144 ? 768 : 512));
+  const uint32_t gx = N / 16;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_agemv2_%s_k%u", tag, kb);
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pN1 = N1, pN = N, pK = K, pnorm = norm ? 1u : 0u;
+  void* args[] = {&act_in, &planes1, &planes2, &out, &pN1, &pN, &pK, &pnorm, &eps, &pws, &pcnt};
+  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
+}
+
 int smith_dequantize_gguf(void* ctx, uint32_t ggml_type, const void* src, float* dst, uint64_t numel) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;

@@ -1053,7 +1053,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
                                            uint32_t epi, uint8_t* __restrict__ act_out,
                                            const float* __restrict__ gamma_out, float* __restrict__ ws,
                                            uint32_t* __restrict__ counters, const int32_t* __restrict__ pos_ptr,
-                                           uint32_t hd) {
+                                           uint32_t hd, uint32_t bx) {
   constexpr int GPW = 4 * S;
   constexpr int BC = 16 * CT;
   constexpr int GMAX = 4 * S * WK;
@@ -1068,7 +1068,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t c = lane & 15, j = lane >> 4;
-  const uint32_t n0 = blockIdx.x * BC;
+  const uint32_t n0 = bx * BC;  // bx: this block's column block
   const uint32_t ksplit = gridDim.y;
   const uint32_t gb = blockIdx.y * GMAX;  // first group of this block
   const uint32_t gw = gb + wk * GPW;
@@ -1374,7 +1374,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     __builtin_amdgcn_s_waitcnt(0);
     uint32_t prev = 0;
     if (lane == 0)
-      prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = __hip_atomic_fetch_add(counters + bx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     prev = __shfl(prev, 0);
     if (prev != ksplit - 1) return;
     v = 0.f;
@@ -1382,7 +1382,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       for (uint32_t sp = 0; sp < ksplit; sp++)
         v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n0 + lane, 0u,
                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    if (lane == 0) __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_exchange(counters + bx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (norm)
       for (uint32_t t = lane; t < T; t += 64) ssum += c1p[2 * T + t];
   }
@@ -1419,7 +1419,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       uint32_t epi, uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out, float* __restrict__ ws, \
       uint32_t* __restrict__ counters) {                                                                     \
     agemv_body<F, CT, S, WK, 0>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters,     \
-                                nullptr, 0);                                                                 \
+                                nullptr, 0, blockIdx.x);                                                     \
   }
 
 // o-projection on attention split partials (SRC 1); parts in place of the act
@@ -1430,7 +1430,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       uint32_t K, const float* __restrict__ R, uint32_t epi, uint8_t* __restrict__ act_out,                   \
       const float* __restrict__ gamma_out, float* __restrict__ ws, uint32_t* __restrict__ counters) {        \
     agemv_body<F, CT, S, WK, 1>((const uint8_t*)parts, B, D, C, N, K, 0u, 0.f, R, epi, act_out, gamma_out, ws, \
-                             counters, pos_ptr, hd);                                                         \
+                             counters, pos_ptr, hd, blockIdx.x);                                             \
   }
 
 // named by the groups one block covers (4*S*WK) and the column tiles per wave;
@@ -1449,11 +1449,50 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k96, F, 1, 3, 8)      \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k128, F, 1, 4, 8)     \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k192, F, 1, 6, 8)
+// Two tile formats in one launch, for q|k|v projections whose weights differ
+// in block type (Q4_K_M keeps attn_v in Q6_K): output columns [0, N1) from
+// planes B1 (format F1), [N1, N) from planes B2 (format F2), the same act in;
+// plain stores (no epilogue, no act out).  Workgroups choose their half by
+// blockIdx.x (uniform); each half keeps its own LDS.
+#define DEF_AGEMV2(NAME, F1, F2, CT, S, WK)                                                                   \
+  extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                                \
+      const uint8_t* __restrict__ act, const uint8_t* __restrict__ B1, const uint8_t* __restrict__ B2,       \
+      float* __restrict__ C, uint32_t N1, uint32_t N, uint32_t K, uint32_t norm, float eps,                  \
+      float* __restrict__ ws, uint32_t* __restrict__ counters) {                                             \
+    const uint32_t nb1 = N1 / (16 * CT);                                                                     \
+    const uint16_t* D1 = F1 == FMT_Q40T ? (const uint16_t*)(B1 + gt_planes(GT_Q40, N1, K / 32).prm)          \
+                                        : (const uint16_t*)B1;                                               \
+    const uint16_t* D2 = F2 == FMT_Q40T ? (const uint16_t*)(B2 + gt_planes(GT_Q40, N - N1, K / 32).prm)      \
+                                        : (const uint16_t*)B2;                                               \
+    if (blockIdx.x < nb1)                                                                                    \
+      agemv_body<F1, CT, S, WK, 0>(act, B1, D1, C, N1, K, norm, eps, nullptr, 0u, nullptr, nullptr, ws,      \
+                                   counters, nullptr, 0, blockIdx.x);                                        \
+    else                                                                                                     \
+      agemv_body<F2, CT, S, WK, 0>(act, B2, D2, C + N1, N - N1, K, norm, eps, nullptr, 0u, nullptr, nullptr, \
+                                   ws + (size_t)gridDim.y * N1, counters + nb1, nullptr, 0, blockIdx.x - nb1); \
+  }
+#define DEF_AGEMV2_FMT(TAG, F1, F2)                       \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k32, F1, F2, 1, 2, 4)   \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k48, F1, F2, 1, 3, 4)   \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k64, F1, F2, 1, 4, 4)   \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k72, F1, F2, 1, 3, 6)   \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k96, F1, F2, 1, 3, 8)   \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k128, F1, F2, 1, 4, 8)  \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k144, F1, F2, 1, 3, 12) \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k192, F1, F2, 1, 6, 8)  \
+  DEF_AGEMV2(smith_agemv2_##TAG##_k288, F1, F2, 1, 9, 8)
+
 DEF_AGEMV_FMT(q40t, FMT_Q40T)
 DEF_AGEMV_FMT(q41t, GT_Q41)
 DEF_AGEMV_FMT(q50t, GT_Q50)
 DEF_AGEMV_FMT(q4kt, GT_Q4K)
 DEF_AGEMV_FMT(q6kt, GT_Q6K)
+// the q|k|v type pairs of the llama.cpp K-quant mixes
+DEF_AGEMV2_FMT(q4kt_q6kt, GT_Q4K, GT_Q6K)
+DEF_AGEMV2_FMT(q4kt_q50t, GT_Q4K, GT_Q50)
+DEF_AGEMV2_FMT(q50t_q6kt, GT_Q50, GT_Q6K)
+DEF_AGEMV2_FMT(q40t_q6kt, FMT_Q40T, GT_Q6K)
+DEF_AGEMV2_FMT(q4kt_q40t, GT_Q4K, FMT_Q40T)
 
 #ifndef SMITH_NO_INSTANCES
 DEF_QGEMV3_FMT(q4s, FMT_Q4S)

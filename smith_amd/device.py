@@ -93,6 +93,9 @@ SYMBOLS = {
                                            _U32, _P, _P]),
     "smith_linear_gguf_tiles_attn": (_INT, [_P, _U32, _P, _P, _U32, _P, _P, _U32, _U32, _P, _U32, _P, _P]),
     "smith_dequantize_gguf": (_INT, [_P, _U32, _P, _P, _U64]),
+    "smith_gguf_tiles_pair_ok": (_INT, [_U32, _U32]),
+    "smith_linear_gguf_tiles_pair_act": (_INT, [_P, _U32, _P, _U32, _U32, _P, _U32, _P, ctypes.c_int, ctypes.c_float,
+                                                _P, _U32]),
     "smith_linear_q8": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
     "smith_rmsnorm": (_INT, [_P, _P, _P, _P, _U32, _U32, ctypes.c_float]),
     "smith_embed": (_INT, [_P, _P, _P, _P, _U32, _U32, _P, _P]),

@@ -88,7 +88,7 @@ class DeviceArray:
         return device.download(self.ptr, self.nbytes, self.dtype).reshape(self.shape)
 
 
-GT_TYPES = {G.GGML_TYPE[t] for t in ("Q4_1", "Q5_0", "Q4_K", "Q6_K")}
+GT_TYPES = {G.GGML_TYPE[t] for t in ("Q4_0", "Q4_1", "Q5_0", "Q4_K", "Q6_K")}
 
 
 class QLinear:
@@ -150,6 +150,9 @@ class QGroup:
         self.N = sum(q.N for q, _ in parts)
         self.kind = "group"
         self._tmp = None
+        # one launch for two tile-plane runs with a two-format kernel
+        self.pair = (len(parts) == 2 and all(q.kind == "gt" for q, _ in parts)
+                     and bool(device.lib.smith_gguf_tiles_pair_ok(parts[0][0].ggml_type, parts[1][0].ggml_type)))
 
     @property
     def has_act(self):
@@ -174,30 +177,44 @@ class QGroup:
     def act(self, act_in, norm, eps, out_ptr, resid=None, epilogue=0, act_out=None, gamma_out=None):
         if resid is not None or epilogue or act_out is not None:
             raise NotImplementedError("epilogues on a mixed-type linear group")
+        if self.pair:
+            (q1, _), (q2, _) = self.parts
+            device.check(device.lib.smith_linear_gguf_tiles_pair_act(
+                device.ops_ctx(), q1.ggml_type, q1.a.ptr, q1.N, q2.ggml_type, q2.a.ptr, q2.N, act_in,
+                1 if norm else 0, eps, out_ptr, self.K), "linear pair (act)")
+            return
         for q, off in self.parts:
             q.act(act_in, norm, eps, out_ptr + off * 4)
 
 
-def _pack_group(parsed, infos, K, cols, interleave):
+def _pack_group(parsed, infos, K, cols, interleave, gt_q4_0=False):
     """Repack one or more [out, in] quantized weights into one device buffer:
     side by side (interleave=False) or column-interleaved.  Weights of
-    different block types side by side become a QGroup."""
+    different block types side by side become a QGroup of same-type runs,
+    every run in tile planes (Q4_0 included: gt_q4_0) so that a two-run
+    group takes the two-format kernel."""
     types = [i["type"] for i in infos]
     if len(set(types)) != 1:
         if interleave:
             raise NotImplementedError("interleaved weights of different GGML types (%s)"
                                       % ", ".join(G.GGML_TYPE_NAME.get(t, str(t)) for t in types))
-        parts, off = [], 0
-        for info, n in zip(infos, cols):
-            parts.append((_pack_group(parsed, [info], K, [n], False), off))
-            off += n
+        # runs of equal type stay fused (q|k of Q4_K, v of Q6_K)
+        parts, off, i = [], 0, 0
+        while i < len(infos):
+            j = i
+            while j < len(infos) and types[j] == types[i]:
+                j += 1
+            run_cols = cols[i:j]
+            parts.append((_pack_group(parsed, infos[i:j], K, run_cols, False, gt_q4_0=True), off))
+            off += sum(run_cols)
+            i = j
         return QGroup(parts)
     t = types[0]
     Ntot = sum(cols)
     Gk = K // 32
     ctx = device.ops_ctx()
     dsc = None
-    if t == G.GGML_TYPE["Q4_0"]:
+    if t == G.GGML_TYPE["Q4_0"] and not gt_q4_0:
         nib = DeviceArray((Gk * Ntot * 16,), np.uint8)
         dsc = DeviceArray((Gk * Ntot,), np.uint16)
         kind = "q4_0t"

@@ -3,6 +3,11 @@
 Weights are generated and quantized on the GPU (smith_randn +
 smith_quantize_q4_0: ggml q4_0 rounding in the reference decoder's
 interleaved nibble order) and streamed to the file one tensor at a time.
+mix="q4_k_m" writes the llama.cpp Q4_K_M type mix instead (Q4_K q/k/o/gate/
+up and token_embd, Q6_K v/down and output.weight) with seeded random block
+fields -- nibbles, 6-bit scales/mins, int8 scales uniform, f16 scales chosen
+for weights of about N(0, 0.02) size: a random init in quantized form, for
+throughput measurement.
 Layout choices (so the reference's own loader would read the same model):
   * linear weights are listed [out, in] with blocks along `in`
     (gguf_loader.js:243-253 transposes such a listing into Smith's [in, out]);
@@ -49,9 +54,34 @@ def _q4_0_producer(rows, cols, seed, std):
     return run
 
 
+def _f16_bytes(v, n):
+    return np.full(n, v, np.float16).view(np.uint8).reshape(n, 2)
+
+
+def _kquant_producer(ggml, rows, cols, seed):
+    """Random Q4_K / Q6_K blocks of a [rows, cols] tensor (cols % 256 == 0)."""
+    def run():
+        nb = rows * cols // 256
+        rng = np.random.default_rng(seed)
+        if ggml == G.GGML_TYPE["Q4_K"]:
+            b = rng.integers(0, 256, (nb, 144), dtype=np.uint8)
+            b[:, 0:2] = _f16_bytes(1.0e-4, nb)   # d: 63 * 15 * 1e-4 ~ 0.09 full scale
+            b[:, 2:4] = _f16_bytes(5.0e-5, nb)   # dmin
+        else:
+            b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+            b[:, 208:210] = _f16_bytes(2.0e-5, nb)  # d: 127 * 32 * 2e-5 ~ 0.08 full scale
+        return b.ravel()
+    return run
+
+
 def build_llama_gguf(path, dim, layers, heads, kv_heads, ffn, vocab, context=8192, eps=1e-5, rope_base=10000.0,
-                     seed=1, std=0.02, tie_embeddings=False):
-    """Write a seeded random-init Llama GGUF (Q4_0 linears) to `path`."""
+                     seed=1, std=0.02, tie_embeddings=False, mix="q4_0"):
+    """Write a seeded random-init Llama GGUF (Q4_0 linears, or the Q4_K_M
+    mix) to `path`."""
+    if mix not in ("q4_0", "q4_k_m"):
+        raise ValueError("mix must be q4_0 or q4_k_m")
+    if mix == "q4_k_m" and (dim % 256 or ffn % 256 or vocab % 256):
+        raise ValueError("the Q4_K_M mix needs dim, ffn and vocab multiples of 256")
     if dim % 32 or ffn % 32 or vocab % 32:
         raise ValueError("dim, ffn and vocab must be multiples of 32 for Q4_0")
     hd = dim // heads
@@ -72,6 +102,8 @@ def build_llama_gguf(path, dim, layers, heads, kv_heads, ffn, vocab, context=819
         "llama.vocab_size": (T["UINT32"], vocab),
     }
     F32, Q40 = G.GGML_TYPE["F32"], G.GGML_TYPE["Q4_0"]
+    Q4K, Q6K = G.GGML_TYPE["Q4_K"], G.GGML_TYPE["Q6_K"]
+    kbytes = {Q4K: 144, Q6K: 210}
     tensors = []
     s = seed * 1000003
 
@@ -80,18 +112,31 @@ def build_llama_gguf(path, dim, layers, heads, kv_heads, ffn, vocab, context=819
         s += 1
         return s
 
-    tensors.append(("token_embd.weight", [vocab, dim], F32, vocab * dim * 4, _f32_producer(vocab * dim, nxt(), std, 0.0)))
+    if mix == "q4_k_m":
+        tensors.append(("token_embd.weight", [vocab, dim], Q4K, vocab * dim // 256 * 144,
+                        _kquant_producer(Q4K, vocab, dim, nxt())))
+    else:
+        tensors.append(("token_embd.weight", [vocab, dim], F32, vocab * dim * 4,
+                        _f32_producer(vocab * dim, nxt(), std, 0.0)))
     for L in range(layers):
         p = "blk.%d." % L
         tensors.append((p + "attn_norm.weight", [dim], F32, dim * 4, _f32_producer(dim, nxt(), 0.02, 1.0)))
         for name, out_, in_ in (("attn_q", dim, dim), ("attn_k", kvd, dim), ("attn_v", kvd, dim),
                                 ("attn_output", dim, dim), ("ffn_gate", ffn, dim), ("ffn_up", ffn, dim),
                                 ("ffn_down", dim, ffn)):
-            tensors.append((p + name + ".weight", [out_, in_], Q40, out_ * in_ // 32 * 18,
-                            _q4_0_producer(out_, in_, nxt(), std)))
+            if mix == "q4_k_m":
+                t = Q6K if name in ("attn_v", "ffn_down") else Q4K
+                tensors.append((p + name + ".weight", [out_, in_], t, out_ * in_ // 256 * kbytes[t],
+                                _kquant_producer(t, out_, in_, nxt())))
+            else:
+                tensors.append((p + name + ".weight", [out_, in_], Q40, out_ * in_ // 32 * 18,
+                                _q4_0_producer(out_, in_, nxt(), std)))
         tensors.append((p + "ffn_norm.weight", [dim], F32, dim * 4, _f32_producer(dim, nxt(), 0.02, 1.0)))
     tensors.append(("output_norm.weight", [dim], F32, dim * 4, _f32_producer(dim, nxt(), 0.02, 1.0)))
-    if not tie_embeddings:
+    if not tie_embeddings and mix == "q4_k_m":
+        tensors.append(("output.weight", [dim, vocab], Q6K, dim * vocab // 256 * 210,
+                        _kquant_producer(Q6K, dim, vocab, nxt())))
+    elif not tie_embeddings:
         tensors.append(("output.weight", [dim, vocab], Q40, dim * vocab // 32 * 18,
                         _q4_0_producer(dim, vocab, nxt(), std)))
     return G.write_gguf(path, meta, tensors)

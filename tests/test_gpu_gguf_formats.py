@@ -283,7 +283,8 @@ def check_tokens(gpu_tokens, ref_logits):
 
 @pytest.mark.parametrize("kw", [Q4_K_M, dict(linear_type="q4_1"), dict(linear_type="q5_0", head_type="q8_0"),
                                 dict(linear_type="q5_0", dim=288, heads=6, kv_heads=3, ffn=768),  # head_dim 48
-                                dict(linear_type="q6_k", tie=True)])
+                                dict(linear_type="q6_k", tie=True),
+                                dict(types={"attn_v": "q6_k", "ffn_down": "q6_k"})])  # Q4_0 + Q6_K pair
 def test_generate_mixed_formats(tmp_path_factory, kw):
     from smith_amd.gguf_loader import loadGGUF
     p = str(tmp_path_factory.mktemp("ggufk") / "m.gguf")
@@ -306,3 +307,25 @@ def test_generate_mixed_formats(tmp_path_factory, kw):
         g = m.forwardDecode(tk, len(prompt) + i, caches)["logits"]
         w = ref.forward([tk], len(prompt) + i)
         assert normwise_rel_err(g, w) <= 1e-3, i
+
+
+@pytest.mark.parametrize("t1,t2", [(O.GGML_Q4_K, O.GGML_Q6_K), (O.GGML_Q4_K, O.GGML_Q5_0), (O.GGML_Q5_0, O.GGML_Q6_K),
+                                   (O.GGML_Q4_0, O.GGML_Q6_K), (O.GGML_Q4_K, O.GGML_Q4_0)])
+@pytest.mark.parametrize("K", [256, 3072, 9216])
+def test_pair_act_gemv(t1, t2, K):
+    """Two block types in one launch (q|k of one type, v of another)."""
+    N1, N2 = 80, 48
+    b1, w1 = _weights(t1, N1, K, 51)
+    b2, w2 = _weights(t2, N2, K, 52)
+    p1, _ = _planes(t1, b1, N1, K)
+    p2, _ = _planes(t2, b2, N2, K)
+    assert device.lib.smith_gguf_tiles_pair_ok(t1, t2) == 1
+    x = prng.randn((K,), 53).astype(np.float64)
+    g = 1 + prng.randn((K,), 54, std=0.1).astype(np.float64)
+    act = _act_of(x, g)
+    out = device.alloc((N1 + N2) * 4)
+    device.check(device.lib.smith_linear_gguf_tiles_pair_act(device.ops_ctx(), t1, p1, N1, t2, p2, N2, act, 1, EPS,
+                                                             out, K))
+    want = np.concatenate([w1, w2]).astype(np.float64) @ _rms(x, g)
+    assert normwise_rel_err(_get(out, N1 + N2), want) <= TOL
+    assert device.lib.smith_gguf_tiles_pair_ok(O.GGML_Q6_K, O.GGML_Q4_1) == 0
