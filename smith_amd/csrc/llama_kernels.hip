@@ -336,6 +336,177 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_cached(ATT_ARG
 }
 
 // ---------------------------------------------------------------------------
+// Prefill attention on the f32 matrix cores (flash-attention form of
+// flash_attention.js:34-70 / flash_attention.metal, which gguf_cache.js:213
+// runs on the prefill rows): S query rows at positions p0 .. p0+S-1, every
+// key row 0 .. p0+s already in the caches (smith_kv_append ran first).
+// Workgroup (h, qb): head h, query rows 64*qb .. +63, one wave per 16 rows.
+// The roped queries sit in LDS; K and V tiles of 64 keys are staged in LDS;
+// per wave S = Q K^T with v_mfma_f32_16x16x4_f32 (f32 operands, exact
+// products, f32 sums -- the reference's arithmetic type), scale, causal mask,
+// online softmax per row (running max m, sum l), P through LDS into the
+// A-operand layout, O += P V on the same MFMA.  hd % 16 == 0, hd <= 128.
+// MFMA 16x16x4 f32 layout: lane (c = lane % 16, j = lane / 16) supplies
+// A[row c][k j] and B[k j][col c] and holds D rows 4j .. 4j+3 of column c.
+// ---------------------------------------------------------------------------
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+#define FA_BQ 64
+#define FA_BK 64
+#define FA_QS 132  // Q / K row stride (floats): A/B reads of 16 rows x 4 k hit 64 banks
+#define FA_VS 144  // V row stride: B reads of 4 keys x 16 columns hit 64 banks
+#define FA_PS 68   // P row stride
+
+template <int NT>  // head_dim / 16
+__device__ __forceinline__ void attention_prefill_body(
+    const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
+    uint32_t nKV, const float* __restrict__ cosT, const float* __restrict__ sinT, const float* __restrict__ kcache,
+    const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out) {
+  constexpr uint32_t hd = 16 * NT;
+  __shared__ __attribute__((aligned(16))) float Qs[FA_BQ * FA_QS];
+  __shared__ __attribute__((aligned(16))) float Ks[FA_BK * FA_QS];
+  __shared__ __attribute__((aligned(16))) float Vs[FA_BK * FA_VS];
+  __shared__ float Ps[4][16 * FA_PS];
+  const uint32_t h = blockIdx.x, s0 = blockIdx.y * FA_BQ;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t c = lane & 15, j = lane >> 4;
+  const uint32_t p0 = (uint32_t)pos_ptr[0];
+  const uint32_t rep = nH / nKV, kvh = h / rep;
+  const uint32_t Wq = nH * hd;
+  const float scale = 1.0f / __builtin_sqrtf((float)hd);
+  const uint32_t nrow = S - s0 < FA_BQ ? S - s0 : FA_BQ;
+  // 1. roped queries (whole-row RoPE of the q part of each qkv row); rows past S zero
+  for (uint32_t i = tid; i < FA_BQ * hd; i += 256) {
+    const uint32_t r = i / hd, e = i % hd;
+    float v = 0.f;
+    if (r < nrow) v = rope_elem(qkv + (size_t)(s0 + r) * ld, Wq, h * hd + e, p0 + s0 + r, cosT, sinT);
+    Qs[r * FA_QS + e] = v;
+  }
+  // this wave's rows and their key range
+  const uint32_t wr0 = s0 + 16 * w;                    // first row of the wave
+  const uint32_t wlast = p0 + (wr0 + 15 < S ? wr0 + 15 : (S > 0 ? S - 1 : 0));  // last key any of them sees
+  const uint32_t Tend = p0 + (s0 + nrow - 1) + 1;      // keys of the block: 0 .. Tend-1
+  f32x4_t o[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) o[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    m[r] = -__builtin_inff();
+    l[r] = 0.f;
+  }
+  const float* kb = kcache + (size_t)kvh * maxSeq * hd;
+  const float* vb = vcache + (size_t)kvh * maxSeq * hd;
+  const uint32_t c4n = hd / 4;
+  for (uint32_t t0 = 0; t0 < Tend; t0 += FA_BK) {
+    __syncthreads();  // previous tile's K/V/P reads done (and, first time, Qs written)
+    // 2. K and V tile (rows past Tend zero: their P is 0 and V must be finite)
+    for (uint32_t i = tid; i < FA_BK * c4n; i += 256) {
+      const uint32_t r = i / c4n, c4 = i % c4n, t = t0 + r;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      if (t < Tend) {
+        kv = *(const float4*)(kb + (size_t)t * hd + 4 * c4);
+        vv = *(const float4*)(vb + (size_t)t * hd + 4 * c4);
+      }
+      *(float4*)&Ks[r * FA_QS + 4 * c4] = kv;
+      *(float4*)&Vs[r * FA_VS + 4 * c4] = vv;
+    }
+    __syncthreads();
+    if (t0 > wlast || wr0 >= S) continue;  // every key of this tile is after every row of the wave
+    // 3. scores of the wave's 16 rows against the tile's 64 keys
+    f32x4_t sc[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) sc[kt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (uint32_t kk = 0; kk < hd; kk += 4) {
+      const float a = Qs[(16 * w + c) * FA_QS + kk + j];
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++)
+        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Ks[(kt * 16 + c) * FA_QS + kk + j], sc[kt], 0, 0, 0);
+    }
+    // 4. online softmax per row (row 4j + r of the wave: lanes of group j)
+    float mx[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t pos = p0 + wr0 + 4 * j + r;
+      float v = -__builtin_inff();
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++) {
+        const uint32_t t = t0 + 16 * kt + c;
+        const float sv = t <= pos ? sc[kt][r] * scale : -__builtin_inff();
+        sc[kt][r] = sv;
+        v = sv > v ? sv : v;
+      }
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) {
+        const float u = __shfl_xor(v, d);
+        v = u > v ? u : v;
+      }
+      mx[r] = v;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float mn = mx[r] > m[r] ? mx[r] : m[r];  // finite: key 0 is in the first tile of every row
+      const float alpha = m[r] == -__builtin_inff() ? 0.f : __expf(m[r] - mn);
+      float rs = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++) {
+        const float pv = sc[kt][r] == -__builtin_inff() ? 0.f : __expf(sc[kt][r] - mn);
+        sc[kt][r] = pv;
+        rs += pv;
+      }
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) rs += __shfl_xor(rs, d);
+      l[r] = __builtin_fmaf(l[r], alpha, rs);
+      m[r] = mn;
+#pragma unroll
+      for (int t = 0; t < NT; t++) o[t][r] *= alpha;
+    }
+    // 5. P to LDS (row-major 16 x 64), read back as the A operand of P V
+    float* P = Ps[w];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) P[(4 * j + r) * FA_PS + 16 * kt + c] = sc[kt][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll 4
+    for (uint32_t kk = 0; kk < FA_BK; kk += 4) {
+      const float a = P[c * FA_PS + kk + j];
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Vs[(kk + j) * FA_VS + 16 * t + c], o[t], 0, 0, 0);
+    }
+  }
+  // 6. out = O / l
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t s = wr0 + 4 * j + r;
+    if (s >= S) continue;
+    const float inv = 1.0f / l[r];
+#pragma unroll
+    for (int t = 0; t < NT; t++) out[(size_t)s * Wq + h * hd + 16 * t + c] = o[t][r] * inv;
+  }
+}
+
+#define DEF_ATT_PREFILL(NT)                                                                                      \
+  extern "C" __global__ __launch_bounds__(256) void smith_attention_prefill_hd##NT(                              \
+      const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,   \
+      uint32_t nKV, const float* __restrict__ cosT, const float* __restrict__ sinT,                              \
+      const float* __restrict__ kcache, const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out) { \
+    attention_prefill_body<NT>(qkv, ld, pos_ptr, S, nH, nKV, cosT, sinT, kcache, vcache, maxSeq, out);           \
+  }
+// named by head_dim / 16
+DEF_ATT_PREFILL(1)
+DEF_ATT_PREFILL(2)
+DEF_ATT_PREFILL(3)
+DEF_ATT_PREFILL(4)
+DEF_ATT_PREFILL(5)
+DEF_ATT_PREFILL(6)
+DEF_ATT_PREFILL(7)
+DEF_ATT_PREFILL(8)
+
+// ---------------------------------------------------------------------------
 // Single-row decode attention writing per-split partials for the output
 // projection to combine (smith_agemv_att_*), so no workgroup of this kernel
 // waits for another.  Row position p0 = *pos_ptr, T = p0 + 1 keys, split

@@ -1164,6 +1164,19 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   if (head_dim > 128 || head_dim % 4) return fail(c, "smith_attention: head_dim %u unsupported (<= 128, % 4)", head_dim);
   if (set_device(c)) return -1;
   if (!S) return 0;
+  if (S > 1 && head_dim % 16 == 0) {
+    // prompt rows: rope + append every row's key/value, then flash attention
+    // on the f32 matrix cores over the caches (64 query rows per workgroup)
+    uint32_t Wq = n_heads * head_dim;
+    void* aargs[] = {&qkv, &ld, &pos_ptr, &Wq, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &kcache, &vcache,
+                     &max_seq};
+    if (launch(c, "smith_kv_append", dim3(S), dim3(256), aargs)) return -1;
+    void* fargs[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &rope_cos, &rope_sin,
+                     &kcache, &vcache, &max_seq, &out};
+    char name[48];
+    snprintf(name, sizeof name, "smith_attention_prefill_hd%u", head_dim / 16);
+    return launch(c, name, dim3(n_heads, (S + 63) / 64), dim3(256), fargs);
+  }
   const uint32_t nsplit = 8;  // ATT_SPLIT in llama_kernels.hip
   size_t slots = (size_t)S * n_heads;
   if (ensure(c, &c->att_ws, &c->att_ws_bytes, slots * nsplit * 130 * sizeof(float))) return -1;

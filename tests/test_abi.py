@@ -68,6 +68,7 @@ def test_code_object_has_kernels():
               "smith_lmhead_q4_0_nb", "smith_repack_lmhead_q4_0",
               "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"] + [
               "smith_repack_gt_%s" % f for f in ("q40", "q41", "q50", "q4k", "q6k")] + [
+              "smith_attention_prefill_hd%d" % n for n in range(1, 9)] + [
               "smith_dequantize_%s" % t for t in ("f16", "bf16", "q4_0", "q4_1", "q5_0", "q8_0", "q4_k", "q6_k")]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
 
