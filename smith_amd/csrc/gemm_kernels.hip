@@ -323,6 +323,270 @@ DEF_GEMM_FMT(q6kt, GT_Q6K)
 
 // C = epilogue(sum over the ks K-split partials ws[0..ks) [M][N]), fixed
 // order; one thread per output (pair for SwiGLU).
+// ---------------------------------------------------------------------------
+// gemm2: the same GEMM with the operands staged by direct-to-LDS loads
+// (global_load_lds, no registers on the way) into a ring of 3 stages, and
+// the weights kept in LDS as their raw records -- dequantized in registers
+// right before the MFMAs.  Per stage of 64 K: A rows (f16, 16-byte chunks
+// XOR-swizzled by row through the choice of each lane's source), weight
+// records of the tile's BN columns for 2 groups (Q4S 24 B, Q4_0 tiles 16 B
+// nibbles + 2 B d).  The A operand's 8-element chunks are in the slot order
+// {0,4,1,5,2,6,3,7} (smith_gemm_prep_a_perm), the order in which a nibble
+// dword converts to f16 with 4 bit-inserts (exponent bias 1024 + q for low
+// nibbles, 64 + q for high): both operands permuted alike leave the dot
+// product unchanged.  Q4_0: w = (h - bias - 8) * d in packed f16 (q - 8
+// exact, one rounding); Q4S: w = fma(h, s, c) in f32 with c = -s*(z + bias),
+// one f16 rounding.  The loop is unrolled by the ring size so every LDS
+// access names its stage buffer at compile time (precise vmcnt waits).
+// ---------------------------------------------------------------------------
+template <int BYTES_PER_WAVE>
+struct DmaUnit {  // dwordx4 or dword loads splitting a wave's bytes evenly (LDS slot = lane * size)
+  static constexpr int U = BYTES_PER_WAVE % 1024 == 0 ? 16 : 4;
+  static constexpr int N = BYTES_PER_WAVE / (64 * U);
+  static_assert(BYTES_PER_WAVE % (64 * U) == 0 && N >= 1, "stage bytes must split over the waves");
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int U>
+__device__ __forceinline__ void dma(const void* g, lds_ptr_t l) {
+  if constexpr (U == 16) __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+  else __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
+}
+
+template <int FMT, int BM, int BN, int WM, int WN>
+struct G2 {
+  static constexpr int NW = (BM / WM) * (BN / WN);
+  static constexpr int A_BYTES = BM * 128;
+  static constexpr int REC = FMT == WF_Q4S ? 24 : 16;
+  static constexpr int B_BYTES = BN * 2 * REC;
+  static constexpr int D_BYTES = FMT == WF_Q40T ? BN * 4 : 0;
+  using UA = DmaUnit<A_BYTES / NW>;
+  using UB = DmaUnit<B_BYTES / NW>;
+  static constexpr int DW = D_BYTES / 256;  // waves that load the d plane, one dword instruction each
+  static_assert(D_BYTES % 256 == 0 && DW <= NW, "d plane split");
+  static constexpr int CNT = UA::N + UB::N;  // DMA instructions per wave per stage (+1 for the d waves)
+};
+
+__device__ __forceinline__ constexpr uint32_t vmcnt_imm(uint32_t n) {
+  return (n & 0xF) | (0x7u << 4) | (0xFu << 8) | (((n >> 4) & 3u) << 14);
+}
+
+template <int FMT, int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, const uint8_t* __restrict__ B,
+                                          const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t M,
+                                          uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,
+                                          float* __restrict__ ws, uint32_t sps) {
+  using P = G2<FMT, BM, BN, WM, WN>;
+  constexpr int NW = P::NW, WAVES_N = BN / WN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t As0[P::A_BYTES], As1[P::A_BYTES], As2[P::A_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t Bs0[P::B_BYTES + P::D_BYTES], Bs1[P::B_BYTES + P::D_BYTES],
+      Bs2[P::B_BYTES + P::D_BYTES];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const uint32_t G = K / 32;
+  const uint32_t MB = (M + BM - 1) / BM, NBk = (N + BN - 1) / BN, T = MB * NBk;
+  uint32_t t = blockIdx.x;
+  if (T % 8 == 0) t = (blockIdx.x % 8) * (T / 8) + blockIdx.x / 8;
+  const uint32_t nb = t / MB, mb = t % MB;
+  const uint32_t m0 = mb * BM, n0 = nb * BN;
+  const uint32_t Sall = K / 64;
+  const uint32_t s0 = blockIdx.y * sps < Sall ? blockIdx.y * sps : Sall;
+  const uint32_t s1 = s0 + sps < Sall ? s0 + sps : Sall;
+  const uint32_t S = s1 - s0;
+
+  // DMA of stage s (absolute) into buffers (as, bs)
+  auto issue = [&](uint32_t s, uint8_t* as, uint8_t* bs) {
+    const uint32_t k0 = s * 64;
+#pragma unroll
+    for (int q = 0; q < P::UA::N; q++) {
+      // this wave's bytes [off, off + 64 U) of the stage's A rows
+      const uint32_t off = (wave * P::UA::N + q) * 64 * P::UA::U + lane * P::UA::U;
+      const uint32_t row = off / 128, cs = (off % 128) / 16, ci = (off % 16) / 2;  // slot chunk, half within
+      const uint32_t c = cs ^ (row & 7);
+      const uint32_t m = m0 + row < M ? m0 + row : M - 1;
+      dma<P::UA::U>(A16 + (size_t)m * K + k0 + 8 * c + ci, (lds_ptr_t)(as + (wave * P::UA::N + q) * 64 * P::UA::U));
+    }
+#pragma unroll
+    for (int q = 0; q < P::UB::N; q++) {
+      const uint32_t off = (wave * P::UB::N + q) * 64 * P::UB::U + lane * P::UB::U;
+      const uint8_t* src;
+      if (FMT == WF_Q4S) {
+        const uint32_t g2 = off / (BN * 24), w = off % (BN * 24);
+        size_t a = ((size_t)(2 * s + g2) * N + n0) * 24 + w;
+        const size_t lim = (size_t)G * N * 24 - P::UB::U;
+        src = B + (a < lim ? a : lim);
+      } else {
+        const uint32_t tt = off / 512, w = off % 512;  // 16-column tile, byte within its 2 groups
+        uint32_t tg = n0 / 16 + tt;
+        tg = tg < N / 16 ? tg : N / 16 - 1;
+        src = B + (((size_t)tg * G + 2 * s) * 16) * 16 + w;
+      }
+      dma<P::UB::U>(src, (lds_ptr_t)(bs + (wave * P::UB::N + q) * 64 * P::UB::U));
+    }
+    if (FMT == WF_Q40T && wave < (uint32_t)P::DW) {
+      const uint32_t off = wave * 256 + lane * 4;
+      const uint32_t tt = off / 64, w = off % 64;
+      uint32_t tg = n0 / 16 + tt;
+      tg = tg < N / 16 ? tg : N / 16 - 1;
+      dma<4>((const uint8_t*)D + ((size_t)tg * G + 2 * s) * 32 + w, (lds_ptr_t)(bs + P::B_BYTES + wave * 256));
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const uint32_t r16 = lane & 15, kq = lane >> 4;
+
+  auto compute = [&](const uint8_t* as, const uint8_t* bs) {
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      half8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const uint32_t row = wm * WM + i * 16 + r16;
+        af[i] = *(const half8*)(as + row * 128 + 16 * ((kk * 4 + kq) ^ (row & 7)));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const uint32_t col = wn * WN + j * 16 + r16;
+        u32x4 u;
+        if (FMT == WF_Q4S) {
+          const uint8_t* rec = bs + (kk * BN + col) * 24;
+          const uint32_t x = *(const uint32_t*)(rec + 4 * kq);
+          const float2 sz = *(const float2*)(rec + 16);
+          const uint32_t y = x >> 8;
+          const uint32_t h[4] = {(x & 0x000F000Fu) | 0x64006400u, (x & 0x00F000F0u) | 0x54005400u,
+                                 (y & 0x000F000Fu) | 0x64006400u, (y & 0x00F000F0u) | 0x54005400u};
+          const float clo = -sz.x * (sz.y + 1024.0f), chi = -sz.x * (sz.y + 64.0f);
+#pragma unroll
+          for (int d = 0; d < 4; d++) {
+            const _Float16 __attribute__((ext_vector_type(2))) hv =
+                __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), h[d]);
+            const float c = (d & 1) ? chi : clo;
+            u[d] = pack_h2(__builtin_fmaf((float)hv.x, sz.x, c), __builtin_fmaf((float)hv.y, sz.x, c));
+          }
+        } else {
+          const uint32_t tt = col / 16, cc = col % 16;
+          const uint32_t x = *(const uint32_t*)(bs + tt * 512 + kk * 256 + cc * 16 + 4 * kq);
+          const _Float16 dh = *(const _Float16*)(bs + P::B_BYTES + tt * 64 + kk * 32 + cc * 2);
+          const uint32_t y = x >> 8;
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          const h2 blo = (h2){(_Float16)1032.0f, (_Float16)1032.0f}, bhi = (h2){(_Float16)72.0f, (_Float16)72.0f};
+          const h2 dd = (h2){dh, dh};
+          const h2 v0 = (__builtin_bit_cast(h2, (x & 0x000F000Fu) | 0x64006400u) - blo) * dd;
+          const h2 v1 = (__builtin_bit_cast(h2, (x & 0x00F000F0u) | 0x54005400u) - bhi) * dd;
+          const h2 v2 = (__builtin_bit_cast(h2, (y & 0x000F000Fu) | 0x64006400u) - blo) * dd;
+          const h2 v3 = (__builtin_bit_cast(h2, (y & 0x00F000F0u) | 0x54005400u) - bhi) * dd;
+          u = (u32x4){__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                      __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)};
+        }
+        bf[j] = __builtin_bit_cast(half8, u);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // ring: stage s in buffer s % 3; stages s+1 and s+2 in flight while s is used
+  if (S > 0) issue(s0, As0, Bs0);
+  if (S > 1) issue(s0 + 1, As1, Bs1);
+  auto step = [&](uint32_t s, uint8_t* as, uint8_t* bs, uint8_t* an, uint8_t* bn) {
+    // this wave's DMA of stage s done (the later stages may stay in flight), then all waves'
+    if (s + 1 >= S) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    else if (FMT == WF_Q40T && wave < (uint32_t)P::DW) __builtin_amdgcn_s_waitcnt(vmcnt_imm(P::CNT + 1));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(P::CNT));
+    __builtin_amdgcn_s_barrier();
+    if (s + 2 < S) issue(s0 + s + 2, an, bn);  // into the buffer stage s-1 used (all waves are past it)
+    compute(as, bs);
+  };
+  for (uint32_t s = 0; s < S; s += 3) {
+    step(s, As0, Bs0, As2, Bs2);
+    if (s + 1 < S) step(s + 1, As1, Bs1, As0, Bs0);
+    if (s + 2 < S) step(s + 2, As2, Bs2, As1, Bs1);
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint32_t n = n0 + wn * WN + j * 16 + r16;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t m = m0 + wm * WM + i * 16 + 4 * kq + e;
+        float v = acc[i][j][e];
+        if (gridDim.y > 1) {
+          if (m < M && n < N) ws[((size_t)blockIdx.y * M + m) * N + n] = v;
+        } else if (epi == 2) {
+          const float u = __shfl_down(v, 1);
+          if (m < M && n + 1 < N && (r16 & 1) == 0) C[(size_t)m * (N / 2) + n / 2] = silu_mul_g(v, u);
+        } else if (m < M && n < N) {
+          if (epi == 1) v += R[(size_t)m * N + n];
+          C[(size_t)m * N + n] = v;
+        }
+      }
+    }
+}
+
+#define DEF_GEMM2(NAME, FMT, BM, BN, WM, WN)                                                                  \
+  extern "C" __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void NAME(                            \
+      const _Float16* __restrict__ A16, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,       \
+      float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,   \
+      float* __restrict__ ws, uint32_t sps) {                                                                \
+    gemm2_body<FMT, BM, BN, WM, WN>(A16, B, D, C, M, N, K, R, epi, ws, sps);                                  \
+  }
+#define DEF_GEMM2_FMT(TAG, FMT)                                   \
+  DEF_GEMM2(smith_gemm2_##TAG##_m128_n64, FMT, 128, 64, 64, 32)   \
+  DEF_GEMM2(smith_gemm2_##TAG##_m128_n128, FMT, 128, 128, 64, 64) \
+  DEF_GEMM2(smith_gemm2_##TAG##_m256_n128, FMT, 256, 128, 64, 64) \
+  DEF_GEMM2(smith_gemm2_##TAG##_m256_n256, FMT, 256, 256, 64, 64)
+DEF_GEMM2_FMT(q4s, WF_Q4S)
+DEF_GEMM2_FMT(q40t, WF_Q40T)
+
+// A16 as smith_gemm_prep_a, with each 8-element chunk in the slot order
+// {0,4,1,5,2,6,3,7} of the gemm2 weight conversion.
+extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a_perm(const float* __restrict__ A,
+                                                                        const float* __restrict__ gamma, float eps,
+                                                                        _Float16* __restrict__ A16, uint32_t K) {
+  __shared__ float red[4];
+  const uint32_t m = blockIdx.x, tid = threadIdx.x;
+  const float* a = A + (size_t)m * K;
+  float rms = 1.f;
+  if (gamma) {
+    float ss = 0.f;
+    for (uint32_t k = 4 * tid; k < K; k += 1024) {
+      const float4 v = *(const float4*)(a + k);
+      ss = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, ss))));
+    }
+    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    rms = 1.0f / __builtin_sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
+  }
+  for (uint32_t k = 8 * tid; k < K; k += 2048) {
+    float4 v0 = *(const float4*)(a + k), v1 = *(const float4*)(a + k + 4);
+    if (gamma) {
+      const float4 g0 = *(const float4*)(gamma + k), g1 = *(const float4*)(gamma + k + 4);
+      v0 = make_float4(v0.x * rms * g0.x, v0.y * rms * g0.y, v0.z * rms * g0.z, v0.w * rms * g0.w);
+      v1 = make_float4(v1.x * rms * g1.x, v1.y * rms * g1.y, v1.z * rms * g1.z, v1.w * rms * g1.w);
+    }
+    // slots (0,4) (1,5) (2,6) (3,7)
+    uint4 o;
+    o.x = pack_h2(v0.x, v1.x);
+    o.y = pack_h2(v0.y, v1.y);
+    o.z = pack_h2(v0.z, v1.z);
+    o.w = pack_h2(v0.w, v1.w);
+    *(uint4*)(A16 + (size_t)m * K + k) = o;
+  }
+}
+
 extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint32_t ks, float* __restrict__ C,
                                              uint32_t M, uint32_t N, const float* __restrict__ R, uint32_t epi) {
   const size_t MN = (size_t)M * N;

@@ -315,6 +315,15 @@ const uint32_t GEMM_MIN_M = 64;
 int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M, uint32_t N,
          uint32_t K, const Epi& ep) {
   if (ensure(c, &c->a16, &c->a16_bytes, (size_t)M * K * 2)) return -1;
+  // Q4_0 tiles with K % 64 == 0: the DMA-staged kernels (smith_gemm2_*),
+  // whose A operand is in the permuted slot order.  (On Q4S records the f32
+  // in-register dequantisation, repeated by the waves sharing a weight
+  // fragment, made them slower at config-4 sizes: 487 vs 331 us.)
+  static const bool gemm2_on = [] {
+    const char* e = getenv("SMITH_GEMM2");
+    return !(e && e[0] == '0');
+  }();
+  const bool g2 = gemm2_on && fmt == FQ40T && K % 64 == 0;
   {
     const float* pa = a;
     const float* pg = ep.gamma;
@@ -322,7 +331,7 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
     void* pd = c->a16;
     uint32_t pK = K;
     void* args[] = {&pa, &pg, &pe, &pd, &pK};
-    if (launch(c, "smith_gemm_prep_a", dim3(M), dim3(256), args)) return -1;
+    if (launch(c, g2 ? "smith_gemm_prep_a_perm" : "smith_gemm_prep_a", dim3(M), dim3(256), args)) return -1;
   }
   // tile choice: the biggest tile that still gives about one tile per CU
   // (bigger tiles carry more MFMA work per K stage to cover load latency);
@@ -332,16 +341,22 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
   if (ntiles(256, 256) >= 256) bm = 256, bn = 256;
   else if (ntiles(256, 128) >= 200) bm = 256, bn = 128;
   else if (ntiles(128, 128) >= 256) bm = 128, bn = 128;
+  if (g2 && M <= 128) bn = ntiles(128, 128) >= 128 ? 128 : 64;
   const uint32_t tiles = ntiles(bm, bn);
   const uint32_t S = (K + 63) / 64;
   uint32_t ks = 1;
-  if (bm == 128 && bn == 64 && tiles < 512) ks = std::min<uint32_t>((512 + tiles - 1) / tiles, std::max<uint32_t>(1, S / 8));
+  if (g2 && bm == 128 && tiles < 512) {
+    // about 450 workgroups, at least 6 stages per split (measured at M = 128)
+    ks = std::min<uint32_t>(std::max<uint32_t>(1, (448 + tiles / 2) / tiles), std::max<uint32_t>(1, S / 6));
+  } else if (bm == 128 && bn == 64 && tiles < 512) {
+    ks = std::min<uint32_t>((512 + tiles - 1) / tiles, std::max<uint32_t>(1, S / 8));
+  }
   const uint32_t sps = (S + ks - 1) / ks;
   ks = (S + sps - 1) / sps;
   if (ks > 1 && ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ks * M * N * sizeof(float))) return -1;
   const uint32_t threads = 64 * (bm / 64) * (bn / (bn >= 128 ? 64 : 32));
   char name[64];
-  snprintf(name, sizeof name, "smith_gemm_%s_m%u_n%u", fmt_tag(fmt), bm, bn);
+  snprintf(name, sizeof name, "smith_gemm%s_%s_m%u_n%u", g2 ? "2" : "", fmt_tag(fmt), bm, bn);
   const void* pA = c->a16;
   const void* pB = B;
   const void* pD = D;
