@@ -208,8 +208,7 @@ def bench_cfg4(D, S, prng, steps=5):
                 "ms_step": round(msx, 3), "kernels_per_step": ktx["launches_per_step"],
                 "gemm_kernel_us": round(kus, 1), "gemm_kernel_TFLOPs": round(fl / kus / 1e6, 1),
                 "gemm_kernel_mfma_util": round(fl / kus / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
-                "path": "f16 activation prep + MFMA GEMM (A and raw Q4S records staged by direct-to-LDS loads, "
-                        "3-stage ring; weights dequantized to f16 in registers; f32 accumulation)"}
+                "path": "f16 activation prep + MFMA GEMM (Q4S dequantized to f16 in LDS, f32 accumulation)"}
             log("cfg4 M=%d N=%d K=%d:" % (M, Nn, Kk), pre["M%d_N%d_K%d" % (M, Nn, Kk)])
     return pre
 
