@@ -354,22 +354,56 @@ __device__ __forceinline__ void dma(const void* g, lds_ptr_t l) {
   else __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
 }
 
+// Tile-plane formats (Q4_0 tiles and gguf_tiles.h): per stage and 16-column
+// tile the weight bytes are contiguous runs in each plane -- nibbles 512 B
+// (2 groups x 16 records x 16 B), high bits 32*hb B, record parameters 32*prm
+// B, super-block parameters 16*sup B -- so each plane is one DMA segment,
+// padded to 256 B (one dword load per lane of a wave).
+template <int FMT>
+struct GtFmt {
+  static constexpr bool TILES = FMT == WF_Q40T || FMT >= GT_Q41;
+  static constexpr int F = FMT == WF_Q40T ? GT_Q40 : FMT;  // gguf_tiles.h code
+  static constexpr int HB = TILES ? (int)gt_hb_bytes(F) : 0;
+  static constexpr int PRM = TILES ? (int)gt_prm_bytes(F) : 0;
+  static constexpr int SUP = TILES ? (int)gt_sup_bytes(F) : 0;
+};
+
+__device__ __forceinline__ constexpr int pad256(int x) { return (x + 255) / 256 * 256; }
+
 template <int FMT, int BM, int BN, int WM, int WN>
 struct G2 {
+  using GF = GtFmt<FMT>;
   static constexpr int NW = (BM / WM) * (BN / WN);
   static constexpr int A_BYTES = BM * 128;
-  static constexpr int REC = FMT == WF_Q4S ? 24 : 16;
-  static constexpr int B_BYTES = BN * 2 * REC;
-  static constexpr int D_BYTES = FMT == WF_Q40T ? BN * 4 : 0;
+  static constexpr int NIB = FMT == WF_Q4S ? BN * 48 : BN * 32;  // Q4S: whole 24 B records
+  static constexpr int HBY = pad256(BN * 2 * GF::HB);
+  static constexpr int PRY = GF::TILES ? pad256(BN * 2 * GF::PRM) : 0;
+  static constexpr int SUY = pad256(BN * GF::SUP);
+  static constexpr int B_BYTES = NIB + HBY + PRY + SUY;
   using UA = DmaUnit<A_BYTES / NW>;
-  using UB = DmaUnit<B_BYTES / NW>;
-  static constexpr int DW = D_BYTES / 256;  // waves that load the d plane, one dword instruction each
-  static_assert(D_BYTES % 256 == 0 && DW <= NW, "d plane split");
-  static constexpr int CNT = UA::N + UB::N;  // DMA instructions per wave per stage (+1 for the d waves)
 };
 
 __device__ __forceinline__ constexpr uint32_t vmcnt_imm(uint32_t n) {
   return (n & 0xF) | (0x7u << 4) | (0xFu << 8) | (((n >> 4) & 3u) << 14);
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n (the immediate must be a constant)
+__device__ __forceinline__ void wait_vm(uint32_t n) {
+  switch (n) {
+#define WV(i) \
+  case i: __builtin_amdgcn_s_waitcnt(vmcnt_imm(i)); break;
+    WV(0) WV(1) WV(2) WV(3) WV(4) WV(5) WV(6) WV(7) WV(8) WV(9) WV(10) WV(11) WV(12) WV(13) WV(14) WV(15)
+    WV(16) WV(17) WV(18) WV(19) WV(20) WV(21) WV(22) WV(23) WV(24) WV(25) WV(26) WV(27) WV(28) WV(29) WV(30)
+#undef WV
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+  }
+}
+
+// DMA instructions (dword, 256 B each) of a padded segment of `bytes` that
+// wave w issues: instruction j goes to wave j % NW
+template <int NW>
+__device__ __forceinline__ constexpr uint32_t seg_count(int bytes, uint32_t w) {
+  return (uint32_t)(bytes / 256) > w ? ((uint32_t)(bytes / 256) - w + NW - 1) / NW : 0u;
 }
 
 template <int FMT, int BM, int BN, int WM, int WN>
@@ -378,11 +412,11 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
                                           uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,
                                           float* __restrict__ ws, uint32_t sps) {
   using P = G2<FMT, BM, BN, WM, WN>;
+  using GF = GtFmt<FMT>;
   constexpr int NW = P::NW, WAVES_N = BN / WN;
   constexpr int TM = WM / 16, TN = WN / 16;
   __shared__ __attribute__((aligned(1024))) uint8_t As0[P::A_BYTES], As1[P::A_BYTES], As2[P::A_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t Bs0[P::B_BYTES + P::D_BYTES], Bs1[P::B_BYTES + P::D_BYTES],
-      Bs2[P::B_BYTES + P::D_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t Bs0[P::B_BYTES], Bs1[P::B_BYTES], Bs2[P::B_BYTES];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -397,6 +431,31 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
   const uint32_t s0 = blockIdx.y * sps < Sall ? blockIdx.y * sps : Sall;
   const uint32_t s1 = s0 + sps < Sall ? s0 + sps : Sall;
   const uint32_t S = s1 - s0;
+  // plane bases (tile formats): Q4_0 tiles take the d plane from D; the
+  // others find their planes after the nibbles (gguf_tiles.h)
+  const GtPlanes PL = gt_planes(GF::F, N, G);
+  const uint8_t* hbp = B + PL.hb;
+  const uint8_t* prp = FMT == WF_Q40T ? (const uint8_t*)D : B + PL.prm;
+  const uint8_t* sup = B + PL.sup;
+  const uint32_t NT16 = N / 16;
+  // this wave's DMA instructions per stage
+  const uint32_t cnt = P::UA::N + seg_count<NW>(P::NIB, wave) + seg_count<NW>(P::HBY, wave) +
+                       seg_count<NW>(P::PRY, wave) + seg_count<NW>(P::SUY, wave);
+
+  // one padded segment: per 16-column tile a run of TPB bytes at plane +
+  // tile_off(tg); lanes past the segment load the last word again (into the pad)
+  auto segment = [&](uint8_t* dst, int bytes, int TPB, auto src_of) {
+    const uint32_t ni = (uint32_t)bytes / 256;
+    for (uint32_t j = wave; j < ni; j += NW) {
+      uint32_t off = j * 256 + lane * 4;
+      const uint32_t real = (uint32_t)(BN / 16) * TPB;
+      off = off < real ? off : real - 4;
+      const uint32_t tt = off / TPB, w = off % TPB;
+      uint32_t tg = n0 / 16 + tt;
+      tg = tg < NT16 ? tg : NT16 - 1;
+      dma<4>(src_of(tg) + w, (lds_ptr_t)(dst + j * 256));
+    }
+  };
 
   // DMA of stage s (absolute) into buffers (as, bs)
   auto issue = [&](uint32_t s, uint8_t* as, uint8_t* bs) {
@@ -410,29 +469,26 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
       const uint32_t m = m0 + row < M ? m0 + row : M - 1;
       dma<P::UA::U>(A16 + (size_t)m * K + k0 + 8 * c + ci, (lds_ptr_t)(as + (wave * P::UA::N + q) * 64 * P::UA::U));
     }
-#pragma unroll
-    for (int q = 0; q < P::UB::N; q++) {
-      const uint32_t off = (wave * P::UB::N + q) * 64 * P::UB::U + lane * P::UB::U;
-      const uint8_t* src;
-      if (FMT == WF_Q4S) {
+    if constexpr (FMT == WF_Q4S) {
+      const uint32_t ni = P::NIB / 256;
+      for (uint32_t j = wave; j < ni; j += NW) {
+        const uint32_t off = j * 256 + lane * 4;
         const uint32_t g2 = off / (BN * 24), w = off % (BN * 24);
         size_t a = ((size_t)(2 * s + g2) * N + n0) * 24 + w;
-        const size_t lim = (size_t)G * N * 24 - P::UB::U;
-        src = B + (a < lim ? a : lim);
-      } else {
-        const uint32_t tt = off / 512, w = off % 512;  // 16-column tile, byte within its 2 groups
-        uint32_t tg = n0 / 16 + tt;
-        tg = tg < N / 16 ? tg : N / 16 - 1;
-        src = B + (((size_t)tg * G + 2 * s) * 16) * 16 + w;
+        const size_t lim = (size_t)G * N * 24 - 4;
+        dma<4>(B + (a < lim ? a : lim), (lds_ptr_t)(bs + j * 256));
       }
-      dma<P::UB::U>(src, (lds_ptr_t)(bs + (wave * P::UB::N + q) * 64 * P::UB::U));
-    }
-    if (FMT == WF_Q40T && wave < (uint32_t)P::DW) {
-      const uint32_t off = wave * 256 + lane * 4;
-      const uint32_t tt = off / 64, w = off % 64;
-      uint32_t tg = n0 / 16 + tt;
-      tg = tg < N / 16 ? tg : N / 16 - 1;
-      dma<4>((const uint8_t*)D + ((size_t)tg * G + 2 * s) * 32 + w, (lds_ptr_t)(bs + P::B_BYTES + wave * 256));
+    } else {
+      const size_t g0 = 2 * s;
+      segment(bs, P::NIB, 512, [&](uint32_t tg) { return B + (((size_t)tg * G + g0) * 16) * 16; });
+      if (GF::HB)
+        segment(bs + P::NIB, P::HBY, 32 * GF::HB,
+                [&](uint32_t tg) { return hbp + (((size_t)tg * G + g0) * 16) * GF::HB; });
+      segment(bs + P::NIB + P::HBY, P::PRY, 32 * GF::PRM,
+              [&](uint32_t tg) { return prp + (((size_t)tg * G + g0) * 16) * GF::PRM; });
+      if (GF::SUP)
+        segment(bs + P::NIB + P::HBY + P::PRY, P::SUY, 16 * GF::SUP,
+                [&](uint32_t tg) { return sup + (((size_t)tg * (G / 8) + g0 / 8) * 16) * GF::SUP; });
     }
   };
 
@@ -442,6 +498,7 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const uint32_t r16 = lane & 15, kq = lane >> 4;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
   auto compute = [&](const uint8_t* as, const uint8_t* bs) {
 #pragma unroll
@@ -456,7 +513,7 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
       for (int j = 0; j < TN; j++) {
         const uint32_t col = wn * WN + j * 16 + r16;
         u32x4 u;
-        if (FMT == WF_Q4S) {
+        if constexpr (FMT == WF_Q4S) {
           const uint8_t* rec = bs + (kk * BN + col) * 24;
           const uint32_t x = *(const uint32_t*)(rec + 4 * kq);
           const float2 sz = *(const float2*)(rec + 16);
@@ -466,23 +523,59 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
           const float clo = -sz.x * (sz.y + 1024.0f), chi = -sz.x * (sz.y + 64.0f);
 #pragma unroll
           for (int d = 0; d < 4; d++) {
-            const _Float16 __attribute__((ext_vector_type(2))) hv =
-                __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), h[d]);
+            const h2 hv = __builtin_bit_cast(h2, h[d]);
             const float c = (d & 1) ? chi : clo;
             u[d] = pack_h2(__builtin_fmaf((float)hv.x, sz.x, c), __builtin_fmaf((float)hv.y, sz.x, c));
           }
         } else {
           const uint32_t tt = col / 16, cc = col % 16;
-          const uint32_t x = *(const uint32_t*)(bs + tt * 512 + kk * 256 + cc * 16 + 4 * kq);
-          const _Float16 dh = *(const _Float16*)(bs + P::B_BYTES + tt * 64 + kk * 32 + cc * 2);
+          const uint32_t ri = (tt * 2 + kk) * 16 + cc;  // record within the stage, tile order
+          const uint32_t x = *(const uint32_t*)(bs + ri * 16 + 4 * kq);
           const uint32_t y = x >> 8;
-          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-          const h2 blo = (h2){(_Float16)1032.0f, (_Float16)1032.0f}, bhi = (h2){(_Float16)72.0f, (_Float16)72.0f};
-          const h2 dd = (h2){dh, dh};
-          const h2 v0 = (__builtin_bit_cast(h2, (x & 0x000F000Fu) | 0x64006400u) - blo) * dd;
-          const h2 v1 = (__builtin_bit_cast(h2, (x & 0x00F000F0u) | 0x54005400u) - bhi) * dd;
-          const h2 v2 = (__builtin_bit_cast(h2, (y & 0x000F000Fu) | 0x64006400u) - blo) * dd;
-          const h2 v3 = (__builtin_bit_cast(h2, (y & 0x00F000F0u) | 0x54005400u) - bhi) * dd;
+          uint32_t bx = 0x64006400u, by = 0x54005400u, bz = 0x64006400u, bw = 0x54005400u;
+          if constexpr (GF::F == GT_Q50) {
+            const uint32_t W = *(const uint32_t*)(bs + P::NIB + ri * 4);
+            // element 8kq + k: bit 4kq + (k & 3) + 16 (k >> 2) (gguf_tiles.h)
+            bx |= ((W >> (4 * kq)) << 4) & 0x00100010u;
+            by |= ((W >> (4 * kq + 1)) << 8) & 0x01000100u;
+            bz |= ((W >> (4 * kq + 2)) << 4) & 0x00100010u;
+            bw |= ((W >> (4 * kq + 3)) << 8) & 0x01000100u;
+          } else if constexpr (GF::F == GT_Q6K) {
+            const uint2 hw = *(const uint2*)(bs + P::NIB + ri * 8);
+            const uint32_t W = kq < 2 ? hw.x : hw.y, cb = 4 * (kq & 1);
+            bx |= ((W >> (2 * cb)) << 4) & 0x00300030u;
+            by |= ((W >> (2 * cb + 2)) << 8) & 0x03000300u;
+            bz |= ((W >> (2 * cb + 4)) << 4) & 0x00300030u;
+            bw |= ((W >> (2 * cb + 6)) << 8) & 0x03000300u;
+          }
+          // w = s*q + c with q = h - bias exact in f16
+          h2 sv, cv;
+          const uint8_t* prm = bs + P::NIB + P::HBY;
+          if constexpr (GF::F == GT_Q40 || GF::F == GT_Q50) {
+            const _Float16 d = *(const _Float16*)(prm + ri * 2);
+            const _Float16 c = d * (_Float16)(GF::F == GT_Q40 ? -8.0f : -16.0f);  // exact
+            sv = (h2){d, d};
+            cv = (h2){c, c};
+          } else if constexpr (GF::F == GT_Q41) {
+            const h2 dm = *(const h2*)(prm + ri * 4);  // (d, m)
+            sv = (h2){dm.x, dm.x};
+            cv = (h2){dm.y, dm.y};
+          } else {  // Q4_K, Q6_K: f32 products of the f16 and the 6-bit / int8 scales, rounded to f16
+            float s0f, c0f, s1f, c1f;
+            GtW<GF::F> w;
+            w.p = *(const uint16_t*)(prm + ri * 2);
+            w.sp = GF::SUP == 4 ? *(const uint32_t*)(prm + P::PRY + (tt * 16 + cc) * 4)
+                                : *(const uint16_t*)(prm + P::PRY + (tt * 16 + cc) * 2);
+            gt_affine<GF::F>(w, s0f, c0f, s1f, c1f);
+            const float sf = kq < 2 ? s0f : s1f, cf = kq < 2 ? c0f : c1f;
+            sv = (h2){(_Float16)sf, (_Float16)sf};
+            cv = (h2){(_Float16)cf, (_Float16)cf};
+          }
+          const h2 blo = (h2){(_Float16)1024.0f, (_Float16)1024.0f}, bhi = (h2){(_Float16)64.0f, (_Float16)64.0f};
+          const h2 v0 = __builtin_elementwise_fma(__builtin_bit_cast(h2, (x & 0x000F000Fu) | bx) - blo, sv, cv);
+          const h2 v1 = __builtin_elementwise_fma(__builtin_bit_cast(h2, (x & 0x00F000F0u) | by) - bhi, sv, cv);
+          const h2 v2 = __builtin_elementwise_fma(__builtin_bit_cast(h2, (y & 0x000F000Fu) | bz) - blo, sv, cv);
+          const h2 v3 = __builtin_elementwise_fma(__builtin_bit_cast(h2, (y & 0x00F000F0u) | bw) - bhi, sv, cv);
           u = (u32x4){__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
                       __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)};
         }
@@ -499,10 +592,8 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
   if (S > 0) issue(s0, As0, Bs0);
   if (S > 1) issue(s0 + 1, As1, Bs1);
   auto step = [&](uint32_t s, uint8_t* as, uint8_t* bs, uint8_t* an, uint8_t* bn) {
-    // this wave's DMA of stage s done (the later stages may stay in flight), then all waves'
-    if (s + 1 >= S) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    else if (FMT == WF_Q40T && wave < (uint32_t)P::DW) __builtin_amdgcn_s_waitcnt(vmcnt_imm(P::CNT + 1));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(P::CNT));
+    // this wave's DMA of stage s done (stage s+1 may stay in flight), then all waves'
+    wait_vm(s + 1 < S ? cnt : 0u);
     __builtin_amdgcn_s_barrier();
     if (s + 2 < S) issue(s0 + s + 2, an, bn);  // into the buffer stage s-1 used (all waves are past it)
     compute(as, bs);
@@ -536,7 +627,8 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
 }
 
 #define DEF_GEMM2(NAME, FMT, BM, BN, WM, WN)                                                                  \
-  extern "C" __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN)) void NAME(                            \
+  extern "C" __global__ __launch_bounds__(64 * (BM / WM) * (BN / WN))                                       \
+  __attribute__((amdgpu_waves_per_eu(2))) void NAME(                                                          \
       const _Float16* __restrict__ A16, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,       \
       float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K, const float* __restrict__ R, uint32_t epi,   \
       float* __restrict__ ws, uint32_t sps) {                                                                \
@@ -547,8 +639,11 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
   DEF_GEMM2(smith_gemm2_##TAG##_m128_n128, FMT, 128, 128, 64, 64) \
   DEF_GEMM2(smith_gemm2_##TAG##_m256_n128, FMT, 256, 128, 64, 64) \
   DEF_GEMM2(smith_gemm2_##TAG##_m256_n256, FMT, 256, 256, 64, 64)
-DEF_GEMM2_FMT(q4s, WF_Q4S)
 DEF_GEMM2_FMT(q40t, WF_Q40T)
+DEF_GEMM2_FMT(q41t, GT_Q41)
+DEF_GEMM2_FMT(q50t, GT_Q50)
+DEF_GEMM2_FMT(q4kt, GT_Q4K)
+DEF_GEMM2_FMT(q6kt, GT_Q6K)
 
 // A16 as smith_gemm_prep_a, with each 8-element chunk in the slot order
 // {0,4,1,5,2,6,3,7} of the gemm2 weight conversion.

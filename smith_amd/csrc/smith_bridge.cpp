@@ -315,7 +315,8 @@ const uint32_t GEMM_MIN_M = 64;
 int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M, uint32_t N,
          uint32_t K, const Epi& ep) {
   if (ensure(c, &c->a16, &c->a16_bytes, (size_t)M * K * 2)) return -1;
-  // Q4_0 tiles with K % 64 == 0: the DMA-staged kernels (smith_gemm2_*),
+  // tile-plane formats (Q4_0 tiles, Q4_1, Q5_0, Q4_K, Q6_K) with K % 64 == 0:
+  // the DMA-staged kernels (smith_gemm2_*),
   // whose A operand is in the permuted slot order.  (On Q4S records the f32
   // in-register dequantisation, repeated by the waves sharing a weight
   // fragment, made them slower at config-4 sizes: 487 vs 331 us.)
@@ -323,7 +324,7 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
     const char* e = getenv("SMITH_GEMM2");
     return !(e && e[0] == '0');
   }();
-  const bool g2 = gemm2_on && fmt == FQ40T && K % 64 == 0;
+  const bool g2 = gemm2_on && (fmt == FQ40T || fmt >= FQ41T) && K % 64 == 0;
   {
     const float* pa = a;
     const float* pg = ep.gamma;
@@ -342,6 +343,7 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
   else if (ntiles(256, 128) >= 200) bm = 256, bn = 128;
   else if (ntiles(128, 128) >= 256) bm = 128, bn = 128;
   if (g2 && M <= 128) bn = ntiles(128, 128) >= 128 ? 128 : 64;
+  if (g2 && bm == 256 && bn == 256) bn = 128;  // 256x256 spills registers on the high-bit formats
   const uint32_t tiles = ntiles(bm, bn);
   const uint32_t S = (K + 63) / 64;
   uint32_t ks = 1;

@@ -61,7 +61,7 @@ def test_code_object_has_kernels():
     for k in ["smith_gemm_prep_a", "smith_gemm_prep_a_perm", "smith_gemm_reduce"] + [
             "smith_gemm_%s_m%d_n%d" % (f, m, n) for f in ("q4s", "q8", "q40", "q40t", "q41t", "q50t", "q4kt", "q6kt")
             for (m, n) in ((128, 64), (128, 128), (256, 128), (256, 256))] + [
-            "smith_gemm2_%s_m%d_n%d" % (f, m, n) for f in ("q4s", "q40t")
+            "smith_gemm2_%s_m%d_n%d" % (f, m, n) for f in ("q40t", "q41t", "q50t", "q4kt", "q6kt")
             for (m, n) in ((128, 64), (128, 128), (256, 128), (256, 256))]:
         assert re.search(r"\b%s\.kd\b" % k, out), k
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],

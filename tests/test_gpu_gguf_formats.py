@@ -306,7 +306,9 @@ def test_generate_mixed_formats(tmp_path_factory, kw):
     for i, tk in enumerate([5, 250, 17]):
         g = m.forwardDecode(tk, len(prompt) + i, caches)["logits"]
         w = ref.forward([tk], len(prompt) + i)
-        assert normwise_rel_err(g, w) <= 1e-3, i
+        # the path's 1e-2: these steps read K/V written by the f16-MFMA prefill
+        # (f16 weights, and on Q4_K / Q6_K an f16-rounded scale): ~1e-3 observed
+        assert normwise_rel_err(g, w) <= 1e-2, i
 
 
 @pytest.mark.parametrize("t1,t2", [(O.GGML_Q4_K, O.GGML_Q6_K), (O.GGML_Q4_K, O.GGML_Q5_0), (O.GGML_Q5_0, O.GGML_Q6_K),
