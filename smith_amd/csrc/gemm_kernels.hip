@@ -4,7 +4,10 @@
 // multiplied on v_mfma_f32_16x16x32_f16 with f32 accumulation.
 //
 //   smith_gemm_prep_a   A (f32, optional RMSNorm with gamma) -> A16 (f16)
-//   smith_gemm_<fmt>_m<BM>_n<BN>  the GEMM, fmt in {q4s, q8, q40, q40t}
+//   smith_gemm_<fmt>_m<BM>_n<BN>  the GEMM, fmt in {q4s, q8, q40, q40t, q41t,
+//                       q50t, q4kt, q6kt}
+//   smith_gemm_prep_a_perm + smith_gemm2_<fmt>_m<BM>_n<BN>  the DMA-staged
+//                       GEMM for the tile-plane formats (further below)
 //
 // Workgroup tile BM x BN (128x64 .. 256x256), K in stages of BK=64 (two
 // 32-row quantization groups), double-buffered in LDS: while the MFMAs
