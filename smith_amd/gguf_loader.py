@@ -40,10 +40,41 @@ LLAMA_MAP = {
 }
 
 
+# gguf_loader.js:48-84: name maps of the other architectures (their weights
+# are only loaded; forward is Llama-only, gguf_loader.js:394-396)
+PHI_MAP = {
+    "token_embd.weight": "embedding.tokenWeight",
+    "output_norm.weight": "lnFGamma",
+    "output_norm.bias": "lnFBeta",
+    "output.weight": "lmHead",
+    "blk.{L}.attn_norm.weight": "blocks.{L}.ln1Gamma",
+    "blk.{L}.attn_norm.bias": "blocks.{L}.ln1Beta",
+    "blk.{L}.ffn_norm.weight": "blocks.{L}.ln2Gamma",
+    "blk.{L}.ffn_norm.bias": "blocks.{L}.ln2Beta",
+    "blk.{L}.attn_qkv.weight": "blocks.{L}.mha.qkvProj.weight",
+    "blk.{L}.attn_qkv.bias": "blocks.{L}.mha.qkvProj.bias",
+    "blk.{L}.attn_output.weight": "blocks.{L}.mha.outProj.weight",
+    "blk.{L}.attn_output.bias": "blocks.{L}.mha.outProj.bias",
+    "blk.{L}.ffn_up.weight": "blocks.{L}.ffn1.weight",
+    "blk.{L}.ffn_up.bias": "blocks.{L}.ffn1.bias",
+    "blk.{L}.ffn_down.weight": "blocks.{L}.ffn2.weight",
+    "blk.{L}.ffn_down.bias": "blocks.{L}.ffn2.bias",
+}
+GPT2_MAP = dict(PHI_MAP)
+del GPT2_MAP["output.weight"]
+GPT2_MAP["position_embd.weight"] = "embedding.posWeight"
+GPT2_MAP["blk.{L}.attn_qkv.weight"] = "blocks.{L}.mha.qkvFused.weight"
+GPT2_MAP["blk.{L}.attn_qkv.bias"] = "blocks.{L}.mha.qkvFused.bias"
+
+
 def getWeightMap(arch):
-    """gguf_loader.js:86-91 (only the Llama map drives generate, finding 8)."""
+    """gguf_loader.js:86-91."""
     if arch == "llama":
         return LLAMA_MAP
+    if arch in ("phi", "phi2", "phi3"):
+        return PHI_MAP
+    if arch == "gpt2":
+        return GPT2_MAP
     raise ValueError("Unsupported GGUF architecture: %s" % arch)
 
 
@@ -364,12 +395,76 @@ class GGUFModel(dict):
             raise AttributeError(k)
 
 
+def _load_other(parsed, config):
+    """createGGUFModel + loadWeights (gguf_loader.js:151-273) for the
+    non-Llama architectures, whose weights the reference loads but never
+    runs: the same parameter set (q/k/v/out projections, ffn1/ffn2, the
+    final norm's beta; no RoPE table for gpt2), the same loaded / skipped
+    lists ("name → path (not found in model)" when the map names a parameter
+    the model lacks), each loaded tensor decoded on the device and stored f32
+    in the Smith shape (transposed when listed [out, in], :240-259), and
+    weight tying when output.weight is absent (:266-270)."""
+    dim, nH = config["dim"], config["numHeads"]
+    hd = dim // nH
+    kvd = (config["numKVHeads"] or nH) * hd
+    ffn = config["ffnDim"] or int(round(dim * 8 / 3 / 256) * 256)
+    vocab = config["vocabSize"]
+    shapes = {"embedding.tokenWeight": (vocab, dim), "lnFGamma": (dim,), "lnFBeta": (dim,), "lmHead": (dim, vocab)}
+    for L in range(config["numLayers"]):
+        b = "blocks.%d." % L
+        shapes.update({b + "ln1Gamma": (dim,), b + "ln2Gamma": (dim,), b + "mha.qProj.weight": (dim, dim),
+                       b + "mha.kProj.weight": (dim, kvd), b + "mha.vProj.weight": (dim, kvd),
+                       b + "mha.outProj.weight": (dim, dim), b + "ffn1.weight": (dim, ffn),
+                       b + "ffn2.weight": (ffn, dim)})
+    wmap = getWeightMap(config["arch"])
+    params, loaded, skipped = {}, [], []
+    for info in parsed["tensors"]:
+        path = resolveWeight(info["name"], wmap)
+        if path is None:
+            skipped.append(info["name"])
+            continue
+        if path not in shapes:
+            skipped.append("%s \u2192 %s (not found in model)" % (info["name"], path))
+            continue
+        flat = device_f32(parsed, info)
+        shp = shapes[path]
+        is_weight = path.endswith(".weight") and not any(t in path for t in ("embd", "norm", "Gamma"))
+        if is_weight and len(info["shape"]) == 2 and tuple(shp) == (info["shape"][1], info["shape"][0]):
+            rows, cols = info["shape"]
+            host = flat.numpy().reshape(rows, cols).T
+            device.release_buffer(flat.ptr)
+            params[path] = DeviceArray.from_host(host)
+        else:
+            flat.shape = tuple(shp) if int(np.prod(shp)) == flat.shape[0] else flat.shape
+            params[path] = flat
+        loaded.append(info["name"])
+    model = {"config": dict(config, headDim=hd, kvDim=kvd, ffnDim=ffn), "arch": config["arch"],
+             "normEps": float(config["normEps"]), "params": params}
+    if "output.weight" not in loaded:
+        params["lmHead"] = params.get("embedding.tokenWeight")
+        model["weightTied"] = True
+    if config["arch"] != "gpt2":
+        cos, sin = precomputeRoPE(hd, config["maxSeqLen"], config["ropeFreqBase"])
+        model["rope"] = {"cos": DeviceArray.from_host(cos), "sin": DeviceArray.from_host(sin)}
+    device.sync()
+    return model, loaded, skipped
+
+
 def loadGGUF(path):
     """gguf_loader.js:381-405."""
     parsed = G.loadGGUFFile(path)
     config = G.extractConfig(parsed["metadata"])
     if config["arch"] != "llama":
-        raise ValueError("Forward not implemented for %s via GGUF loader" % config["arch"])
+        model, loaded, skipped = _load_other(parsed, config)
+
+        def unsupported(*_a, **_k):
+            # the reference's forward throws this (gguf_loader.js:394-396); its
+            # cached entry points fail on the missing Llama FFN for these models
+            raise RuntimeError("Forward not implemented for %s via GGUF loader" % config["arch"])
+        return GGUFModel(model=model, config=config, metadata=parsed["metadata"], loaded=loaded, skipped=skipped,
+                         forward=unsupported, createCache=lambda: createGGUFCache(model["config"]),
+                         forwardPrefill=unsupported, forwardDecode=unsupported, generate=unsupported,
+                         resetCache=resetCache)
     model = createGGUFModel(config)
     res = loadWeights(parsed, model)
     return GGUFModel(
