@@ -315,7 +315,7 @@ def e2e_weight_bytes(mix):
         return 1981808640 + 55296000  # Q4_0 linears + Q4_0 LM head
     q4k = L * (2 * d * d + d * kv + 2 * d * f)  # q, o, k, gate, up
     q6k = L * (d * kv + f * d)                  # v, down
-    return q4k * 144 // 256 + q6k * 210 // 256 + d * v * 4  # + the f32 LM head
+    return q4k * 144 // 256 + q6k * 210 // 256 + d * v * 210 // 256  # + the Q6_K LM head
 
 
 def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3, mix="q4_0"):

@@ -246,6 +246,15 @@ int smith_gguf_tiles_pair_ok(uint32_t type1, uint32_t type2);
 int smith_linear_gguf_tiles_pair_act(void* ctx, uint32_t type1, const void* planes1, uint32_t N1, uint32_t type2,
                                      const void* planes2, uint32_t N2, const void* act_in, int norm, float eps,
                                      float* out, uint32_t K);
+/* LM head on a Q6_K output.weight read as lmHead[K=dim][N=vocab] (256-element
+ * blocks along vocab, dequantQ6_K src/gguf.js:309-339): the blocks are split
+ * into one plane buffer of smith_lmhead_q6_k_bytes(K, N) bytes (nibbles,
+ * high bits, int8 scales and f16 d; N % 256 == 0), then
+ * y = rmsnorm(x, gamma) . lmHead as smith_lmhead_q4_0_nb (K % 16 == 0). */
+uint64_t smith_lmhead_q6_k_bytes(uint32_t K, uint32_t N);
+int smith_repack_lmhead_q6_k(void* ctx, const void* blocks, void* planes, uint32_t K, uint32_t N);
+int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes, float* y,
+                         uint32_t K, uint32_t N);
 /* dequantizeTensor (src/gguf.js:343-394) on the device: numel elements of a
  * flat GGUF tensor of type F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q8_0, Q4_K or
  * Q6_K to f32, bit-identical to the reference's Float32Array. */

@@ -913,6 +913,176 @@ extern "C" __global__ void smith_randn_f32(float* __restrict__ out, uint64_t n, 
 }
 
 // ---------------------------------------------------------------------------
+// LM head on a Q6_K output.weight read as lmHead[K=dim][N=vocab] (256-element
+// blocks along vocab, dequantQ6_K, src/gguf.js:309-339).  Planes of one
+// buffer (offsets below): per (k, 32-column group vb) 16 B of low nibbles
+// (the block's ql bytes of that group) and 8 B of high bits (its qh bytes:
+// element e's 2 bits at bit 2e), the int8 scales transposed to [N/16][K] and
+// the f16 d to [N/256][K] (16 / 8 rows per 16-byte load).  Same structure as
+// smith_lmhead_q4_0_nb: lane (vb, sub) owns outputs 32vb + 8sub .. +7; per
+// row c = x_k * d * scale, 8 fma(c, q) and one -32c correction.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline void lmh6_offsets(uint32_t K, uint32_t N, size_t* hb, size_t* sc, size_t* d, size_t* total) {
+  const size_t KN = (size_t)K * N;
+  *hb = gt_align(KN / 2);
+  *sc = gt_align(*hb + KN / 4);
+  *d = gt_align(*sc + KN / 16);
+  *total = gt_align(*d + KN / 256 * 2);
+}
+
+extern "C" __global__ void smith_repack_lmhead_q6_k(const uint8_t* __restrict__ src, uint8_t* __restrict__ planes,
+                                                    uint32_t K, uint32_t N) {
+  size_t ohb, osc, od, tot;
+  lmh6_offsets(K, N, &ohb, &osc, &od, &tot);
+  const uint32_t NB = N / 256, NB32 = N / 32;
+  const size_t total = (size_t)K * NB;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t k = (uint32_t)(idx / NB), vb = (uint32_t)(idx % NB);
+    const uint8_t* b = src + idx * 210;
+    for (int i8 = 0; i8 < 8; i8++) {
+      const size_t r = (size_t)k * NB32 + vb * 8 + i8;
+      for (int q = 0; q < 16; q++) planes[r * 16 + q] = b[16 * i8 + q];
+      for (int q = 0; q < 8; q++) planes[ohb + r * 8 + q] = b[128 + 8 * i8 + q];
+    }
+    for (int t = 0; t < 16; t++) planes[osc + ((size_t)vb * 16 + t) * K + k] = b[192 + t];
+    ((uint16_t*)(planes + od))[(size_t)vb * K + k] = (uint16_t)(b[208] | (b[209] << 8));
+  }
+}
+
+extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
+    const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ planes,
+    float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws, uint32_t* __restrict__ counters) {
+  __shared__ float xs[8192];
+  __shared__ float part[8][512];
+  __shared__ float red[8];
+  __shared__ int s_last;
+  size_t ohb, osc, od, tot;
+  lmh6_offsets(K, N, &ohb, &osc, &od, &tot);
+  const uint8_t* nib = planes;
+  const uint16_t* hbp = (const uint16_t*)(planes + ohb);
+  const int8_t* scp = (const int8_t*)(planes + osc);
+  const uint16_t* dp = (const uint16_t*)(planes + od);
+  const uint32_t NB = N / 32;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t vb0 = blockIdx.x * 16 + lane / 4, sub = lane & 3;
+  const uint32_t vb = vb0 < NB ? vb0 : NB - 1;  // clamped; lanes past NB store nothing
+  const uint32_t v16 = 2 * vb + sub / 2, v256 = vb / 8;
+  const uint32_t ksplit = gridDim.y;
+  // split and wave row counts are multiples of 16 (K % 16 == 0): aligned 16-byte scale loads
+  const uint32_t kb = ((K + ksplit - 1) / ksplit + 15) / 16 * 16;
+  const uint32_t kb0 = blockIdx.y * kb < K ? blockIdx.y * kb : K, kb1 = kb0 + kb < K ? kb0 + kb : K;
+  const uint32_t kper = ((kb1 - kb0 + 7) / 8 + 15) / 16 * 16;
+  const uint32_t k0 = kb0 + wave * kper < kb1 ? kb0 + wave * kper : kb1;
+  const uint32_t k1 = k0 + kper < kb1 ? k0 + kper : kb1;
+
+  float xv[16], gvv[16];
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const uint32_t i = threadIdx.x + 512 * q;
+    xv[q] = i < K ? x[i] : 0.f;
+    gvv[q] = gamma && i < K ? gamma[i] : 1.f;
+  }
+  uint32_t wn[LMH_BATCH], wh[LMH_BATCH];
+  uint4 ws8, wd[2];
+  auto load_batch = [&](uint32_t kbase) {
+#pragma unroll
+    for (int r = 0; r < LMH_BATCH; r++) {
+      const uint32_t k = kbase + r < k1 ? kbase + r : (k1 > 0 ? k1 - 1 : 0);
+      wn[r] = *(const uint32_t*)(nib + ((size_t)k * NB + vb) * 16 + 4 * sub);
+      wh[r] = hbp[((size_t)k * NB + vb) * 4 + sub];
+    }
+    const uint32_t kc = kbase < K ? kbase : K - 16;  // K % 16 == 0
+    ws8 = *(const uint4*)(scp + (size_t)v16 * K + kc);
+    wd[0] = *(const uint4*)(dp + (size_t)v256 * K + kc);
+    wd[1] = *(const uint4*)(dp + (size_t)v256 * K + kc + 8);
+  };
+  if (k0 < k1) load_batch(k0);
+
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; q++) ss = __builtin_fmaf(xv[q], xv[q], ss);
+  float rms = 1.f;
+  if (gamma) {
+    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot2 = 0.f;
+    for (int w = 0; w < 8; w++) tot2 += red[w];
+    rms = 1.0f / __builtin_sqrtf(tot2 / (float)K + eps);
+  }
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const uint32_t i = threadIdx.x + 512 * q;
+    if (i < K) xs[i] = gamma ? xv[q] * rms * gvv[q] : xv[q];
+  }
+  __syncthreads();
+
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = 0.f;
+  float corr = 0.f;
+  for (uint32_t kb16 = k0; kb16 < k1; kb16 += LMH_BATCH) {
+    uint32_t cn[LMH_BATCH], ch[LMH_BATCH];
+#pragma unroll
+    for (int r = 0; r < LMH_BATCH; r++) {
+      cn[r] = wn[r];
+      ch[r] = wh[r];
+    }
+    const uint4 cs = ws8, cd0 = wd[0], cd1 = wd[1];
+    if (kb16 + LMH_BATCH < k1) load_batch(kb16 + LMH_BATCH);
+#pragma unroll
+    for (int r = 0; r < LMH_BATCH; r++) {
+      const uint32_t k = kb16 + r;
+      const uint32_t sw = (&cs.x)[r / 4];
+      const int8_t sc = (int8_t)((sw >> (8 * (r % 4))) & 0xFFu);
+      const uint32_t dw = r < 8 ? (&cd0.x)[r / 2] : (&cd1.x)[(r - 8) / 2];
+      const uint16_t dh = (uint16_t)((r & 1) ? dw >> 16 : dw & 0xFFFFu);
+      const float c = k < k1 ? xs[k] * ((float)__builtin_bit_cast(_Float16, dh) * (float)sc) : 0.f;
+      const uint32_t w = cn[r], h = ch[r];
+      corr += c;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const uint32_t q = ((w >> (4 * e)) & 0xFu) | (((h >> (2 * e)) & 3u) << 4);
+        acc[e] = __builtin_fmaf(c, (float)q, acc[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) part[wave][lane * 8 + e] = __builtin_fmaf(-32.0f, corr, acc[e]);
+  __syncthreads();
+  const uint32_t nb0 = blockIdx.x * 512;
+  const uint32_t o = threadIdx.x, n = nb0 + o;
+  float v = 0.f;
+#pragma unroll
+  for (int w = 0; w < 8; w++) v += part[w][o];
+  if (ksplit == 1) {
+    if (n < N) y[n] = v;
+    return;
+  }
+  if (n < N)
+    __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == ksplit - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (n < N) {
+    float t = 0.f;
+    for (uint32_t sp = 0; sp < ksplit; sp++)
+      t += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n, 0u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT));
+    y[n] = t;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // GGUF weights [out=N rows, in=K] of Q4_0 / Q4_1 / Q5_0 / Q4_K / Q6_K blocks
 // -> the tile planes of gguf_tiles.h.  Values are moved, never changed: the
 // same integers, f16 fields and 6-bit / int8 scales the reference's decoders

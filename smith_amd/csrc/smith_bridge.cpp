@@ -1438,6 +1438,44 @@ int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, flo
   return launch(c, "smith_lmhead_q4_0_nb", dim3(gx, ksplit), dim3(512), args);
 }
 
+uint64_t smith_lmhead_q6_k_bytes(uint32_t K, uint32_t N) {
+  if (!K || !N || N % 256) return 0;
+  const size_t KN = (size_t)K * N;
+  size_t hb = gt_align(KN / 2), sc = gt_align(hb + KN / 4), d = gt_align(sc + KN / 16);
+  return gt_align(d + KN / 256 * 2);
+}
+
+int smith_repack_lmhead_q6_k(void* ctx, const void* blocks, void* planes, uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (N % 256 || !N) return fail(c, "smith_repack_lmhead_q6_k: vocab %u is not a multiple of 256", N);
+  if (set_device(c)) return -1;
+  uint64_t total = (uint64_t)K * (N / 256);
+  if (!total) return 0;
+  void* args[] = {&blocks, &planes, &K, &N};
+  return launch(c, "smith_repack_lmhead_q6_k", dim3((unsigned)std::min<uint64_t>((total + 255) / 256, 1 << 20)),
+                dim3(256), args);
+}
+
+int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes, float* y,
+                         uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (N % 256 || !N) return fail(c, "smith_lmhead_q6_k_nb: vocab %u is not a multiple of 256", N);
+  if (K > 8192 || K % 16 || !K) return fail(c, "smith_lmhead_q6_k_nb: dim %u unsupported (16..8192, %% 16)", K);
+  if (set_device(c)) return -1;
+  uint32_t gx = (N / 32 + 15) / 16;
+  uint32_t ksplit = std::max<uint32_t>(1, std::min<uint32_t>((K + 255) / 256, 64));
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  void* args[] = {&x, &norm_gamma, &eps, &planes, &y, &K, &N, &pws, &pcnt};
+  return launch(c, "smith_lmhead_q6_k_nb", dim3(gx, ksplit), dim3(512), args);
+}
+
 int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,
                    uint32_t K, uint32_t N, int w_is_nk) {
   Ctx* c = (Ctx*)ctx;

@@ -154,6 +154,9 @@ class _Engine:
             rc = device.lib.smith_lmhead_q4_0_nb(ctx, x_ptr, g, eps, head["nib"].ptr, head["d"].ptr, self.logits.ptr,
                                                  cfg["dim"],
                                                  cfg["vocabSize"])
+        elif head["kind"] == "q6_k_nb":
+            rc = device.lib.smith_lmhead_q6_k_nb(ctx, x_ptr, g, eps, head["planes"].ptr, self.logits.ptr, cfg["dim"],
+                                                 cfg["vocabSize"])
         elif head["kind"] == "f32_kn":
             rc = device.lib.smith_gemv_f32(ctx, x_ptr, g, eps, head["w"].ptr, self.logits.ptr, cfg["dim"],
                                            cfg["vocabSize"], 0)

@@ -377,6 +377,14 @@ def loadWeights(parsed, model):
         model["lmHead"] = {"kind": "q4_0_nb", "nib": nibp, "d": dscp}
     elif head["type"] in (G.GGML_TYPE["F32"], G.GGML_TYPE["F16"]):
         model["lmHead"] = {"kind": "f32_kn", "w": DeviceArray.from_host(G.dense_f32(parsed, head))}
+    elif head["type"] == G.GGML_TYPE["Q6_K"] and vocab % 256 == 0 and dim % 16 == 0 and dim <= 8192:
+        raw = DeviceArray.from_host(np.asarray(G.readTensorData(parsed, head)), np.uint8)
+        planes = DeviceArray((int(device.lib.smith_lmhead_q6_k_bytes(dim, vocab)),), np.uint8)
+        device.check(device.lib.smith_repack_lmhead_q6_k(device.ops_ctx(), raw.ptr, planes.ptr, dim, vocab),
+                     "repack output.weight")
+        device.sync()
+        device.release_buffer(raw.ptr)
+        model["lmHead"] = {"kind": "q6_k_nb", "planes": planes}
     else:
         # other block types: decoded once to the f32 [dim][vocab] the reference
         # builds (its blocks run along vocab, so no K-blocked GEMV applies)

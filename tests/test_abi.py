@@ -67,7 +67,7 @@ def test_code_object_has_kernels():
     out = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--syms", device.LLAMA_CODE_OBJECT_PATH],
                          capture_output=True, text=True, check=True).stdout
     for k in ["smith_rmsnorm_rows", "smith_embed_rows", "smith_attention", "smith_attention_part", "smith_kv_append", "smith_attention_cached",
-              "smith_lmhead_q4_0_nb", "smith_repack_lmhead_q4_0",
+              "smith_lmhead_q4_0_nb", "smith_repack_lmhead_q4_0", "smith_lmhead_q6_k_nb", "smith_repack_lmhead_q6_k",
               "smith_gemv_f32_kn", "smith_gemv_f32_nk", "smith_argmax_embed", "smith_set_i32", "smith_randn_f32"] + [
               "smith_repack_gt_%s" % f for f in ("q40", "q41", "q50", "q4k", "q6k")] + [
               "smith_attention_prefill_hd%d" % n for n in range(1, 9)] + [

@@ -331,3 +331,25 @@ def test_pair_act_gemv(t1, t2, K):
     want = np.concatenate([w1, w2]).astype(np.float64) @ _rms(x, g)
     assert normwise_rel_err(_get(out, N1 + N2), want) <= TOL
     assert device.lib.smith_gguf_tiles_pair_ok(O.GGML_Q6_K, O.GGML_Q4_1) == 0
+
+
+@pytest.mark.parametrize("K,N", [(256, 256), (3072, 32000), (8192, 512), (48, 768)])
+def test_lmhead_q6_k_matches_reference(K, N):
+    """Q6_K output.weight read as lmHead[K][N] (256-element blocks along N):
+    planes from smith_repack_lmhead_q6_k, y = rmsnorm(x) . lmHead vs float64
+    of the oracle's weights (f32 FMA throughout: 2e-6)."""
+    w = prng.randn((K, N), 81, std=0.02)
+    blocks = O.quantize_rows(O.GGML_Q6_K, w)  # rows of N: blocks run along the vocab axis
+    wd = O.dequantize_tensor(O.GGML_Q6_K, blocks, K * N).reshape(K, N).astype(np.float64)
+    ctx = device.ops_ctx()
+    src = _buf(blocks)
+    planes = device.alloc(int(device.lib.smith_lmhead_q6_k_bytes(K, N)))
+    device.check(device.lib.smith_repack_lmhead_q6_k(ctx, src, planes, K, N))
+    x = prng.randn((K,), 82).astype(np.float64)
+    g = 1 + prng.randn((K,), 83, std=0.1).astype(np.float64)
+    xb, gb, yb = _buf(x.astype(np.float32)), _buf(g.astype(np.float32)), device.alloc(N * 4)
+    device.check(device.lib.smith_lmhead_q6_k_nb(ctx, xb, gb, EPS, planes, yb, K, N))
+    assert normwise_rel_err(_get(yb, N), _rms(x, g) @ wd) <= 2e-6
+    device.check(device.lib.smith_lmhead_q6_k_nb(ctx, xb, None, 0.0, planes, yb, K, N))
+    assert normwise_rel_err(_get(yb, N), x @ wd) <= 2e-6
+    assert device.lib.smith_lmhead_q6_k_nb(ctx, xb, None, 0.0, planes, yb, 40, N) != 0  # K % 16
