@@ -496,14 +496,22 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
     r.q = *(const u32x4*)(B + rec * 16);
     r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
   } else {
+    // the 36 bytes from the dword holding the record's first byte, in two
+    // 128-bit loads + one dword (global loads need dword alignment only):
+    // 3 load instructions per record.  Records are 2-byte aligned: at an
+    // aligned record the f16 scale is bytes 0-1 and the int8 start at byte 2;
+    // otherwise the scale is bytes 2-3 and the int8 are dwords 1..8.
     const uint8_t* p = B + rec * 34;
-    r.s = (float)__builtin_bit_cast(_Float16, *(const uint16_t*)p);
-    size_t a = (size_t)(p + 2);
+    const size_t a = (size_t)p;
     const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
-    r.sh = (uint32_t)(a & 3);  // bytes: 0 or 2
-    r.q = (u32x4){w[0], w[1], w[2], w[3]};
-    r.q8b = (u32x4){w[4], w[5], w[6], w[7]};
-    r.q8c = w[8];
+    u32x4 w0 = *(const u32x4*)w, w1 = *(const u32x4*)(w + 4);
+    uint32_t w8 = w[8];
+    const bool odd = (a & 3) != 0;
+    r.s = (float)__builtin_bit_cast(_Float16, (uint16_t)(odd ? (w0.x >> 16) : (w0.x & 0xFFFFu)));
+    r.sh = odd ? 0u : 2u;
+    r.q = odd ? (u32x4){w0.y, w0.z, w0.w, w1.x} : w0;
+    r.q8b = odd ? (u32x4){w1.y, w1.z, w1.w, w8} : w1;
+    r.q8c = w8;
   }
   r.s = ok ? r.s : 0.f;
   r.z = ok ? r.z : 0.f;
@@ -569,49 +577,9 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   const uint32_t gw = gb + wk * GPW;
   const uint32_t ksplit = gridDim.y;
 
-  // 1. weights first: every record of this wave, all loads in flight
-  Rec<FMT> wr[S][CT];
-  if (FMT == FMT_Q40T && n0 + 16 * CT <= N && gw + 4 * S <= G) {
-    // interior wave of the tile-major layout: one base address, the records
-    // of step st / tile ct at fixed offsets (1 KB per step of 4 groups)
-    const size_t rec0 = ((size_t)(n0 >> 4) * G + gw + j) * 16 + c;
-    const uint8_t* pb = B + rec0 * 16;
-    const uint16_t* pd = D + rec0;
-#pragma unroll
-    for (int st = 0; st < S; st++)
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++) {
-        wr[st][ct].q = *(const u32x4*)(pb + (size_t)ct * G * 256 + st * 1024);
-        wr[st][ct].s = (float)__builtin_bit_cast(_Float16, pd[(size_t)ct * G * 16 + st * 64]);
-        wr[st][ct].z = 0.f;
-        wr[st][ct].sh = 0;
-      }
-  } else {
-#pragma unroll
-    for (int st = 0; st < S; st++)
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
-  }
-
-  // 2. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
-  //    that consumes it): every workgroup sums x^2 over its rows' full K
-  float nss[MR];
-#pragma unroll
-  for (int m = 0; m < MR; m++) nss[m] = 0.f;
-  if (gamma) {
-    // K % 32 == 0 on this path: float4 loads, all of a thread's issued together
-#pragma unroll
-    for (int m = 0; m < MR; m++)
-      if ((uint32_t)m < M) {
-        const float4* ar = (const float4*)(A + (size_t)m * K);
-        for (uint32_t i = threadIdx.x; i < K / 4; i += NT) {
-          float4 v = ar[i];
-          nss[m] = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, nss[m]))));
-        }
-      }
-  }
-
-  // 3. activation loads (small, cache resident), with the RMSNorm gammas
+  // 1. activation loads (small, cache resident) and the RMSNorm gammas go out
+  //    BEFORE the weights: vector loads complete in order, so the prep below
+  //    then waits only for these, not for the weight records behind them
   const int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
   const int perm_q8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
   const float off_q4[8] = {1024.f, 1024.f, 64.f, 64.f, 1024.f, 1024.f, 64.f, 64.f};
@@ -648,6 +616,48 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
         av[cc][e] = (ch < (uint32_t)NCH && m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
       }
     }
+  }
+
+  // 2. weights: every record of this wave, all loads in flight
+  Rec<FMT> wr[S][CT];
+  if (FMT == FMT_Q40T && n0 + 16 * CT <= N && gw + 4 * S <= G) {
+    // interior wave of the tile-major layout: one base address, the records
+    // of step st / tile ct at fixed offsets (1 KB per step of 4 groups)
+    const size_t rec0 = ((size_t)(n0 >> 4) * G + gw + j) * 16 + c;
+    const uint8_t* pb = B + rec0 * 16;
+    const uint16_t* pd = D + rec0;
+#pragma unroll
+    for (int st = 0; st < S; st++)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        wr[st][ct].q = *(const u32x4*)(pb + (size_t)ct * G * 256 + st * 1024);
+        wr[st][ct].s = (float)__builtin_bit_cast(_Float16, pd[(size_t)ct * G * 16 + st * 64]);
+        wr[st][ct].z = 0.f;
+        wr[st][ct].sh = 0;
+      }
+  } else {
+#pragma unroll
+    for (int st = 0; st < S; st++)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+  }
+
+  // 3. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
+  //    that consumes it): every workgroup sums x^2 over its rows' full K
+  float nss[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) nss[m] = 0.f;
+  if (gamma) {
+    // K % 32 == 0 on this path: float4 loads, all of a thread's issued together
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+      if ((uint32_t)m < M) {
+        const float4* ar = (const float4*)(A + (size_t)m * K);
+        for (uint32_t i = threadIdx.x; i < K / 4; i += NT) {
+          float4 v = ar[i];
+          nss[m] = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, nss[m]))));
+        }
+      }
   }
 
   // 4. activations -> f16 hi/lo fragments + (C1, S) in LDS
@@ -862,11 +872,8 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   const uint32_t ksplit = gridDim.y;
   const uint32_t g0 = (blockIdx.y * WK + wk) * GPW;
 
-  Rec<FMT> wr[S][CT];
-#pragma unroll
-  for (int st = 0; st < S; st++)
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, g0 + 4 * st + j, n0 + ct * 16 + c);
+  // activation fragments first (small, L2 resident): loads complete in
+  // order, so the MFMAs of step st then wait only for the weights up to st
   u32x4 afr[S][4][RB];
   float4 cvv[S][4][RB][(VPL + 1) / 2];
 #pragma unroll
@@ -883,6 +890,12 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
         for (int h = 0; h < (VPL + 1) / 2; h++) cvv[st][t][rb][h] = cp[h];
       }
     }
+
+  Rec<FMT> wr[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, g0 + 4 * st + j, n0 + ct * 16 + c);
 
   f32x4 acc[CT][RB];
 #pragma unroll
