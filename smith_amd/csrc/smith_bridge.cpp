@@ -273,6 +273,52 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   return launch(c, name, dim3(gx, ksplit), dim3(nthreads), args);
 }
 
+// 2 < M <= 32 in one launch (smith_qgemv4_*): each workgroup converts its K
+// range of the activations into MFMA fragments in LDS.  64 columns per
+// block; 32 groups per block unless that leaves fewer than ~200 blocks.
+int qgemv4_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
+                 uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
+  const char* tag = fmt_tag(fmt);
+  const char* rows = M <= 8 ? "h8" : (M <= 16 ? "p16" : "p32");
+  if (ep.gamma) {
+    if (ensure(c, &c->normbuf, &c->normbuf_bytes, (size_t)M * K * sizeof(float))) return -1;
+    const float* pa = a;
+    const float* pg = ep.gamma;
+    void* py = c->normbuf;
+    uint32_t pr = M, pc = K;
+    float pe = ep.eps;
+    void* nargs[] = {&pa, &pg, &py, &pr, &pc, &pe};
+    if (launch(c, "smith_rmsnorm_rows", dim3(M), dim3(256), nargs)) return -1;
+    a = (const float*)c->normbuf;
+  }
+  static const int force_kb = [] {
+    const char* e = getenv("SMITH_QGEMV4_KB");
+    return e ? atoi(e) : 0;
+  }();
+  const uint32_t bc = 64;
+  const uint32_t gx = (N + bc - 1) / bc;
+  uint32_t kb = force_kb == 16 ? 16 : 32;
+  if (kb == 32 && (uint64_t)gx * ((G + 31) / 32) < 200) kb = 16;
+  const uint32_t ksplit = (G + kb - 1) / kb;
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_qgemv4_%s_%s_k%u", tag, rows, kb);
+  const float* pa = a;
+  const void* pB = B;
+  const void* pD = D;
+  float* pC = out;
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pM = M, pN = N, pK = K, pG = G;
+  const float* pR = ep.resid;
+  uint32_t pepi = ep.mode;
+  void* args[] = {&pa, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pK, &pG, &pR, &pepi};
+  return launch(c, name, dim3(gx, ksplit), dim3(512), args);
+}
+
 // M <= 2: the fused kernel (activation prep in LDS, whole records per lane,
 // K split across the waves of a block; a cross-block split only when one
 // block's 64/128 groups do not cover K).
@@ -389,8 +435,15 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
     float* om = out + (size_t)m0 * nout;
     Epi e = ep;
     if (e.resid) e.resid += (size_t)m0 * N;
+    // SMITH_QGEMV=3 / 4 forces one of the two M > 2 paths (comparisons)
+    static const int vq = [] {
+      const char* e = getenv("SMITH_QGEMV");
+      return e ? atoi(e) : 0;
+    }();
+    const bool v3 = vq == 3 || (vq != 4 && mc > 8);
     int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
-                     : qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G, e);
+                     : (v3 ? qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
+                           : qgemv4_chunk(c, fmt, am, B, D, om, mc, N, K, G, e));
     if (rc) return -1;
   }
   return 0;

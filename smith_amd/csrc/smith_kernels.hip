@@ -419,11 +419,23 @@ __device__ __forceinline__ void splitk_finish(float* __restrict__ ws, uint32_t* 
   }
   __syncthreads();
   if (!*s_last) return;
+  // partials summed in split order; the reads go out four at a time (one
+  // memory round trip per four splits instead of one per split)
+  auto rd = [&](uint32_t sp, uint32_t m, uint32_t n) {
+    return __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  };
   auto part = [&](uint32_t m, uint32_t n) {
     float v = 0.f;
-    for (uint32_t sp = 0; sp < ksplit; sp++)
-      v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    uint32_t sp = 0;
+    for (; sp + 4 <= ksplit; sp += 4) {
+      const float x0 = rd(sp, m, n), x1 = rd(sp + 1, m, n), x2 = rd(sp + 2, m, n), x3 = rd(sp + 3, m, n);
+      v += x0;
+      v += x1;
+      v += x2;
+      v += x3;
+    }
+    for (; sp < ksplit; sp++) v += rd(sp, m, n);
     return v;
   };
   if (epi == EPI_SWIGLU) {
@@ -1037,6 +1049,295 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   DEF_QGEMV3(smith_qgemv3_##TAG##_m16, FMT, 1, false, 4, 2, 1, 8, 1)      \
   DEF_QGEMV3(smith_qgemv3_##TAG##_m32, FMT, 2, false, 4, 2, 1, 8, 1)
 
+// ---------------------------------------------------------------------------
+// Batched decode GEMV for 2 < M <= 32 in ONE launch (activation prep fused).
+//
+// Workgroup (column block, K range): its 512 threads first load their share
+// of A[rows, K range] (before any weight load: loads complete in order), then
+// every wave issues all of its weight records (lane (c, j): the whole record
+// of column c in group g+j, as in qgemv1/qgemv3), then the activations become
+// MFMA A fragments in LDS -- virtual rows as in smith_qprep (hi/lo for M <= 8,
+// plain f16 otherwise; per group and row C1 = sum(a*offset) (+8S for Q4_0)
+// and S = sum(a)) -- shared by all waves of the block.  Per step a wave
+// transposes its four records' dwords across lane groups (xpose4) into the
+// K-slice B layout, so one v_mfma_f32_16x16x32_f16 per (group, row block)
+// covers 16 columns x 16 virtual rows; the per-column scale / zero of the four
+// groups reach every lane through the same transpose.  WK waves split the
+// block's K range (LDS reduction); K splits across workgroups use the
+// deterministic split-K finish.
+// Grid: x = column blocks of 16*CT*WN, y = K splits of 4*S*WK groups.
+// ---------------------------------------------------------------------------
+template <int FMT, int RB, bool HILO, int CT, int S, int WK, int WN>
+__device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                            const uint16_t* __restrict__ D, float* __restrict__ C,
+                                            float* __restrict__ ws, uint32_t* __restrict__ counters,
+                                            uint32_t M, uint32_t N, uint32_t K, uint32_t G,
+                                            const float* __restrict__ R, uint32_t epi) {
+  constexpr int GPW = 4 * S;               // groups per wave
+  constexpr int KB = GPW * WK;             // groups per block
+  constexpr int BC = 16 * CT * WN;         // block columns
+  constexpr int NT = 64 * WK * WN;         // threads
+  constexpr int RPB = HILO ? 8 : 16;       // real rows per row block
+  constexpr int NITEM = KB * RB * RPB * 4; // prep items (group, rb, row, kslice), kslice fastest
+  constexpr int IPT = (NITEM + NT - 1) / NT;
+  static_assert(NT % 4 == 0, "prep items of one (group, row) must share a quad of lanes");
+  __shared__ u32x4 fragL[KB][RB][64];
+  __shared__ float4 cstL[KB][RB][8];       // (C1, S) of virtual rows 2q, 2q+1
+  __shared__ int s_last;
+  // the wave partials reuse the fragment area once every wave is past its MFMAs
+  static_assert(sizeof(float) * WK * RB * 16 * BC <= sizeof(fragL), "reduction area");
+  float(*red)[RB][16][BC] = reinterpret_cast<float(*)[RB][16][BC]>(&fragL[0][0][0]);
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wk = wave / WN, wn = wave % WN;
+  const uint32_t c = lane & 15, j = lane >> 4;
+  const uint32_t n0 = blockIdx.x * BC + wn * 16 * CT;
+  const uint32_t gb = blockIdx.y * KB;
+  const uint32_t gw = gb + wk * GPW;
+  const uint32_t ksplit = gridDim.y;
+
+  // 1. activation loads of this block's K range
+  float av[IPT][8];
+#pragma unroll
+  for (int it = 0; it < IPT; it++) {
+    const uint32_t item = threadIdx.x + it * NT;
+    const uint32_t kq = item & 3, rest = item >> 2;
+    const uint32_t r = rest % RPB, rb = (rest / RPB) % RB, gl = rest / (RPB * RB);
+    const uint32_t m = rb * RPB + r;
+    const uint32_t k0 = (gb + gl) * 32 + 8 * kq;
+    const bool live = item < (uint32_t)NITEM && m < M;
+    if (live && k0 + 8 <= K) {
+      const float4* ap = (const float4*)(A + (size_t)m * K + k0);
+      float4 x0 = ap[0], x1 = ap[1];
+      av[it][0] = x0.x; av[it][1] = x0.y; av[it][2] = x0.z; av[it][3] = x0.w;
+      av[it][4] = x1.x; av[it][5] = x1.y; av[it][6] = x1.z; av[it][7] = x1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) av[it][e] = (live && k0 + e < K) ? A[(size_t)m * K + k0 + e] : 0.f;
+    }
+  }
+
+  // 2. weight records of this wave, all loads in flight
+  Rec<FMT> wr[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+
+  // 3. activations -> f16 fragments and (C1, S) in LDS
+  {
+    const int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    const int perm_q8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    const float off_q4[8] = {1024.f, 1024.f, 64.f, 64.f, 1024.f, 1024.f, 64.f, 64.f};
+    const float fold = is_q40(FMT) ? 8.0f : 0.0f;
+    float* cst1 = (float*)&cstL[0][0][0];
+#pragma unroll
+    for (int it = 0; it < IPT; it++) {
+      const uint32_t item = threadIdx.x + it * NT;
+      const uint32_t kq = item & 3, rest = item >> 2;
+      const uint32_t r = rest % RPB, rb = (rest / RPB) % RB, gl = rest / (RPB * RB);
+      float c1h = 0.f, sh_ = 0.f, c1l = 0.f, sl = 0.f;
+      _Float16 hv[8], lv[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int el = FMT == FMT_Q8 ? perm_q8[e] : perm_q4[e];
+        const float off = FMT == FMT_Q8 ? 1152.f : off_q4[e];
+        const float a = av[it][el];
+        const _Float16 h = (_Float16)a;
+        const float hf = (float)h;
+        hv[e] = h;
+        c1h = __builtin_fmaf(hf, off, c1h);
+        sh_ += hf;
+        if (HILO) {
+          const _Float16 l = (_Float16)((a - hf) * 2048.0f);
+          const float lf = (float)l;
+          lv[e] = l;
+          c1l = __builtin_fmaf(lf, off, c1l);
+          sl += lf;
+        }
+      }
+#pragma unroll
+      for (int d = 1; d < 4; d <<= 1) {
+        c1h += __shfl_xor(c1h, d);
+        sh_ += __shfl_xor(sh_, d);
+        if (HILO) {
+          c1l += __shfl_xor(c1l, d);
+          sl += __shfl_xor(sl, d);
+        }
+      }
+      if (item < (uint32_t)NITEM) {
+        u32x4 hp, lp;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          hp[q] = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){hv[2 * q], hv[2 * q + 1]});
+          if (HILO)
+            lp[q] = __builtin_bit_cast(uint32_t, (_Float16 __attribute__((ext_vector_type(2)))){lv[2 * q], lv[2 * q + 1]});
+        }
+        fragL[gl][rb][r + 16 * kq] = hp;
+        if (HILO) fragL[gl][rb][r + 8 + 16 * kq] = lp;
+        float* cp = cst1 + ((size_t)gl * RB + rb) * 32;  // 16 virtual rows x (C1, S)
+        if (kq == 0) {
+          cp[2 * r] = __builtin_fmaf(fold, sh_, c1h);
+          cp[2 * r + 1] = sh_;
+        }
+        if (HILO && kq == 1) {
+          cp[2 * (r + 8)] = __builtin_fmaf(fold, sl, c1l);
+          cp[2 * (r + 8) + 1] = sl;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. MFMAs: per step, the four groups' records transposed into K slices
+  f32x4 acc[CT][RB];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const uint32_t gl0 = wk * GPW + 4 * st;
+    half8 af[4][RB];
+    float4 cv[4][RB][2];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) {
+        af[t][rb] = __builtin_bit_cast(half8, fragL[gl0 + t][rb][lane]);
+        cv[t][rb][0] = cstL[gl0 + t][rb][2 * j];
+        cv[t][rb][1] = cstL[gl0 + t][rb][2 * j + 1];
+      }
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      const Rec<FMT>& rr = wr[st][ct];
+      half8 bf[4];
+      if (FMT == FMT_Q8) {
+        uint32_t d[9] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w, rr.q8b.x, rr.q8b.y, rr.q8b.z, rr.q8b.w, rr.q8c};
+        uint32_t e[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) e[q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], rr.sh);
+        xpose4(e[0], e[2], e[4], e[6]);
+        xpose4(e[1], e[3], e[5], e[7]);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          uint32_t x0 = e[2 * t] ^ 0x80808080u, x1 = e[2 * t + 1] ^ 0x80808080u;
+          u32x4 u;
+          u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);
+          u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);
+          u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);
+          u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);
+          bf[t] = __builtin_bit_cast(half8, u);
+        }
+      } else {
+        uint32_t x[4] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w};
+        xpose4(x[0], x[1], x[2], x[3]);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const uint32_t y = x[t] >> 8;
+          u32x4 u;
+          u.x = bfi(0x000F000Fu, x[t], 0x64006400u);
+          u.y = bfi(0x00F000F0u, x[t], 0x54005400u);
+          u.z = bfi(0x000F000Fu, y, 0x64006400u);
+          u.w = bfi(0x00F000F0u, y, 0x54005400u);
+          bf[t] = __builtin_bit_cast(half8, u);
+        }
+      }
+      // scale (and zero) of group t for this lane's column: register t after
+      // the same transpose of four copies
+      uint32_t sv[4] = {__float_as_uint(rr.s), __float_as_uint(rr.s), __float_as_uint(rr.s), __float_as_uint(rr.s)};
+      xpose4(sv[0], sv[1], sv[2], sv[3]);
+      uint32_t zv[4] = {0u, 0u, 0u, 0u};
+      if (FMT == FMT_Q4S) {
+        zv[0] = zv[1] = zv[2] = zv[3] = __float_as_uint(rr.z);
+        xpose4(zv[0], zv[1], zv[2], zv[3]);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const float s = __uint_as_float(sv[t]), z = __uint_as_float(zv[t]);
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+          const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bf[t], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const float4 c01 = cv[t][rb][0], c23 = cv[t][rb][1];
+          const float c1v[4] = {c01.x, c01.z, c23.x, c23.z}, sv4[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float tt = p[i] - c1v[i];
+            if (FMT == FMT_Q4S) tt = __builtin_fmaf(-z, sv4[i], tt);
+            acc[ct][rb][i] = __builtin_fmaf(s, tt, acc[ct][rb][i]);
+          }
+        }
+      }
+    }
+  }
+
+  // 5. the WK waves of the block in fixed order, then the epilogue or the
+  //    cross-block split
+  __syncthreads();
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[wk][rb][j * 4 + i][wn * 16 * CT + ct * 16 + c] = acc[ct][rb][i];
+  __syncthreads();
+  const uint32_t mrows = M < (uint32_t)(RB * RPB) ? M : RB * RPB;
+  const uint32_t nb = blockIdx.x * BC;
+  auto colsum = [&](uint32_t m, uint32_t cc) {
+    const uint32_t rb = m / RPB, rr = m % RPB;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WK; w++) {
+      if (HILO) v += red[w][rb][rr][cc] + red[w][rb][rr + 8][cc] * (1.0f / 2048.0f);
+      else v += red[w][rb][rr][cc];
+    }
+    return v;
+  };
+  if (ksplit == 1) {
+    if (epi == EPI_SWIGLU) {
+      for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
+        const uint32_t m = e / (BC / 2), cc = 2 * (e % (BC / 2)), n = nb + cc;
+        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(colsum(m, cc), colsum(m, cc + 1));
+      }
+    } else {
+      for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+        const uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+        if (n >= N) continue;
+        const float v = colsum(m, cc);
+        C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+      }
+    }
+    return;
+  }
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+    const uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+    if (n >= N) continue;
+    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(colsum(m, cc)),
+                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
+}
+
+#define DEF_QGEMV4(NAME, FMT, RB, HILO, CT, S, WK, WN)                                                  \
+  extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                       \
+      const float* A, const uint8_t* B, const uint16_t* D, float* C, float* ws, uint32_t* counters,      \
+      uint32_t M, uint32_t N, uint32_t K, uint32_t G, const float* R, uint32_t epi) {                    \
+    qgemv4_body<FMT, RB, HILO, CT, S, WK, WN>(A, B, D, C, ws, counters, M, N, K, G, R, epi);             \
+  }
+
+// Row buckets h8 (M <= 8, hi/lo), p16 (M <= 16), p32 (M <= 32, two row
+// blocks); k32 / k16 = groups per block (64 columns per block, 8 waves:
+// 2 along K x 4 along N).  (Blocks over all of K = 4096 with 16 columns lost:
+// every block then converts the whole activation, 11.7 vs 9.4 us at M = 4.)
+#define DEF_QGEMV4_FMT(TAG, FMT)                                         \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_h8_k32, FMT, 1, true, 1, 4, 2, 4)      \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_h8_k16, FMT, 1, true, 1, 2, 2, 4)      \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_p16_k32, FMT, 1, false, 1, 4, 2, 4)    \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_p16_k16, FMT, 1, false, 1, 2, 2, 4)    \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_p32_k32, FMT, 2, false, 1, 4, 2, 4)    \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_p32_k16, FMT, 2, false, 1, 2, 2, 4)
+
 
 // ---------------------------------------------------------------------------
 // Single-row decode GEMV on a prepared activation (act_frag.h) and Q4_0
@@ -1512,6 +1813,10 @@ DEF_QGEMV3_FMT(q4s, FMT_Q4S)
 DEF_QGEMV3_FMT(q8, FMT_Q8)
 DEF_QGEMV3_FMT(q40, FMT_Q40)
 DEF_QGEMV3_FMT(q40t, FMT_Q40T)
+DEF_QGEMV4_FMT(q4s, FMT_Q4S)
+DEF_QGEMV4_FMT(q8, FMT_Q8)
+DEF_QGEMV4_FMT(q40, FMT_Q40)
+DEF_QGEMV4_FMT(q40t, FMT_Q40T)
 DEF_QGEMV1_FMT(q4s, FMT_Q4S)
 DEF_QGEMV1_FMT(q8, FMT_Q8)
 DEF_QGEMV1_FMT(q40, FMT_Q40)
