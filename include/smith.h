@@ -201,10 +201,14 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
  * combination of its key splits to the output projection: parts receives,
  * per head and split, (m, l, pad, pad, o[head_dim]) in 132-float records
  * (n_heads * 8 * 132 floats); caches appended as smith_attention.
- * head_dim <= 128, % 32. */
+ * rope_row (may be NULL): 4 + n_heads*head_dim + n_kv_heads*head_dim floats
+ * that smith_argmax_embed fills with the cos / sin table entries of the next
+ * position (int32 tag = that position in the first word); when the tag is
+ * *pos_ptr the RoPE reads them instead of the table (one memory round trip
+ * less), otherwise the table.  head_dim <= 128, % 32. */
 int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, uint32_t n_heads, uint32_t n_kv_heads,
-                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, float* kcache,
-                          float* vcache, uint32_t max_seq, float* parts);
+                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, const float* rope_row,
+                          float* kcache, float* vcache, uint32_t max_seq, float* parts);
 /* smith_linear_q4_0_t_act whose input is smith_attention_parts' partials
  * (K = n_heads * head_dim; the splits are combined per head first). */
 int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_ptr, uint32_t head_dim,
@@ -273,9 +277,13 @@ int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps
                    uint32_t K, uint32_t N, int w_is_nk);
 /* greedy step on device: token = argmax(logits) (generate.js:70-76),
  * tokens[*count] = token, x = E[token], ++*count, ++*pos; with act_out also
- * the act of x times gamma_out. */
+ * the act of x times gamma_out.  With rope_row (may be NULL) also the rope
+ * row of the new position for smith_attention_parts (q rows wq wide, k rows
+ * wk wide; written only when the tables, rope_len entries each, reach it). */
 int smith_argmax_embed(void* ctx, const float* logits, uint32_t N, const float* E, uint32_t dim, float* x,
-                       int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out);
+                       int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out,
+                       const float* rope_cos, const float* rope_sin, uint32_t rope_len, uint32_t wq, uint32_t wk,
+                       float* rope_row);
 int smith_set_i32(void* ctx, int32_t* p, int32_t v);
 /* seeded N(mean, std) f32 stream (SplitMix64 + Box-Muller), offset even. */
 int smith_randn(void* ctx, float* out, uint64_t n, uint64_t seed, uint64_t offset, float stdv, float mean);

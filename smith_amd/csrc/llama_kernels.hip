@@ -509,56 +509,173 @@ DEF_ATT_PREFILL(8)
 // ---------------------------------------------------------------------------
 // Single-row decode attention writing per-split partials for the output
 // projection to combine (smith_agemv_att_*), so no workgroup of this kernel
-// waits for another.  Row position p0 = *pos_ptr, T = p0 + 1 keys, split
-// count nsplit = min(ATTP_MAXSPLIT, ceil(T / ATTP_ROWS)) decided on the
-// device (one captured grid serves every position; workgroups past nsplit
-// leave at once).  Workgroup (b, z): query head h of KV head b % nKV (the
-// rep query heads of a KV head get workgroup ids congruent mod nKV, i.e. the
-// same XCD when nKV is a multiple of 8, so they share its L2), key split z.
-// Math as smith_attention (RoPE'd q, 1/sqrt(hd) scores, online softmax over
-// 32-row K/V tiles staged in LDS); the partial (m, l, o[hd]) of (h, z) goes
-// to parts[(h*ATTP_MAXSPLIT + z)*ATTP_STRIDE ..] with plain stores.  The
-// (h % rep == 0, z == 0) workgroup appends the row's key/value to the caches.
+// waits for another.  Row position p0 = *pos_ptr, T = p0 + 1 keys in 32-row
+// tiles; split count nsplit = min(ATTP_MAXSPLIT, tiles) decided on the device
+// (one captured grid serves every position; workgroups past nsplit leave at
+// once); split z takes tiles z, z + ATTP_MAXSPLIT, ...  Workgroup (b, z):
+// query head h of KV head b % nKV (the rep query heads of a KV head get
+// workgroup ids congruent mod nKV, i.e. the same XCD when nKV is a multiple
+// of 8, so they share its L2), key split z.
+//
+// Everything that does not depend on the position is issued at once: the
+// split's first K/V tile from the caches (rows 32z .. 32z+31), the q row and
+// this KV head's new k / v (with their whole-row RoPE partners), the position
+// and the rope row -- cos / sin of the current position for the q and k row
+// widths, tagged with that position, written by the previous greedy step
+// (smith_argmax_embed) -- so one memory round trip feeds the split.  A rope
+// row of another position (or none) falls back to the table.  Cache rows
+// past p0 are zeroed in LDS (their weight is 0; the cache may hold anything
+// there) and row p0 is this token's roped k and v.  Math as smith_attention
+// (1/sqrt(hd) scores, online softmax over the tile); the partial (m, l, o[hd])
+// of (h, z) goes to parts[(h*ATTP_MAXSPLIT + z)*ATTP_STRIDE ..] with plain
+// stores.  The (h % rep == 0, z == 0) workgroup appends the row's key/value.
 // ---------------------------------------------------------------------------
 #define ATTP_ROWS 32
 #define ATTP_MAXSPLIT 8
 #define ATTP_STRIDE 132  // floats per partial: m, l, 2 pad, o[128] (16-byte aligned)
+#define ROPE_ROW_HDR 4   // rope row: int32 position tag, 3 pad, then cos_q, sin_q, cos_k, sin_k
 
 extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     const float* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, uint32_t nH, uint32_t nKV, uint32_t hd,
-    const float* __restrict__ cosT, const float* __restrict__ sinT, float* __restrict__ kcache,
-    float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts) {
+    const float* __restrict__ cosT, const float* __restrict__ sinT, const float* __restrict__ rrow,
+    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts) {
   __shared__ AttShared sh;
+  __shared__ float kn[128], vn[128];
   __shared__ float ored[2][128];
   const uint32_t rep = nH / nKV;
   const uint32_t kvh = blockIdx.x % nKV, h = kvh * rep + blockIdx.x / nKV, z = blockIdx.y;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t p0 = (uint32_t)pos_ptr[0];
-  const uint32_t T = p0 + 1;
-  uint32_t nsplit = (T + ATTP_ROWS - 1) / ATTP_ROWS;
-  nsplit = nsplit < ATTP_MAXSPLIT ? nsplit : ATTP_MAXSPLIT;
-  if (z >= nsplit) return;
-  const uint32_t Wq = nH * hd, Wk = nKV * hd;
+  const uint32_t tid = threadIdx.x, c4n = hd / 4;
+  const uint32_t Wq = nH * hd, Wk = nKV * hd, hq = Wq / 2, hk = Wk / 2;
   const float scale = 1.0f / __builtin_sqrtf((float)hd);
   const float* krow = qkv + Wq;
-  const uint32_t per = (T + nsplit - 1) / nsplit;
-  const uint32_t t0 = z * per, t1 = t0 + per < T ? t0 + per : T;
-  const uint32_t e = tid % 128, part = tid / 128;
-  float m, l, o;
-  att_split<true>(sh, kcache + (size_t)kvh * maxSeq * hd, vcache + (size_t)kvh * maxSeq * hd, krow, 0, Wk, kvh, hd, p0, t0,
-            t1, cosT, sinT, scale,
-            [&]() {
-              for (uint32_t e2 = tid; e2 < hd; e2 += 256) sh.qr[e2] = rope_elem(qkv, Wq, h * hd + e2, p0, cosT, sinT);
-              if (h % rep == 0 && z == 0) {
-                for (uint32_t e2 = tid; e2 < hd; e2 += 256) {
-                  size_t oo = ((size_t)kvh * maxSeq + p0) * hd + e2;
-                  kcache[oo] = rope_elem(krow, Wk, kvh * hd + e2, p0, cosT, sinT);
-                  vcache[oo] = krow[Wk + kvh * hd + e2];
-                }
-              }
-            },
-            m, l, o);
-  if (e < hd) ored[part][e] = o;
+  const float* kb = kcache + (size_t)kvh * maxSeq * hd;
+  const float* vb = vcache + (size_t)kvh * maxSeq * hd;
+
+  // 1. loads that need no position
+  const int32_t p0i = pos_ptr[0];
+  const int32_t tag = rrow ? *(const int32_t*)rrow : -1;
+  float4 kreg[4], vreg[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t idx = tid + 256 * i, r = idx / c4n, c4 = idx % c4n;
+    uint32_t t = ATTP_ROWS * z + (r < ATTP_ROWS ? r : ATTP_ROWS - 1);
+    t = t < maxSeq ? t : maxSeq - 1;
+    kreg[i] = *(const float4*)(kb + (size_t)t * hd + 4 * c4);
+    vreg[i] = *(const float4*)(vb + (size_t)t * hd + 4 * c4);
+  }
+  const uint32_t e = tid < hd ? tid : 0;
+  const uint32_t iq = h * hd + e, pq = iq < hq ? iq : iq - hq;
+  const uint32_t ik = kvh * hd + e, pk = ik < hk ? ik : ik - hk;
+  const float q0 = qkv[pq], q1 = qkv[pq + hq];
+  const float k0 = krow[pk], k1 = krow[pk + hk];
+  const float vnew = krow[Wk + ik];
+  float cq = 0.f, sq = 0.f, ck = 0.f, sk = 0.f;
+  if (rrow) {
+    cq = rrow[ROPE_ROW_HDR + pq];
+    sq = rrow[ROPE_ROW_HDR + hq + pq];
+    ck = rrow[ROPE_ROW_HDR + Wq + pk];
+    sk = rrow[ROPE_ROW_HDR + Wq + hk + pk];
+  }
+
+  // 2. the position: split count, RoPE of q and of the new k (rope_elem's
+  //    whole-row pairing), the cache append
+  const uint32_t p0 = (uint32_t)p0i, T = p0 + 1;
+  const uint32_t ntile = (T + ATTP_ROWS - 1) / ATTP_ROWS;
+  const uint32_t nsplit = ntile < ATTP_MAXSPLIT ? ntile : ATTP_MAXSPLIT;
+  if (z >= nsplit) return;
+  if (tag != p0i) {
+    cq = cosT[(size_t)p0 * hq + pq];
+    sq = sinT[(size_t)p0 * hq + pq];
+    ck = cosT[(size_t)p0 * hk + pk];
+    sk = sinT[(size_t)p0 * hk + pk];
+  }
+  if (tid < hd) {
+    sh.qr[tid] = iq < hq ? q0 * cq - q1 * sq : q0 * sq + q1 * cq;
+    const float kr = ik < hk ? k0 * ck - k1 * sk : k0 * sk + k1 * ck;
+    kn[tid] = kr;
+    vn[tid] = vnew;
+    if (h % rep == 0 && z == 0) {
+      const size_t oo = ((size_t)kvh * maxSeq + p0) * hd + tid;
+      kcache[oo] = kr;
+      vcache[oo] = vnew;
+    }
+  }
+
+  // 3. the split's tiles
+  const uint32_t ee = tid % 128, part = tid / 128;
+  float m = -__builtin_inff(), l = 0.f, o = 0.f;
+  __syncthreads();  // qr, kn, vn visible
+  for (uint32_t tau = z; tau < ntile; tau += ATTP_MAXSPLIT) {
+    const uint32_t tb = ATTP_ROWS * tau;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t idx = tid + 256 * i, r = idx / c4n, c4 = idx % c4n;
+      if (r < ATTP_ROWS) {
+        const uint32_t t = tb + r;
+        float4 kv = kreg[i], vv = vreg[i];
+        if (t > p0) kv = vv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t == p0) {
+          kv = make_float4(kn[4 * c4], kn[4 * c4 + 1], kn[4 * c4 + 2], kn[4 * c4 + 3]);
+          vv = make_float4(vn[4 * c4], vn[4 * c4 + 1], vn[4 * c4 + 2], vn[4 * c4 + 3]);
+        }
+        sh.Kt[r][4 * c4] = kv.x;
+        sh.Kt[r][4 * c4 + 1] = kv.y;
+        sh.Kt[r][4 * c4 + 2] = kv.z;
+        sh.Kt[r][4 * c4 + 3] = kv.w;
+        *(float4*)&sh.Vt[r][4 * c4] = vv;
+      }
+    }
+    __syncthreads();
+    if (tau + ATTP_MAXSPLIT < ntile) {  // the split's next tile in flight during this one
+      const uint32_t tn = tb + ATTP_ROWS * ATTP_MAXSPLIT;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t idx = tid + 256 * i, r = idx / c4n, c4 = idx % c4n;
+        uint32_t t = tn + (r < ATTP_ROWS ? r : ATTP_ROWS - 1);
+        t = t < maxSeq ? t : maxSeq - 1;
+        kreg[i] = *(const float4*)(kb + (size_t)t * hd + 4 * c4);
+        vreg[i] = *(const float4*)(vb + (size_t)t * hd + 4 * c4);
+      }
+    }
+    {
+      const uint32_t r = tid / 8, sub = tid % 8;
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint32_t c = sub + 8 * i;
+        if (c < hd) d = __builtin_fmaf(sh.qr[c], sh.Kt[r][c], d);
+      }
+      d += __shfl_xor(d, 1);
+      d += __shfl_xor(d, 2);
+      d += __shfl_xor(d, 4);
+      if (sub == 0) sh.sc[r] = tb + r <= p0 ? d * scale : -__builtin_inff();
+    }
+    __syncthreads();
+    const float sl = sh.sc[tid & 31];
+    float tm = sl;
+#pragma unroll
+    for (int k = 16; k >= 1; k >>= 1) {
+      const float ov = __shfl_xor(tm, k);
+      tm = ov > tm ? ov : tm;
+    }
+    const float mn = tm > m ? tm : m;
+    const float alpha = __expf(m - mn);  // first tile: m = -inf -> 0
+    const float pl = __expf(sl - mn);    // masked rows: exp(-inf) = 0
+    float ps = pl;
+#pragma unroll
+    for (int k = 16; k >= 1; k >>= 1) ps += __shfl_xor(ps, k);
+    float acc = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < ATTP_ROWS / 2; rr++) {
+      const uint32_t row = 2 * rr + part;
+      acc = __builtin_fmaf(__shfl(pl, (int)row), sh.Vt[row][ee < hd ? ee : 0], acc);
+    }
+    l = l * alpha + ps;
+    o = o * alpha + acc;
+    m = mn;
+    __syncthreads();
+  }
+  if (ee < hd) ored[part][ee] = o;
   __syncthreads();
   float* pp = parts + ((size_t)h * ATTP_MAXSPLIT + z) * ATTP_STRIDE;
   if (tid < hd) pp[4 + tid] = ored[0][tid] + ored[1][tid];
@@ -810,38 +927,53 @@ extern "C" __global__ __launch_bounds__(256) void smith_gemv_f32_nk(const float*
 // ---------------------------------------------------------------------------
 // Greedy step on device: token = argmax(logits) (generate.js:70-76: the
 // first maximum wins), tokens[*count] = token, x = E[token], then *count and
-// *pos advance.  One workgroup of 1024 threads.
+// *pos advance.  With rrow, the rope row of the new position (cos / sin of
+// the table rows the whole-row RoPE of a q row (wq wide) and a k row (wk
+// wide) reads, tag = the position) is written for the next decode step's
+// attention, if the tables (rope_len entries each) reach that far.  One workgroup of 1024 threads;
+// every thread's logits loads go out together with the count / position
+// loads, so the only dependent round trip is the embedding row.
 // ---------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(const float* __restrict__ logits, uint32_t N,
-                                                                      const float* __restrict__ E, uint32_t dim,
-                                                                      float* __restrict__ x,
-                                                                      int32_t* __restrict__ tokens,
-                                                                      int32_t* __restrict__ count,
-                                                                      int32_t* __restrict__ pos,
-                                                                      uint8_t* __restrict__ act_out,
-                                                                      const float* __restrict__ gamma_out) {
+#define AMX_BATCH 32
+extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(
+    const float* __restrict__ logits, uint32_t N, const float* __restrict__ E, uint32_t dim, float* __restrict__ x,
+    int32_t* __restrict__ tokens, int32_t* __restrict__ count, int32_t* __restrict__ pos,
+    uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out, const float* __restrict__ cosT,
+    const float* __restrict__ sinT, uint32_t rope_len, uint32_t wq, uint32_t wk, float* __restrict__ rrow) {
   __shared__ float bv[16];
   __shared__ int32_t bi[16];
   __shared__ int32_t s_tok;
+  const int32_t c0 = count[0], p = pos[0];
   float best = -__builtin_inff();
   int32_t bidx = 0x7fffffff;
-  // thread t scans indices t, t + 1024, ... in increasing order, 8 loads in
-  // flight per batch
-  for (uint32_t i0 = threadIdx.x; i0 < N; i0 += 8 * 1024) {
-    float v[8];
+  // thread t scans indices t, t + 1024, ... in increasing order
+  for (uint32_t i0 = threadIdx.x; i0 < N; i0 += AMX_BATCH * 1024) {
+    float v[AMX_BATCH];
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < AMX_BATCH; u++) {
       const uint32_t i = i0 + 1024 * u;
       v[u] = logits[i < N ? i : N - 1];
     }
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < AMX_BATCH; u++) {
       const uint32_t i = i0 + 1024 * u;
       if (i < N && v[u] > best) {  // strictly greater: earliest index within this thread
         best = v[u];
         bidx = (int32_t)i;
       }
     }
+  }
+  // the next position's rope row (independent of the token)
+  const uint32_t np = (uint32_t)p + 1, hq = wq / 2, hk = wk / 2;
+  if (rrow && (size_t)(np + 1) * hq <= rope_len && (size_t)(np + 1) * hk <= rope_len) {
+    for (uint32_t i = threadIdx.x; i < hq + hk; i += 1024) {
+      const size_t t = i < hq ? (size_t)np * hq + i : (size_t)np * hk + (i - hq);
+      const uint32_t o = i < hq ? ROPE_ROW_HDR + i : ROPE_ROW_HDR + wq + (i - hq);
+      const uint32_t half = i < hq ? hq : hk;
+      rrow[o] = cosT[t];
+      rrow[o + half] = sinT[t];
+    }
+    if (threadIdx.x == 0) *(int32_t*)rrow = (int32_t)np;
   }
   for (int d = 32; d >= 1; d >>= 1) {
     float ov = __shfl_xor(best, d);
@@ -866,9 +998,8 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(const floa
       }
     if (t == 0x7fffffff) t = 0;  // all NaN: the reference's argmax returns 0
     s_tok = t;
-    int32_t c = count[0];
-    tokens[c] = t;
-    count[0] = c + 1;
+    tokens[c0] = t;
+    count[0] = c0 + 1;
   }
   __syncthreads();
   const int32_t t = s_tok;
@@ -877,8 +1008,7 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(const floa
     x[i] = v;
     if (act_out) act_emit8(act_out, dim, i, v, gamma_out ? gamma_out[i] : 1.0f);  // dim % 32 == 0
   }
-  __syncthreads();
-  if (threadIdx.x == 0) pos[0] = pos[0] + 1;
+  if (threadIdx.x == 0) pos[0] = (int32_t)np;
 }
 
 // Set a device int (graph-capturable replacement for a tiny H2D copy).

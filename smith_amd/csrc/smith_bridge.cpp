@@ -1280,8 +1280,8 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
 }
 
 int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, uint32_t n_heads, uint32_t n_kv_heads,
-                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, float* kcache,
-                          float* vcache, uint32_t max_seq, float* parts) {
+                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, const float* rope_row,
+                          float* kcache, float* vcache, uint32_t max_seq, float* parts) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
   if (!n_kv_heads || n_heads % n_kv_heads)
@@ -1289,7 +1289,9 @@ int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, u
   if (head_dim > 128 || head_dim % 32)
     return fail(c, "smith_attention_parts: head_dim %u unsupported (<= 128, %% 32)", head_dim);
   if (set_device(c)) return -1;
-  void* args[] = {&qkv, &pos_ptr, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
+  if ((n_heads * head_dim) % 2 || (n_kv_heads * head_dim) % 2)
+    return fail(c, "smith_attention_parts: q / k row widths must be even (RoPE pairs)");
+  void* args[] = {&qkv, &pos_ptr, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &rope_row,
                   &kcache, &vcache, &max_seq, &parts};
   return launch(c, "smith_attention_part", dim3(n_heads, 8), dim3(256), args);  // ATTP_MAXSPLIT splits
 }
@@ -1541,12 +1543,17 @@ int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps
 }
 
 int smith_argmax_embed(void* ctx, const float* logits, uint32_t N, const float* E, uint32_t dim, float* x,
-                       int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out) {
+                       int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out,
+                       const float* rope_cos, const float* rope_sin, uint32_t rope_len, uint32_t wq, uint32_t wk,
+                       float* rope_row) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
   if (act_out && dim % 32) return fail(c, "smith_argmax_embed: an act output needs dim %% 32 == 0 (dim %u)", dim);
   if (set_device(c)) return -1;
-  void* args[] = {&logits, &N, &E, &dim, &x, &tokens, &count, &pos, &act_out, &gamma_out};
+  if (rope_row && (!rope_cos || !rope_sin || wq % 2 || wk % 2))
+    return fail(c, "smith_argmax_embed: a rope row needs both tables and even row widths");
+  void* args[] = {&logits, &N, &E, &dim, &x, &tokens, &count, &pos, &act_out, &gamma_out,
+                  &rope_cos, &rope_sin, &rope_len, &wq, &wk, &rope_row};
   return launch(c, "smith_argmax_embed", dim3(1), dim3(1024), args);
 }
 

@@ -89,6 +89,10 @@ class _Engine:
         self.use_parts = self.use_act and hd % 32 == 0 and hd <= 128
         if self.use_parts:
             self.att_parts = DeviceArray((cfg["numHeads"] * 8 * 132,))
+            # cos / sin of the current decode position, written by the greedy
+            # step for the next one (tag -1: none yet, the attention reads the table)
+            self.rope_row = DeviceArray((4 + cfg["numHeads"] * hd + cfg["numKVHeads"] * hd,))
+            device.check(device.lib.smith_set_i32(device.ops_ctx(), self.rope_row.ptr, -1), "rope row")
 
     def set_pos(self, p):
         device.check(device.lib.smith_set_i32(device.ops_ctx(), self.pos.ptr, int(p)), "set_pos")
@@ -126,7 +130,8 @@ class _Engine:
                 parts = self.att_parts.ptr
                 device.check(device.lib.smith_attention_parts(
                     ctx, qkv, self.pos.ptr, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"], rope["cos"].ptr,
-                    rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], parts), "attention")
+                    rope["sin"].ptr, self.rope_row.ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], parts),
+                    "attention")
                 blk["outProj"].attn(parts, self.pos.ptr, cfg["headDim"], x2, x, 1, ax2, blk["ln2Gamma"].ptr)
             else:
                 device.check(device.lib.smith_attention(
@@ -168,9 +173,13 @@ class _Engine:
     def greedy_step(self, model):
         cfg = self.cfg
         a0, g0 = self._act0(model)
+        rope, hd = model["rope"], cfg["headDim"]
+        rr = self.rope_row.ptr if self.use_parts else None
         device.check(device.lib.smith_argmax_embed(device.ops_ctx(), self.logits.ptr, cfg["vocabSize"],
                                                    self.model_embedding, cfg["dim"], self.x.ptr, self.tokens.ptr,
-                                                   self.count.ptr, self.pos.ptr, a0, g0), "argmax")
+                                                   self.count.ptr, self.pos.ptr, a0, g0, rope["cos"].ptr,
+                                                   rope["sin"].ptr, rope["cos"].shape[0], cfg["numHeads"] * hd,
+                                                   cfg["numKVHeads"] * hd, rr), "argmax")
 
     def embed(self, model, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
