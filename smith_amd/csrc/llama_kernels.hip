@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #include "act_frag.h"
+#include "splitk.h"
 #include "gguf_tiles.h"
 
 // ---------------------------------------------------------------------------
@@ -838,11 +839,7 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
   __syncthreads();
   if (!s_last) return;
   if (n < N) {
-    float t = 0.f;
-    for (uint32_t sp = 0; sp < ksplit; sp++)
-      t += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n, 0u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT));
-    y[n] = t;
+    y[n] = splitk_sum(ws + n, N, ksplit);
   }
   if (threadIdx.x == 0)
     __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1202,11 +1199,7 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
   __syncthreads();
   if (!s_last) return;
   if (n < N) {
-    float t = 0.f;
-    for (uint32_t sp = 0; sp < ksplit; sp++)
-      t += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n, 0u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT));
-    y[n] = t;
+    y[n] = splitk_sum(ws + n, N, ksplit);
   }
   if (threadIdx.x == 0)
     __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -38,6 +38,7 @@
 #include <stdint.h>
 
 #include "act_frag.h"
+#include "splitk.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -419,25 +420,7 @@ __device__ __forceinline__ void splitk_finish(float* __restrict__ ws, uint32_t* 
   }
   __syncthreads();
   if (!*s_last) return;
-  // partials summed in split order; the reads go out four at a time (one
-  // memory round trip per four splits instead of one per split)
-  auto rd = [&](uint32_t sp, uint32_t m, uint32_t n) {
-    return __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + ((size_t)sp * M + m) * N + n, 0u,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  };
-  auto part = [&](uint32_t m, uint32_t n) {
-    float v = 0.f;
-    uint32_t sp = 0;
-    for (; sp + 4 <= ksplit; sp += 4) {
-      const float x0 = rd(sp, m, n), x1 = rd(sp + 1, m, n), x2 = rd(sp + 2, m, n), x3 = rd(sp + 3, m, n);
-      v += x0;
-      v += x1;
-      v += x2;
-      v += x3;
-    }
-    for (; sp < ksplit; sp++) v += rd(sp, m, n);
-    return v;
-  };
+  auto part = [&](uint32_t m, uint32_t n) { return splitk_sum(ws + (size_t)m * N + n, (size_t)M * N, ksplit); };
   if (epi == EPI_SWIGLU) {
     for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
       uint32_t m = e / (BC / 2), n = nb + 2 * (e % (BC / 2));
@@ -1693,9 +1676,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     if (prev != ksplit - 1) return;
     v = 0.f;
     if (lane < BC && n0 + lane < N)
-      for (uint32_t sp = 0; sp < ksplit; sp++)
-        v += __uint_as_float(__hip_atomic_fetch_add((uint32_t*)ws + (size_t)sp * N + n0 + lane, 0u,
-                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      v = splitk_sum(ws + n0 + lane, N, ksplit);
     if (lane == 0) __hip_atomic_exchange(counters + bx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (norm)
       for (uint32_t t = lane; t < T; t += 64) ssum += c1p[2 * T + t];
