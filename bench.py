@@ -30,9 +30,9 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 400 << 20
 # HBM bytes per config-1 GEMV launch from two rocprofv3 --pmc passes
-# (the committed qgemv1 config-1 HBM traffic profile): FETCH_SIZE 6251.5 KiB x 1.996
+# (the committed qgemv1 config-1 HBM traffic profile): FETCH_SIZE 6273.5 KiB x 1.996
 # (factor from a 12,582,912 B device copy) + WRITE_SIZE 16.0 KiB x 1.0.
-TRAFFIC_CFG1 = 12793900
+TRAFFIC_CFG1 = 12838686
 
 
 def log(*a):
