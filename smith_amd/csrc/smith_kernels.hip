@@ -1064,12 +1064,13 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
   constexpr int NITEM = KB * RB * RPB * 4; // prep items (group, rb, row, kslice), kslice fastest
   constexpr int IPT = (NITEM + NT - 1) / NT;
   static_assert(NT % 4 == 0, "prep items of one (group, row) must share a quad of lanes");
-  __shared__ u32x4 fragL[KB][RB][64];
+  // the wave partials reuse the fragment area once every wave is past its MFMAs
+  constexpr size_t FRAG_BYTES = sizeof(u32x4) * KB * RB * 64, RED_BYTES = sizeof(float) * WK * RB * 16 * BC;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[FRAG_BYTES > RED_BYTES ? FRAG_BYTES : RED_BYTES];
   __shared__ float4 cstL[KB][RB][8];       // (C1, S) of virtual rows 2q, 2q+1
   __shared__ int s_last;
-  // the wave partials reuse the fragment area once every wave is past its MFMAs
-  static_assert(sizeof(float) * WK * RB * 16 * BC <= sizeof(fragL), "reduction area");
-  float(*red)[RB][16][BC] = reinterpret_cast<float(*)[RB][16][BC]>(&fragL[0][0][0]);
+  u32x4(*fragL)[RB][64] = reinterpret_cast<u32x4(*)[RB][64]>(smem);
+  float(*red)[RB][16][BC] = reinterpret_cast<float(*)[RB][16][BC]>(smem);
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
