@@ -268,13 +268,15 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
     store_stage(r0, 0);
   }
   __syncthreads();
-  for (uint32_t s = 0; s < S; s++) {
+  // steady state without guards (the last stage is peeled off)
+  for (uint32_t s = 0; s + 1 < S; s++) {
     const uint32_t buf = s & 1;
-    if (s + 1 < S) load_stage(r0, s0 + s + 1);
+    load_stage(r0, s0 + s + 1);
     mfma_stage(buf);
-    if (s + 1 < S) store_stage(r0, buf ^ 1);
+    store_stage(r0, buf ^ 1);
     __syncthreads();
   }
+  if (S > 0) mfma_stage((S - 1) & 1);
 
   // epilogue: lane (c = lane % 16, kq) holds rows 4kq .. 4kq+3 of column c of each tile
 #pragma unroll
