@@ -390,10 +390,19 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
   else if (ntiles(128, 128) >= 256) bm = 128, bn = 128;
   if (g2 && M <= 128) bn = ntiles(128, 128) >= 128 ? 128 : 64;
   if (g2 && bm == 256 && bn == 256) bn = 128;  // 256x256 spills registers on the high-bit formats
+  // M >= 256 on the register-staged kernel: 256x256 tiles (one 1024-thread
+  // workgroup per CU) and enough K splits to fill one wave of workgroups,
+  // each split at least 8 stages -- measured best at config 4 (M = 512:
+  // 123 -> 114 us at K = 4096, 191 -> 110 us at K = 14336; M = 2048,
+  // K = 14336: 411 -> 359 us; M = 2048, K = 4096 unchanged)
+  const bool big = !g2 && M >= 256;
+  if (big) bm = bn = 256;
   const uint32_t tiles = ntiles(bm, bn);
   const uint32_t S = (K + 63) / 64;
   uint32_t ks = 1;
-  if (g2 && bm == 128 && tiles < 512) {
+  if (big) {
+    ks = std::max<uint32_t>(1, std::min<uint32_t>(256 / tiles, S / 8));
+  } else if (g2 && bm == 128 && tiles < 512) {
     // about 450 workgroups, at least 6 stages per split (measured at M = 128)
     ks = std::min<uint32_t>(std::max<uint32_t>(1, (448 + tiles / 2) / tiles), std::max<uint32_t>(1, S / 6));
   } else if (bm == 128 && bn == 64 && tiles < 512) {

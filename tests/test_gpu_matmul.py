@@ -239,3 +239,46 @@ def test_config4_prefill_gemm(N, K):
     cols = np.sort(np.random.default_rng(0).choice(N, 512, replace=False))
     e = err(y[:, cols], a.astype(np.float64) @ dq[:, cols])
     assert e <= TOL_GEMM, e
+
+
+# ---------------- M >= 256: 256x256 tiles with K splits ----------------
+
+@pytest.mark.parametrize("M,K,N", [(300, 4096, 300), (257, 1024, 520), (512, 14336, 96)])
+def test_gemm_big_tiles_ragged(M, K, N):
+    """M >= 256 runs 256x256 tiles with enough K splits to fill the chip
+    (8 / 2 / 8 splits here) over ragged row and column tiles, Q4S and Q8."""
+    w = prng.randn((K, N), 61, std=0.02)
+    a = prng.randn((M, K), 62)
+    q = S.quantizeQ4(w)
+    ref = a.astype(np.float64) @ O.dequant_q4s(dev_bytes(q), K, N).astype(np.float64)
+    assert err(S.matmulQ4(S.tensor(a), q).data, ref) <= TOL_GEMM
+    q8 = S.quantizeQ8(w)
+    ref8 = a.astype(np.float64) @ O.dequant_q8(dev_bytes(q8), K, N).astype(np.float64)
+    assert err(S.matmulQ8(S.tensor(a), q8).data, ref8) <= TOL_GEMM
+
+
+@pytest.mark.parametrize("epi", [1, 2])
+def test_gemm_big_tiles_epilogues(epi):
+    """The K-split reduce applies the residual / SwiGLU epilogue (Q8 linear
+    with a fused RMSNorm, M = 300 rows on 256x256 tiles)."""
+    M, K, N, eps = 300, 2048, 320, 1e-5
+    w = prng.randn((K, N), 63, std=0.02)
+    x = prng.randn((M, K), 64)
+    g = 1 + prng.randn((K,), 65, std=0.1)
+    r = prng.randn((M, N), 66)
+    q8 = S.quantizeQ8(w)
+    wd = O.dequant_q8(dev_bytes(q8), K, N).astype(np.float64)
+    x64 = x.astype(np.float64)
+    xn = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + eps) * g.astype(np.float64)
+    y = xn @ wd
+    if epi == 1:
+        y = y + r
+    else:
+        gt, up = y[:, 0::2], y[:, 1::2]
+        y = gt / (1 + np.exp(-gt)) * up
+    ctx = device.ops_ctx()
+    xb, gb, rb = S.tensor(x), S.tensor(g), S.tensor(r)
+    out = S.create([M, N if epi == 1 else N // 2])
+    device.check(device.lib.smith_linear_q8(ctx, xb.buffer, q8["buffer"], out.buffer, M, N, K, gb.buffer, eps,
+                                            rb.buffer, epi))
+    assert err(out.data, y) <= TOL_GEMM
