@@ -151,6 +151,43 @@ __device__ __forceinline__ void dequant_wrec(const WRec& r, uint32_t (&o)[16]) {
   }
 }
 
+// elements 16h .. 16h+15 of a record (h = 0 or 1, per thread) as 8 packed f16
+// pairs: the half of dequant_wrec a thread stores when two threads share a
+// record (same arithmetic, so the same bits)
+template <int FMT>
+__device__ __forceinline__ void dequant_half(const WRec& r, uint32_t h, uint32_t (&o)[8]) {
+  if constexpr (FMT >= GT_Q41) {
+    uint32_t full[16];
+    dequant_wrec<FMT>(r, full);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = h ? full[8 + i] : full[i];
+  } else if constexpr (FMT == WF_Q8) {
+    const uint32_t d[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
+#pragma unroll
+    for (int ii = 0; ii < 4; ii++) {
+      // int8 16h + 4ii .. +3 (dwords 4h+ii, 4h+ii+1 of the shifted window)
+      const uint32_t lo = h ? d[4 + ii] : d[ii], hi = h ? d[5 + ii] : d[1 + ii];
+      const uint32_t x = __builtin_amdgcn_alignbyte(hi, lo, r.sh);
+      const float v0 = (float)(int8_t)(x & 0xFF), v1 = (float)(int8_t)((x >> 8) & 0xFF);
+      const float v2 = (float)(int8_t)((x >> 16) & 0xFF), v3 = (float)(int8_t)(x >> 24);
+      o[2 * ii] = pack_h2(r.s * v0, r.s * v1);
+      o[2 * ii + 1] = pack_h2(r.s * v2, r.s * v3);
+    }
+  } else {
+    const float c = -r.s * r.z;
+    const uint32_t d[2] = {h ? r.q.z : r.q.x, h ? r.q.w : r.q.y};
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const uint32_t lo = d[i] & 0x0F0F0F0Fu, hi = (d[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const float ql = (float)((lo >> (8 * b)) & 0xFFu), qh = (float)((hi >> (8 * b)) & 0xFFu);
+        o[4 * i + b] = pack_h2(__builtin_fmaf(ql, r.s, c), __builtin_fmaf(qh, r.s, c));
+      }
+    }
+  }
+}
+
 // 16-byte chunk position of chunk c (0..7) of LDS row r: with padded rows
 // (LD > 64) the identity; unpadded rows (LD == 64) XOR-swizzle the chunk by
 // the row so the 16-row MFMA operand reads and the row-wise stores spread
@@ -172,8 +209,10 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
   constexpr int ACH = BM * GBK / 8;                  // 16-byte A chunks per stage
   constexpr int APT = ACH / NT;                      // per thread
   constexpr int NREC = BN * GBK / 32;                // weight records per stage
-  constexpr int RPT = (NREC + NT - 1) / NT;
+  constexpr int RPT = NREC >= NT ? NREC / NT : 1;    // records per thread
+  constexpr bool HALF = NREC < NT;                   // two threads per record, 16 elements each
   static_assert(ACH % NT == 0, "A chunks must divide evenly");
+  static_assert(NREC >= NT ? NREC % NT == 0 : NT == 2 * NREC, "records must divide evenly over the threads");
   __shared__ __attribute__((aligned(16))) _Float16 As[2][BM][LD];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN][LD];
 
@@ -209,9 +248,9 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
     }
 #pragma unroll
     for (int q = 0; q < RPT; q++) {
-      const uint32_t idx = tid + NT * q;
+      const uint32_t idx = HALF ? tid % NREC : tid + NT * q;  // every thread has a record: no branch
       const uint32_t n = idx % BN, gi = idx / BN;
-      if (idx < NREC) rg.wr[q] = load_wrec<FMT>(B, D, N, G, 2 * s + gi, n0 + n);
+      rg.wr[q] = load_wrec<FMT>(B, D, N, G, 2 * s + gi, n0 + n);
     }
   };
   auto store_stage = [&](const Regs& rg, uint32_t buf) {
@@ -222,9 +261,18 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
     }
 #pragma unroll
     for (int q = 0; q < RPT; q++) {
-      const uint32_t idx = tid + NT * q;
-      const uint32_t n = idx % BN, gi = idx / BN;
-      if (idx < NREC) {
+      if constexpr (HALF) {
+        const uint32_t idx = tid % NREC, h = tid / NREC;
+        const uint32_t n = idx % BN, gi = idx / BN;
+        uint32_t o[8];
+        dequant_half<FMT>(rg.wr[q], h, o);
+#pragma unroll
+        for (int v = 0; v < 2; v++)
+          *(u32x4*)&Bs[buf][n][8 * swz<LD>(n, 4 * gi + 2 * h + v)] =
+              (u32x4){o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]};
+      } else {
+        const uint32_t idx = tid + NT * q;
+        const uint32_t n = idx % BN, gi = idx / BN;
         uint32_t o[16];
         dequant_wrec<FMT>(rg.wr[q], o);
 #pragma unroll
@@ -268,7 +316,9 @@ __device__ __forceinline__ void gemm_body(const _Float16* __restrict__ A16, cons
     store_stage(r0, 0);
   }
   __syncthreads();
-  // steady state without guards (the last stage is peeled off)
+  // steady state without guards (the last stage is peeled off).  (Pinning the
+  // loads to the top of the stage with scheduling barriers measured slower:
+  // the compiler's interleaving of the dequant work with the MFMAs wins.)
   for (uint32_t s = 0; s + 1 < S; s++) {
     const uint32_t buf = s & 1;
     load_stage(r0, s0 + s + 1);
