@@ -330,7 +330,10 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   uint32_t kb = G <= 64 ? 64 : (G <= 96 ? 96 : (G <= 128 ? 128 : (G <= 288 ? 288 : 128)));
   uint32_t threads = kb == 64 ? 256 : 512;
   // wide outputs: two column tiles per wave halve the workgroup count
-  bool c2 = M == 1 && (kb == 96 || kb == 128) && N >= 16384;
+  // (4-bit records from N = 8192: 11.3 -> 10.5 us at N = 14336; the Q8 records,
+  // 34 B and more registers per record, lose below 16384: 16.2 -> 17.3 us)
+  const uint32_t c2min = fmt == FQ8 ? 16384u : 8192u;
+  bool c2 = M == 1 && (kb == 96 || kb == 128) && N >= c2min;
   uint32_t gx = c2 ? (N + 31) / 32 : (N + 15) / 16;
   uint32_t ksplit = (G + kb - 1) / kb;
   if (ksplit > 1) {
