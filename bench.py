@@ -9,7 +9,8 @@ roofline.achieved = algorithmic bytes / average duration of the GEMV kernel,
 from HIP events recorded around every GEMV launch on the stream it runs on.
 
 Also measured in the same run (under "configs"): Q4_0 GEMV (GGUF format),
-Q8 GEMV [4096 x 14336] (config 2), the Q4 batched-decode sweep (config 3),
+Q8 GEMV [4096 x 14336] (config 2), the Q4 batched-decode sweep (config 3, on
+quantizeQ4 records and on GGUF Q4_0 blocks),
 the Q4 prefill shapes (config 4), and the CPU baseline: the oracle's
 dequantize + f32 matmul (single thread) on a bounded sample of config 1.
 
@@ -160,6 +161,9 @@ def bench_q8(D, S, prng, M, K, N, steps, warmup):
 
 
 def bench_q40(D, S, prng, M, K, N, steps, warmup):
+    """GGUF Q4_0 blocks as the GGUF decode path holds them: nibble and scale
+    planes in 16-column tile-major order (smith_repack_q4_0_t_into), through
+    smith_linear_q4_0_t (the same GEMV kernels as matmulQ4 for M <= 32)."""
     ctx = D.ops_ctx()
     x = S.tensor(prng.randn((N, K), 1, std=0.02))  # GGUF listing [out, in]
     G = K // 32
@@ -167,16 +171,22 @@ def bench_q40(D, S, prng, M, K, N, steps, warmup):
     D.check(D.lib.smith_quantize_q4_0(ctx, x.buffer, blocks, N, K))
     nib = D.alloc(N * G * 16)
     dsc = D.alloc(N * G * 2)
-    D.check(D.lib.smith_repack_q4_0(ctx, blocks, nib, dsc, N, K))
+    D.check(D.lib.smith_repack_q4_0_t_into(ctx, blocks, nib, dsc, N, K, 0, 1, N))
     W = Weights(D, nib, N * G * 16, extra=(dsc, N * G * 2))
     a = S.tensor(prng.randn((M, K), 0))
     out = S.create([M, N])
 
     def step(i):
         j = i % len(W.bufs)
-        D.lib.smith_matmul_q4_0(ctx, a.buffer, W.bufs[j], W.extra[j][0], out.buffer, M, N, K)
+        D.lib.smith_linear_q4_0_t(ctx, a.buffer, W.bufs[j], W.extra[j][0], out.buffer, M, N, K, None, 0.0, None, 0)
 
     ms, kt = time_steps(D, step, steps, warmup)
+    for b in W.bufs[1:]:
+        D.release_buffer(b)
+    for eb, _ in W.extra[1:]:
+        D.release_buffer(eb)
+    for b in (blocks, nib, dsc):
+        D.release_buffer(b)
     return ms, kt, alg_bytes(q40_bytes(K, N), M, K, N)
 
 
@@ -426,6 +436,15 @@ def main():
                     "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
         configs["cfg3_q4s_batched_decode"] = sweep
         log("cfg3:", json.dumps(sweep))
+        sweep40 = {}  # the same sweep on GGUF Q4_0 blocks (18 B per 32 weights, tile-major planes)
+        for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
+            for M in (1, 4, 8, 16, 32):
+                msx, ktx, bx = bench_q40(D, S, prng, M, Kk, Nn, sub, 5)
+                sweep40["M%d_N%d_K%d" % (M, Nn, Kk)] = {
+                    "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
+                    "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
+        configs["cfg3_q4_0_batched_decode"] = sweep40
+        log("cfg3 q4_0:", json.dumps(sweep40))
         pre = bench_cfg4(D, S, prng)
         configs["cfg4_q4s_prefill"] = pre
         log("cfg4:", json.dumps(pre))
