@@ -258,10 +258,12 @@ def test_gemm_big_tiles_ragged(M, K, N):
 
 
 @pytest.mark.parametrize("epi", [1, 2])
-def test_gemm_big_tiles_epilogues(epi):
-    """The K-split reduce applies the residual / SwiGLU epilogue (Q8 linear
-    with a fused RMSNorm, M = 300 rows on 256x256 tiles)."""
-    M, K, N, eps = 300, 2048, 320, 1e-5
+@pytest.mark.parametrize("K", [2048, 1024])
+def test_gemm_big_tiles_epilogues(epi, K):
+    """The K-split finish applies the residual / SwiGLU epilogue (Q8 linear
+    with a fused RMSNorm, M = 300 rows on 256x256 tiles): 4 splits summed by
+    smith_gemm_reduce (K = 2048) and 2 (K = 1024)."""
+    M, N, eps = 300, 320, 1e-5
     w = prng.randn((K, N), 63, std=0.02)
     x = prng.randn((M, K), 64)
     g = 1 + prng.randn((K,), 65, std=0.1)
