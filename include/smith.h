@@ -265,13 +265,28 @@ int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, flo
 int smith_dequantize_gguf(void* ctx, uint32_t ggml_type, const void* src, float* dst, uint64_t numel);
 /* LM head on a Q4_0 output.weight read as lmHead[K=dim][N=vocab] (blocks run
  * along the vocab axis, gguf_loader.js:240-259): smith_repack_lmhead_q4_0
- * splits the raw blocks into a nibble plane (K*N/2 bytes, block order) and a
- * scale plane transposed to [N/32][K] (f16); smith_lmhead_q4_0_nb computes
- * y = x . lmHead on those planes, optional fused final RMSNorm.
- * K % 8 == 0, K <= 8192, N % 32 == 0. */
+ * regroups the raw blocks by row octets into a nibble plane (K*N/2 bytes:
+ * record (k/8, vocab block) = 8 rows x 16 nibble bytes, quarter-major) and a
+ * scale plane (K*N/16 bytes: the 8 f16 scales of each record);
+ * smith_lmhead_q4_0_nb computes y = x . lmHead on those planes, optional
+ * fused final RMSNorm.  K % 8 == 0, K <= 8192, N % 32 == 0.
+ * Replaces the f32 lm-head matmul of gguf_cache.js:174-184. */
 int smith_repack_lmhead_q4_0(void* ctx, const void* blocks, void* nib, void* d, uint32_t K, uint32_t N);
 int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
                          const void* d, float* y, uint32_t K, uint32_t N);
+/* smith_lmhead_q4_0_nb followed by smith_argmax_embed's greedy step in the
+ * same launch (gguf_cache.js:174-184 then generate.js:70-76 and the token
+ * append of gguf_cache.js:335-341): logits are written as by
+ * smith_lmhead_q4_0_nb; token = first maximum of the logits (a NaN at index 0
+ * gives 0, as the reference's scan), tokens[*count] = token, x_out =
+ * E[token] (may be x: it is written after every read of x), ++*count, ++*pos,
+ * the act of x_out times gamma_out and the rope row as smith_argmax_embed.
+ * Calls on one context must not overlap (one device-side argmax slot). */
+int smith_lmhead_q4_0_greedy(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
+                             const void* d, float* logits, uint32_t K, uint32_t N, const float* E, float* x_out,
+                             int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out,
+                             const float* rope_cos, const float* rope_sin, uint32_t rope_len, uint32_t wq,
+                             uint32_t wk, float* rope_row);
 /* f32 GEMV, W [K][N] (w_is_nk = 0) or [N][K] (weight tying, 1). */
 int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,
                    uint32_t K, uint32_t N, int w_is_nk);

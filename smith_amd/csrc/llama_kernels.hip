@@ -12,6 +12,8 @@
 #include "splitk.h"
 #include "gguf_tiles.h"
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------------------
 // RMSNorm rows: y = x * rsqrt(mean(x^2) + eps) * gamma
 // (shaders/rmsnorm.metal:15-47; one workgroup per row).
@@ -692,18 +694,14 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
 // path that does not end in ".weight"), so for Q4_0 the 32-weight blocks run
 // along the VOCAB axis: block (k, vb) at (k*(N/32) + vb)*18 covers
 // lmHead[k][32vb .. 32vb+31] = d*(nib - 8), element e in nibble e (byte
-// e/2, low nibble first).  smith_repack_lmhead_q4_0 splits the blocks into
-// a nibble plane in the same (k, vb) order (16 bytes per block) and a scale
-// plane transposed to [vb][k], so a lane reads one dword of nibbles per row
-// and the scales of 8 rows in one 16-byte load.
-// y[n] = sum_k x[k] * lmHead[k][n] for M = 1, optionally with the final
-// RMSNorm of x fused (gamma != null).
-// Lane (vb = lane/4, sub = lane%4) owns outputs 32vb + 8sub .. +7 of the 16
-// blocks a workgroup covers; per row: c = x_k * d, 8 fma(c, nibble), and one
-// -8c correction for the lane's 8 outputs.  Rows go in batches of 16 with
-// the next batch's loads issued before the current one is used.  8 waves
-// split the workgroup's K range (LDS reduction); K splits across workgroups
-// (grid.y) are summed by the last-arriving workgroup.
+// e/2, low nibble first).  smith_repack_lmhead_q4_0 regroups the blocks by
+// row octets: record (o = k/8, vb) holds the nibbles of rows 8o .. 8o+7 as
+// 128 bytes [quarter q = 0..3][row r = 0..7][the 4 nibble bytes 4q .. 4q+3 of
+// block (8o+r, vb)] in a nibble plane, and the 8 scales as 16 bytes in a
+// scale plane, both in (o, vb) order.  Lane (vb, q) then reads its 8 outputs'
+// nibbles of 8 rows as two 16-byte loads and their scales as one, and a wave
+// (16 blocks x 4 quarters) reads 2 KB of contiguous nibbles per row octet.
+// K % 8 == 0.
 // ---------------------------------------------------------------------------
 extern "C" __global__ void smith_repack_lmhead_q4_0(const uint8_t* __restrict__ src, uint8_t* __restrict__ nib,
                                                     uint16_t* __restrict__ dsc, uint32_t K, uint32_t NB) {
@@ -712,66 +710,176 @@ extern "C" __global__ void smith_repack_lmhead_q4_0(const uint8_t* __restrict__ 
        idx += (size_t)gridDim.x * blockDim.x) {
     const uint32_t k = (uint32_t)(idx / NB), vb = (uint32_t)(idx % NB);
     const uint16_t* b = (const uint16_t*)(src + idx * 18);
-    dsc[(size_t)vb * K + k] = b[0];
-    uint16_t* dn = (uint16_t*)(nib + idx * 16);
+    const size_t rec = (size_t)(k / 8) * NB + vb;
+    const uint32_t r = k % 8;
+    dsc[rec * 8 + r] = b[0];
 #pragma unroll
-    for (int i = 0; i < 8; i++) dn[i] = b[1 + i];
+    for (int q = 0; q < 4; q++)
+      *(uint32_t*)(nib + rec * 128 + q * 32 + r * 4) = (uint32_t)b[1 + 2 * q] | ((uint32_t)b[2 + 2 * q] << 16);
   }
 }
 
-#define LMH_BATCH 16
+// Greedy step after the logits (generate.js:70-76 argmax, gguf_cache.js:
+// 335-341 append): the token goes to tokens[count], count and the position
+// advance, x = E[token] (and its act for the next step's first GEMV), and the
+// rope row of the next position is written (cos / sin of the q and k row
+// widths, tagged with that position) when the table holds it.
+struct GreedyTail {
+  const float* E;  // null: no greedy step
+  float* x;
+  int32_t* tokens;
+  int32_t* count;
+  int32_t* pos;
+  uint8_t* act_out;
+  const float* gamma_out;
+  const float* cosT;
+  const float* sinT;
+  float* rrow;
+  uint64_t* amx;  // [0] best key, [1] low word: tiles finished (zero between calls)
+  uint32_t rope_len, wq, wk, dim;
+};
 
-extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
+// Order-preserving key of (logit, index) for an unsigned max: larger logits
+// win, and among equal logits the smaller index (the reference keeps the
+// first maximum).  NaNs never win (key 0); -0 counts as +0.  A NaN at index 0
+// gets the largest key: the reference's scan compares against logits[0]
+// first and then never moves.  Key 0 and the all-ones key both decode to 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t n) {
+  if (v != v) return n == 0 ? ~0ull : 0ull;
+  uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - n);
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)k, d), hi = __shfl_xor((uint32_t)(k >> 32), d);
+    k = umax64(k, ((uint64_t)hi << 32) | lo);
+  }
+  return k;
+}
+
+// The rope row of position np (tag np), written when the tables hold it;
+// threads tid, tid + nt, ... of the caller.
+__device__ __forceinline__ void rope_row_write(float* __restrict__ rrow, const float* __restrict__ cosT,
+                                               const float* __restrict__ sinT, uint32_t rope_len, uint32_t wq,
+                                               uint32_t wk, uint32_t np, uint32_t tid, uint32_t nt) {
+  const uint32_t hq = wq / 2, hk = wk / 2;
+  if (!rrow || (size_t)(np + 1) * hq > rope_len || (size_t)(np + 1) * hk > rope_len) return;
+  for (uint32_t i = tid; i < hq + hk; i += nt) {
+    const size_t t = i < hq ? (size_t)np * hq + i : (size_t)np * hk + (i - hq);
+    const uint32_t o = i < hq ? ROPE_ROW_HDR + i : ROPE_ROW_HDR + wq + (i - hq);
+    const uint32_t half = i < hq ? hq : hk;
+    rrow[o] = cosT[t];
+    rrow[o + half] = sinT[t];
+  }
+  if (tid == 0) *(int32_t*)rrow = (int32_t)np;
+}
+
+// x = E[t] and its act (gamma_out may be null), by NT threads: every load of
+// a chunk of CH * NT elements is issued before the first store (the stores
+// may alias E as far as the compiler knows, so a load-store loop would take
+// one memory round trip per iteration).  dim % 32 == 0 with an act.
+template <int NT, int CH>
+__device__ __forceinline__ void embed_row(const float* __restrict__ E, int32_t t, uint32_t dim, float* x,
+                                          uint8_t* act_out, const float* gamma_out, uint32_t tid) {
+  for (uint32_t base = 0; base < dim; base += CH * NT) {
+    float ev[CH], gv[CH];
+#pragma unroll
+    for (int q = 0; q < CH; q++) {
+      const uint32_t i = base + tid + NT * q;
+      ev[q] = i < dim ? E[(size_t)t * dim + i] : 0.f;
+      gv[q] = i < dim && gamma_out ? gamma_out[i] : 1.f;
+    }
+#pragma unroll
+    for (int q = 0; q < CH; q++) {
+      const uint32_t i = base + tid + NT * q;
+      if (i < dim) {
+        x[i] = ev[q];
+        if (act_out) act_emit8(act_out, dim, i, ev[q], gv[q]);
+      }
+    }
+  }
+}
+
+// y[n] = sum_k x[k] * lmHead[k][n] for M = 1, optionally with the final
+// RMSNorm of x fused (gamma != null).  Workgroup (bx, split): 16 blocks of
+// 32 outputs, the split's row octets shared by 8 waves (at most 4 octets per
+// wave: the host picks splits of <= 256 rows), every load of a wave issued
+// at once.  Lane (vb, q) owns outputs 32vb + 8q .. +7; per row c = x_k * d,
+// 8 fma(c, nibble) and one -8c correction.  Waves are summed in LDS, splits
+// by the last-arriving workgroup of the column tile (agent-scope atomics).
+// With a greedy tail (gt.E != null), each tile's finisher publishes the
+// argmax key of its 512 logits with one 64-bit atomic max, and the last tile
+// to finish runs the greedy step with the winning token.
+#define LMH_OCT 4
+#define LMH_ROWS (8 * 8 * LMH_OCT)
+
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void smith_lmhead_q4_0_nb(
     const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ nib,
     const uint16_t* __restrict__ dsc, float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws,
-    uint32_t* __restrict__ counters) {
-  __shared__ float xs[8192];
+    uint32_t* __restrict__ counters, GreedyTail gt) {
+  __shared__ float xs[LMH_ROWS];
   __shared__ float part[8][512];
   __shared__ float red[8];
+  __shared__ uint64_t kred[8];
   __shared__ int s_last;
   const uint32_t NB = N / 32;
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t vb0 = blockIdx.x * 16 + lane / 4, sub = lane & 3;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t vb0 = blockIdx.x * 16 + lane / 4, qq = lane & 3;
   const uint32_t vb = vb0 < NB ? vb0 : NB - 1;  // clamped; lanes past NB store nothing
   const uint32_t ksplit = gridDim.y;
-  // split and wave row counts are multiples of 8 (K % 8 == 0): aligned 16-byte scale loads
-  const uint32_t kb = ((K + ksplit - 1) / ksplit + 7) / 8 * 8;
-  const uint32_t kb0 = blockIdx.y * kb < K ? blockIdx.y * kb : K, kb1 = kb0 + kb < K ? kb0 + kb : K;
-  const uint32_t kper = ((kb1 - kb0 + 7) / 8 + 7) / 8 * 8;
-  const uint32_t k0 = kb0 + wave * kper < kb1 ? kb0 + wave * kper : kb1;
-  const uint32_t k1 = k0 + kper < kb1 ? k0 + kper : kb1;
+  const uint32_t KO = K / 8;
+  const uint32_t ob = (KO + ksplit - 1) / ksplit;  // octets per split (<= 8 * LMH_OCT)
+  const uint32_t os0 = blockIdx.y * ob < KO ? blockIdx.y * ob : KO, os1 = os0 + ob < KO ? os0 + ob : KO;
+  const uint32_t ow = (os1 - os0 + 7) / 8;  // octets per wave (<= LMH_OCT)
+  const uint32_t o0 = os0 + wave * ow < os1 ? os0 + wave * ow : os1, o1 = o0 + ow < os1 ? o0 + ow : os1;
 
-  // 1. x (and gamma) loads, then the first row batch in flight
-  float xv[16], gvv[16];
+  // 1. x for the norm (the first 4096 entries; the rest, if any, later),
+  //    this split's x / gamma, the weights: all in flight
+  float xv[8];
 #pragma unroll
-  for (int q = 0; q < 16; q++) {
-    const uint32_t i = threadIdx.x + 512 * q;
+  for (int q = 0; q < 8; q++) {
+    const uint32_t i = tid + 512 * q;
     xv[q] = i < K ? x[i] : 0.f;
-    gvv[q] = gamma && i < K ? gamma[i] : 1.f;
   }
-  uint32_t wn[LMH_BATCH];
-  uint4 wd[LMH_BATCH / 8];
-  auto load_batch = [&](uint32_t kbase) {
+  const uint32_t kx = os0 * 8 + tid;
+  const bool xin = tid < LMH_ROWS && kx < os1 * 8;
+  const float xsv = xin ? x[kx] : 0.f;
+  const float gsv = xin && gamma ? gamma[kx] : 1.f;
+  u32x4 wn[LMH_OCT][2], wd[LMH_OCT];
 #pragma unroll
-    for (int r = 0; r < LMH_BATCH; r++) {
-      const uint32_t k = kbase + r < k1 ? kbase + r : (k1 > 0 ? k1 - 1 : 0);
-      wn[r] = *(const uint32_t*)(nib + ((size_t)k * NB + vb) * 16 + 4 * sub);
-    }
-#pragma unroll
-    for (int q = 0; q < LMH_BATCH / 8; q++) {
-      uint32_t k = kbase + 8 * q;
-      k = k < K ? k : K - 8;  // K % 8 == 0
-      wd[q] = *(const uint4*)(dsc + (size_t)vb * K + k);
-    }
-  };
-  if (k0 < k1) load_batch(k0);
+  for (int j = 0; j < LMH_OCT; j++) {
+    uint32_t oc = o0 + j < o1 ? o0 + j : (o1 > 0 ? o1 - 1 : 0);
+    oc = oc < KO ? oc : KO - 1;
+    const size_t rec = (size_t)oc * NB + vb;
+    const uint8_t* pn = nib + rec * 128 + qq * 32;
+    wn[j][0] = *(const u32x4*)pn;
+    wn[j][1] = *(const u32x4*)(pn + 16);
+    wd[j] = *(const u32x4*)(dsc + rec * 8);
+  }
 
-  // 2. RMSNorm of x into LDS
-  float ss = 0.f;
-#pragma unroll
-  for (int q = 0; q < 16; q++) ss = __builtin_fmaf(xv[q], xv[q], ss);
+  // the greedy step's count and position (written only by this launch's last
+  // workgroup, after every other has finished), and the next position's rope
+  // row, which does not depend on the token (workgroup (0, 0))
+  int32_t c0 = 0, p0 = 0;
+  if (gt.E) {
+    c0 = gt.count[0];
+    p0 = gt.pos[0];
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      rope_row_write(gt.rrow, gt.cosT, gt.sinT, gt.rope_len, gt.wq, gt.wk, (uint32_t)p0 + 1, tid, 512);
+  }
+
+  // 2. RMSNorm scale; this split's normalized x into LDS
   float rms = 1.f;
   if (gamma) {
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) ss = __builtin_fmaf(xv[q], xv[q], ss);
+    for (uint32_t i = tid + 4096; i < K; i += 512) ss = __builtin_fmaf(x[i], x[i], ss);
     for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
@@ -779,11 +887,7 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
     for (int w = 0; w < 8; w++) tot += red[w];
     rms = 1.0f / __builtin_sqrtf(tot / (float)K + eps);
   }
-#pragma unroll
-  for (int q = 0; q < 16; q++) {
-    const uint32_t i = threadIdx.x + 512 * q;
-    if (i < K) xs[i] = gamma ? xv[q] * rms * gvv[q] : xv[q];
-  }
+  if (tid < LMH_ROWS) xs[tid] = gamma ? xsv * rms * gsv : xsv;
   __syncthreads();
 
   // 3. rows
@@ -791,21 +895,15 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = 0.f;
   float corr = 0.f;
-  for (uint32_t kb16 = k0; kb16 < k1; kb16 += LMH_BATCH) {
-    uint32_t cn[LMH_BATCH];
-    uint4 cd[LMH_BATCH / 8];
 #pragma unroll
-    for (int r = 0; r < LMH_BATCH; r++) cn[r] = wn[r];
+  for (int j = 0; j < LMH_OCT; j++) {
+    const uint32_t oc = o0 + j;
 #pragma unroll
-    for (int q = 0; q < LMH_BATCH / 8; q++) cd[q] = wd[q];
-    if (kb16 + LMH_BATCH < k1) load_batch(kb16 + LMH_BATCH);
-#pragma unroll
-    for (int r = 0; r < LMH_BATCH; r++) {
-      const uint32_t k = kb16 + r;
-      const uint32_t dw = (&cd[r / 8].x)[(r % 8) / 2];
+    for (int r = 0; r < 8; r++) {
+      const uint32_t dw = wd[j][r / 2];
       const uint16_t dh = (uint16_t)((r & 1) ? dw >> 16 : dw & 0xFFFFu);
-      const float c = k < k1 ? xs[k] * (float)__builtin_bit_cast(_Float16, dh) : 0.f;
-      const uint32_t w = cn[r];
+      const float c = oc < o1 ? xs[(oc - os0) * 8 + r] * (float)__builtin_bit_cast(_Float16, dh) : 0.f;
+      const uint32_t w = wn[j][r / 4][r % 4];
       const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 2j / 2j+1 in byte j
       corr += c;
 #pragma unroll
@@ -818,31 +916,58 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q4_0_nb(
 #pragma unroll
   for (int e = 0; e < 8; e++) part[wave][lane * 8 + e] = __builtin_fmaf(-8.0f, corr, acc[e]);
   __syncthreads();
-  const uint32_t nb0 = blockIdx.x * 512;
-  const uint32_t o = threadIdx.x, n = nb0 + o;
+  const uint32_t n = blockIdx.x * 512 + tid;
   float v = 0.f;
 #pragma unroll
-  for (int w = 0; w < 8; w++) v += part[w][o];
-  if (ksplit == 1) {
-    if (n < N) y[n] = v;
-    return;
+  for (int w = 0; w < 8; w++) v += part[w][tid];
+  if (ksplit > 1) {
+    if (n < N)
+      __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == ksplit - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (n < N) v = splitk_sum(ws + n, N, ksplit);
+    if (tid == 0)
+      __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (n < N)
-    __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
+  if (n < N) y[n] = v;
+  if (!gt.E) return;
+
+  // 4. greedy: this tile's best key, then the last tile runs the step.  The
+  //    max is a returning atomic, complete (performed at agent scope) before
+  //    the tile counter moves, so no fence is needed.
+  const uint64_t key = wave_max64(n < N ? argmax_key(v, n) : 0ull);
+  if (lane == 0) kred[wave] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == ksplit - 1;
+  if (tid == 0) {
+    uint64_t b = kred[0];
+    for (int w = 1; w < 8; w++) b = umax64(b, kred[w]);
+    kred[0] = __hip_atomic_fetch_max(gt.amx, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t prev =
+        __hip_atomic_fetch_add((uint32_t*)(gt.amx + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == gridDim.x - 1;
+    if (s_last) {
+      kred[1] = __hip_atomic_exchange(gt.amx, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store((uint32_t*)(gt.amx + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   if (!s_last) return;
-  if (n < N) {
-    y[n] = splitk_sum(ws + n, N, ksplit);
+  const uint64_t best = kred[1];
+  const int32_t t = best == 0 ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)best);
+  if (tid == 0) {
+    gt.tokens[c0] = t;
+    gt.count[0] = c0 + 1;
+    gt.pos[0] = p0 + 1;
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  embed_row<512, 6>(gt.E, t, gt.dim, gt.x, gt.act_out, gt.gamma_out, tid);
 }
 
 // f32 GEMV on a [K][N] row-major weight (an F32 output.weight read as
@@ -961,17 +1086,7 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(
     }
   }
   // the next position's rope row (independent of the token)
-  const uint32_t np = (uint32_t)p + 1, hq = wq / 2, hk = wk / 2;
-  if (rrow && (size_t)(np + 1) * hq <= rope_len && (size_t)(np + 1) * hk <= rope_len) {
-    for (uint32_t i = threadIdx.x; i < hq + hk; i += 1024) {
-      const size_t t = i < hq ? (size_t)np * hq + i : (size_t)np * hk + (i - hq);
-      const uint32_t o = i < hq ? ROPE_ROW_HDR + i : ROPE_ROW_HDR + wq + (i - hq);
-      const uint32_t half = i < hq ? hq : hk;
-      rrow[o] = cosT[t];
-      rrow[o + half] = sinT[t];
-    }
-    if (threadIdx.x == 0) *(int32_t*)rrow = (int32_t)np;
-  }
+  rope_row_write(rrow, cosT, sinT, rope_len, wq, wk, (uint32_t)p + 1, threadIdx.x, 1024);
   for (int d = 32; d >= 1; d >>= 1) {
     float ov = __shfl_xor(best, d);
     int32_t oi = __shfl_xor(bidx, d);
@@ -994,18 +1109,15 @@ extern "C" __global__ __launch_bounds__(1024) void smith_argmax_embed(
         t = bi[w];
       }
     if (t == 0x7fffffff) t = 0;  // all NaN: the reference's argmax returns 0
+    if (logits[0] != logits[0]) t = 0;  // the reference's scan never moves past a NaN at index 0
     s_tok = t;
     tokens[c0] = t;
     count[0] = c0 + 1;
   }
   __syncthreads();
   const int32_t t = s_tok;
-  for (uint32_t i = threadIdx.x; i < dim; i += 1024) {
-    const float v = E[(size_t)t * dim + i];
-    x[i] = v;
-    if (act_out) act_emit8(act_out, dim, i, v, gamma_out ? gamma_out[i] : 1.0f);  // dim % 32 == 0
-  }
-  if (threadIdx.x == 0) pos[0] = (int32_t)np;
+  embed_row<1024, 4>(E, t, dim, x, act_out, gamma_out, threadIdx.x);
+  if (threadIdx.x == 0) pos[0] = p + 1;
 }
 
 // Set a device int (graph-capturable replacement for a tiny H2D copy).
@@ -1076,6 +1188,8 @@ extern "C" __global__ void smith_repack_lmhead_q6_k(const uint8_t* __restrict__ 
     ((uint16_t*)(planes + od))[(size_t)vb * K + k] = (uint16_t)(b[208] | (b[209] << 8));
   }
 }
+
+#define LMH_BATCH 16  // rows per batch of loads
 
 extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
     const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ planes,

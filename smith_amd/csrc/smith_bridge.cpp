@@ -54,6 +54,7 @@ struct Ctx {
   float* ws = nullptr;
   size_t ws_bytes = 0;
   uint32_t* counters = nullptr;
+  uint64_t* amx = nullptr;  // greedy LM head: best key, tiles finished (zero between calls)
   size_t counters_n = 0;
   void* normbuf = nullptr;
   size_t normbuf_bytes = 0;
@@ -203,6 +204,30 @@ int ensure_counters(Ctx* c, size_t n) {
   c->counters_n = cap;
   return 0;
 }
+
+int ensure_amx(Ctx* c) {
+  if (c->amx) return 0;
+  if (c->capturing) return fail(c, "smith: greedy LM head state needed while capturing a graph; run the op once first");
+  HIPCHK(c, hipMalloc((void**)&c->amx, 2 * sizeof(uint64_t)));
+  HIPCHK(c, hipMemset(c->amx, 0, 2 * sizeof(uint64_t)));
+  return 0;
+}
+
+// Kernel argument of smith_lmhead_q4_0_nb (same layout as the device struct).
+struct GreedyTail {
+  const float* E;
+  float* x;
+  int32_t* tokens;
+  int32_t* count;
+  int32_t* pos;
+  void* act_out;
+  const float* gamma_out;
+  const float* cosT;
+  const float* sinT;
+  float* rrow;
+  uint64_t* amx;
+  uint32_t rope_len, wq, wk, dim;
+};
 
 enum Fmt { FQ4S = 0, FQ8 = 1, FQ40 = 2, FQ40T = 3, FQ41T = 4, FQ50T = 5, FQ4KT = 6, FQ6KT = 7 };
 
@@ -518,6 +543,7 @@ void smith_destroy(void* ctx) {
   if (c->att_cnt) hipFree(c->att_cnt);
   if (c->ws) hipFree(c->ws);
   if (c->counters) hipFree(c->counters);
+  if (c->amx) hipFree(c->amx);
   for (auto& r : c->recs) {
     hipEventDestroy(r.a);
     hipEventDestroy(r.b);
@@ -1485,24 +1511,48 @@ int smith_repack_lmhead_q4_0(void* ctx, const void* blocks, void* nib, void* d, 
                 dim3(256), args);
 }
 
-int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
-                         const void* d, float* y, uint32_t K, uint32_t N) {
-  Ctx* c = (Ctx*)ctx;
-  if (!c) return -1;
-  if (N % 32) return fail(c, "smith_lmhead_q4_0_nb: vocab %u is not a multiple of 32", N);
-  if (K > 8192 || K % 8 || !K) return fail(c, "smith_lmhead_q4_0_nb: dim %u unsupported (8..8192, %% 8)", K);
+static int lmhead_q4_0(Ctx* c, const char* who, const float* x, const float* norm_gamma, float eps,
+                       const void* nib, const void* d, float* y, uint32_t K, uint32_t N, GreedyTail gt) {
+  if (N % 32) return fail(c, "%s: vocab %u is not a multiple of 32", who, N);
+  if (K > 8192 || K % 8 || !K) return fail(c, "%s: dim %u unsupported (8..8192, %% 8)", who, K);
   if (set_device(c)) return -1;
   uint32_t gx = (N / 32 + 15) / 16;
-  // enough K splits that each of a workgroup's 8 waves has <= 32 rows
-  uint32_t ksplit = std::max<uint32_t>(1, std::min<uint32_t>((K + 255) / 256, 64));
+  // splits of <= 256 rows: at most 4 row octets per wave, all loads in flight at once
+  uint32_t ksplit = std::max<uint32_t>(1, (K + 255) / 256);
   if (ksplit > 1) {
     if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * N * sizeof(float))) return -1;
     if (ensure_counters(c, gx)) return -1;
   }
   float* pws = c->ws;
   uint32_t* pcnt = c->counters;
-  void* args[] = {&x, &norm_gamma, &eps, &nib, &d, &y, &K, &N, &pws, &pcnt};
+  void* args[] = {&x, &norm_gamma, &eps, &nib, &d, &y, &K, &N, &pws, &pcnt, &gt};
   return launch(c, "smith_lmhead_q4_0_nb", dim3(gx, ksplit), dim3(512), args);
+}
+
+int smith_lmhead_q4_0_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
+                         const void* d, float* y, uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  GreedyTail gt{};
+  return lmhead_q4_0(c, "smith_lmhead_q4_0_nb", x, norm_gamma, eps, nib, d, y, K, N, gt);
+}
+
+int smith_lmhead_q4_0_greedy(void* ctx, const float* x, const float* norm_gamma, float eps, const void* nib,
+                             const void* d, float* logits, uint32_t K, uint32_t N, const float* E, float* x_out,
+                             int32_t* tokens, int32_t* count, int32_t* pos, void* act_out, const float* gamma_out,
+                             const float* rope_cos, const float* rope_sin, uint32_t rope_len, uint32_t wq,
+                             uint32_t wk, float* rope_row) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!E || !x_out || !tokens || !count || !pos)
+    return fail(c, "smith_lmhead_q4_0_greedy: embedding, x, tokens, count and position are required");
+  if (act_out && K % 32) return fail(c, "smith_lmhead_q4_0_greedy: an act output needs dim %% 32 == 0 (dim %u)", K);
+  if (rope_row && (!rope_cos || !rope_sin || wq % 2 || wk % 2))
+    return fail(c, "smith_lmhead_q4_0_greedy: a rope row needs both tables and even row widths");
+  if (set_device(c) || ensure_amx(c)) return -1;
+  GreedyTail gt{E, x_out, tokens, count, pos, act_out, gamma_out, rope_cos, rope_sin, rope_row, c->amx,
+                rope_len, wq, wk, K};
+  return lmhead_q4_0(c, "smith_lmhead_q4_0_greedy", x, norm_gamma, eps, nib, d, logits, K, N, gt);
 }
 
 uint64_t smith_lmhead_q6_k_bytes(uint32_t K, uint32_t N) {

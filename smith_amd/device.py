@@ -105,6 +105,8 @@ SYMBOLS = {
     "smith_attention": (_INT, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _U32, _P, _P]),
     "smith_repack_lmhead_q4_0": (_INT, [_P, _P, _P, _P, _U32, _U32]),
     "smith_lmhead_q4_0_nb": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _P, _U32, _U32]),
+    "smith_lmhead_q4_0_greedy": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _P, _P,
+                                        _P, _P, _P, _U32, _U32, _U32, _P]),
     "smith_gemv_f32": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _U32, _U32, _INT]),
     "smith_argmax_embed": (_INT, [_P, _P, _U32, _P, _U32, _P, _P, _P, _P, _P, _P, _P, _P, _U32, _U32, _U32, _P]),
     "smith_set_i32": (_INT, [_P, _P, ctypes.c_int32]),

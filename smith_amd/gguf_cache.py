@@ -32,6 +32,8 @@ from . import device
 # SMITH_DECODE_GRAPH=0 runs every decode step eagerly (kernel-level profilers
 # that cannot trace graph replays); results are identical.
 USE_GRAPH = os.environ.get("SMITH_DECODE_GRAPH", "1") != "0"
+# Q4_0 LM head and the greedy step in one launch (smith_lmhead_q4_0_greedy)
+FUSED_GREEDY = os.environ.get("SMITH_FUSED_GREEDY", "1") != "0"
 
 PREFILL_CHUNK = 256
 
@@ -180,6 +182,23 @@ class _Engine:
                                                    self.count.ptr, self.pos.ptr, a0, g0, rope["cos"].ptr,
                                                    rope["sin"].ptr, rope["cos"].shape[0], cfg["numHeads"] * hd,
                                                    cfg["numKVHeads"] * hd, rr), "argmax")
+
+    def head_greedy(self, model):
+        """LM head on x, then the greedy step: one launch for a Q4_0 head."""
+        head = model["lmHead"]
+        if not (FUSED_GREEDY and head["kind"] == "q4_0_nb"):
+            self.lm_head(model, self.x.ptr)
+            self.greedy_step(model)
+            return
+        cfg = self.cfg
+        a0, g0 = self._act0(model)
+        rope, hd = model["rope"], cfg["headDim"]
+        rr = self.rope_row.ptr if self.use_parts else None
+        device.check(device.lib.smith_lmhead_q4_0_greedy(
+            device.ops_ctx(), self.x.ptr, model["lnFGamma"].ptr, model["normEps"], head["nib"].ptr, head["d"].ptr,
+            self.logits.ptr, cfg["dim"], cfg["vocabSize"], self.model_embedding, self.x.ptr, self.tokens.ptr,
+            self.count.ptr, self.pos.ptr, a0, g0, rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0],
+            cfg["numHeads"] * hd, cfg["numKVHeads"] * hd, rr), "lm head + greedy step")
 
     def embed(self, model, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.int32)
@@ -334,8 +353,7 @@ def generateGGUF(model, promptIds, config=None, callbacks=None):
                 device.check(device.lib.smith_graph_launch(device.ops_ctx(), graph), "graph launch")
             else:
                 e.layers(model, caches, 1)
-                e.lm_head(model, e.x.ptr)
-                e.greedy_step(model)
+                e.head_greedy(model)
             if sync_each:
                 tok = int(e.tokens.numpy()[i])
                 generated.append(tok)
@@ -382,8 +400,7 @@ def _decode_graph(model, e, caches):
     device.check(device.lib.smith_graph_begin(ctx), "graph begin")
     try:
         e.layers(model, caches, 1)
-        e.lm_head(model, e.x.ptr)
-        e.greedy_step(model)
+        e.head_greedy(model)
     finally:
         g = device.lib.smith_graph_end(ctx)
     if not g:

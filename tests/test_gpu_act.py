@@ -201,3 +201,88 @@ def test_lmhead_planes_match_reference(K, N):
     assert O.normwise_rel_err(_get(yb, N), _rms(x, g) @ wd) <= TOL_F32
     device.check(device.lib.smith_lmhead_q4_0_nb(ctx, xb, None, 0.0, nib, dsc, yb, K, N))
     assert O.normwise_rel_err(_get(yb, N), x @ wd) <= TOL_F32
+
+
+def _greedy_state(ctx, dim, wq, wk, count, pos):
+    st = {"x": device.alloc(dim * 4), "toks": device.alloc(64 * 4), "cnt": device.alloc(4), "pos": device.alloc(4),
+          "act": device.alloc(_act_bytes(dim)), "rr": device.alloc((4 + wq + wk) * 4)}
+    device.upload(st["toks"], np.full(64, -7, np.int32))
+    device.upload(st["cnt"], np.array([count], np.int32))
+    device.upload(st["pos"], np.array([pos], np.int32))
+    device.check(device.lib.smith_set_i32(ctx, st["rr"], -1))
+    return st
+
+
+def _greedy_read(st, dim, wq, wk, N, logits):
+    device.sync()
+    return {"toks": device.download(st["toks"], 64 * 4, np.int32), "cnt": device.download(st["cnt"], 4, np.int32),
+            "pos": device.download(st["pos"], 4, np.int32), "x": device.download(st["x"], dim * 4, np.float32),
+            "act": device.download(st["act"], _act_bytes(dim), np.uint8),
+            "rr": device.download(st["rr"], (4 + wq + wk) * 4, np.uint8),
+            "logits": device.download(logits, N * 4, np.float32)}
+
+
+@pytest.mark.parametrize("K,N,case", [(1024, 32000, "ties"), (1024, 32000, "nan0"), (1024, 32000, "nan5"),
+                                      (200, 96, "ties"), (3072, 4096, "plain")])
+def test_lmhead_greedy_matches_two_step(K, N, case):
+    """smith_lmhead_q4_0_greedy == smith_lmhead_q4_0_nb then
+    smith_argmax_embed, bit for bit (logits, token, count, position, x, its
+    act, rope row), on two calls in a row.  "ties": vocab blocks copied to
+    a later block of the same 512-column tile and of another tile, with a
+    dominant column, so equal maxima sit in three tiles and the first must
+    win; "nan0": a NaN scale in block 0 (logits 0..31 NaN, the reference's
+    scan returns 0); "nan5": NaNs in block 5 only (skipped)."""
+    nh, hd = 4, 8
+    wq, wk = nh * hd, 2 * hd
+    w = prng.randn((K, N), 71, std=0.02)
+    xs = [prng.randn((K,), 72), prng.randn((K,), 73)]
+    if case == "ties":
+        w[:, 32 * 1 + 5] = 0.06 * np.sign(xs[0])
+        nb = N // 32
+        for b in (2, nb - 1):
+            w[:, 32 * b:32 * b + 32] = w[:, 32:64]
+    blocks = O.quantize_rows(O.GGML_Q4_0, w)
+    if case in ("nan0", "nan5"):
+        b = 0 if case == "nan0" else 5
+        view = blocks.reshape(K, N // 32, 18)
+        view[K // 2, b, 0:2] = np.frombuffer(np.array([0x7E00], np.uint16).tobytes(), np.uint8)
+    ctx = device.ops_ctx()
+    src = device.alloc(blocks.size)
+    device.upload(src, blocks)
+    nib, dsc = device.alloc(K * N // 2), device.alloc(K * N // 16)
+    device.check(device.lib.smith_repack_lmhead_q4_0(ctx, src, nib, dsc, K, N))
+    E = device.alloc(N * K * 4)
+    device.check(device.lib.smith_randn(ctx, E, N * K, 74, 0, 1.0, 0.0))
+    g = _buf(1 + prng.randn((K,), 75, std=0.1))
+    gout = _buf(1 + prng.randn((K,), 76, std=0.1))
+    rope_len = 64 * hd // 2 * nh
+    cos, sin = _buf(prng.randn((rope_len,), 77)), _buf(prng.randn((rope_len,), 78))
+    xin = device.alloc(K * 4)
+    la, lb = device.alloc(N * 4), device.alloc(N * 4)
+    sa = _greedy_state(ctx, K, wq, wk, 3, 20)
+    sb = _greedy_state(ctx, K, wq, wk, 3, 20)
+    act = sa["act"] if K % 32 == 0 else None
+    actb = sb["act"] if K % 32 == 0 else None
+    for call, xv in enumerate(xs):
+        device.upload(xin, xv.astype(np.float32))
+        device.check(device.lib.smith_lmhead_q4_0_nb(ctx, xin, g, EPS, nib, dsc, la, K, N))
+        device.check(device.lib.smith_argmax_embed(ctx, la, N, E, K, sa["x"], sa["toks"], sa["cnt"], sa["pos"], act,
+                                                   gout, cos, sin, rope_len, wq, wk, sa["rr"]))
+        device.check(device.lib.smith_lmhead_q4_0_greedy(ctx, xin, g, EPS, nib, dsc, lb, K, N, E, sb["x"],
+                                                         sb["toks"], sb["cnt"], sb["pos"], actb, gout, cos, sin,
+                                                         rope_len, wq, wk, sb["rr"]))
+        ra, rb = _greedy_read(sa, K, wq, wk, N, la), _greedy_read(sb, K, wq, wk, N, lb)
+        for k in ra:
+            assert np.array_equal(ra[k].view(np.uint8), rb[k].view(np.uint8)), (call, k)
+        lg = ra["logits"].astype(np.float64)
+        tok = int(rb["toks"][3 + call])
+        if case == "nan0":
+            assert tok == 0
+        else:
+            finite = np.where(np.isnan(lg), -np.inf, lg)
+            assert tok == int(np.argmax(finite)), (call, tok)
+        if case == "ties" and call == 0:
+            assert tok == 32 + 5 and lg[32 + 5] == lg[64 + 5] == lg[N - 32 + 5]
+        assert rb["cnt"][0] == 4 + call and rb["pos"][0] == 21 + call
+        Eh = device.download(E, K * 4, np.float32, offset=tok * K * 4)
+        assert np.array_equal(rb["x"], Eh)
