@@ -343,21 +343,24 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_cached(ATT_ARG
 // flash_attention.js:34-70 / flash_attention.metal, which gguf_cache.js:213
 // runs on the prefill rows): S query rows at positions p0 .. p0+S-1, every
 // key row 0 .. p0+s already in the caches (smith_kv_append ran first).
-// Workgroup (h, qb): head h, query rows 64*qb .. +63, one wave per 16 rows.
-// The roped queries sit in LDS; K and V tiles of 64 keys are staged in LDS;
-// per wave S = Q K^T with v_mfma_f32_16x16x4_f32 (f32 operands, exact
-// products, f32 sums -- the reference's arithmetic type), scale, causal mask,
-// online softmax per row (running max m, sum l), P through LDS into the
-// A-operand layout, O += P V on the same MFMA.  hd % 16 == 0, hd <= 128.
+// Workgroup (h, qb): head h, query rows 16*qb .. +15 (roped, in LDS).  K and
+// V tiles of 64 keys are staged in LDS; wave w takes keys 16w .. 16w+15 of
+// every tile, so the four waves split the key range and each keeps its own
+// online softmax (running max m, sum l, O) for the 16 rows: S = Q K^T with
+// v_mfma_f32_16x16x4_f32 (f32 operands, exact products, f32 sums -- the
+// reference's arithmetic type), scale, causal mask, P through LDS into the
+// A-operand layout, O += P V on the same MFMA.  At the end the four
+// partials are combined in LDS: out = sum_w e^(m_w - M) O_w / sum_w e^(m_w - M) l_w.
+// hd % 16 == 0, hd <= 128.
 // MFMA 16x16x4 f32 layout: lane (c = lane % 16, j = lane / 16) supplies
 // A[row c][k j] and B[k j][col c] and holds D rows 4j .. 4j+3 of column c.
 // ---------------------------------------------------------------------------
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-#define FA_BQ 64
+#define FA_BQ 16
 #define FA_BK 64
 #define FA_QS 132  // Q / K row stride (floats): A/B reads of 16 rows x 4 k hit 64 banks
 #define FA_VS 144  // V row stride: B reads of 4 keys x 16 columns hit 64 banks
-#define FA_PS 68   // P row stride
+#define FA_PS 20   // P row stride: A reads of 16 rows x 4 keys hit 64 banks
 
 template <int NT>  // head_dim / 16
 __device__ __forceinline__ void attention_prefill_body(
@@ -366,9 +369,11 @@ __device__ __forceinline__ void attention_prefill_body(
     const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out) {
   constexpr uint32_t hd = 16 * NT;
   __shared__ __attribute__((aligned(16))) float Qs[FA_BQ * FA_QS];
-  __shared__ __attribute__((aligned(16))) float Ks[FA_BK * FA_QS];
-  __shared__ __attribute__((aligned(16))) float Vs[FA_BK * FA_VS];
+  __shared__ __attribute__((aligned(16))) float KV[FA_BK * FA_QS + FA_BK * FA_VS];  // then the waves' O
   __shared__ float Ps[4][16 * FA_PS];
+  __shared__ float MLs[4][2][16];
+  float* Ks = KV;
+  float* Vs = KV + FA_BK * FA_QS;
   const uint32_t h = blockIdx.x, s0 = blockIdx.y * FA_BQ;
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint32_t c = lane & 15, j = lane >> 4;
@@ -384,10 +389,7 @@ __device__ __forceinline__ void attention_prefill_body(
     if (r < nrow) v = rope_elem(qkv + (size_t)(s0 + r) * ld, Wq, h * hd + e, p0 + s0 + r, cosT, sinT);
     Qs[r * FA_QS + e] = v;
   }
-  // this wave's rows and their key range
-  const uint32_t wr0 = s0 + 16 * w;                    // first row of the wave
-  const uint32_t wlast = p0 + (wr0 + 15 < S ? wr0 + 15 : (S > 0 ? S - 1 : 0));  // last key any of them sees
-  const uint32_t Tend = p0 + (s0 + nrow - 1) + 1;      // keys of the block: 0 .. Tend-1
+  const uint32_t Tend = p0 + s0 + nrow;  // keys of the block: 0 .. Tend-1
   f32x4_t o[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) o[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
@@ -400,8 +402,9 @@ __device__ __forceinline__ void attention_prefill_body(
   const float* kb = kcache + (size_t)kvh * maxSeq * hd;
   const float* vb = vcache + (size_t)kvh * maxSeq * hd;
   const uint32_t c4n = hd / 4;
+  float* P = Ps[w];
   for (uint32_t t0 = 0; t0 < Tend; t0 += FA_BK) {
-    __syncthreads();  // previous tile's K/V/P reads done (and, first time, Qs written)
+    __syncthreads();  // previous tile's K/V reads done (and, first time, Qs written)
     // 2. K and V tile (rows past Tend zero: their P is 0 and V must be finite)
     for (uint32_t i = tid; i < FA_BK * c4n; i += 256) {
       const uint32_t r = i / c4n, c4 = i % c4n, t = t0 + r;
@@ -414,81 +417,79 @@ __device__ __forceinline__ void attention_prefill_body(
       *(float4*)&Vs[r * FA_VS + 4 * c4] = vv;
     }
     __syncthreads();
-    if (t0 > wlast || wr0 >= S) continue;  // every key of this tile is after every row of the wave
-    // 3. scores of the wave's 16 rows against the tile's 64 keys
-    f32x4_t sc[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; kt++) sc[kt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const uint32_t k0 = t0 + 16 * w;  // this wave's 16 keys
+    if (k0 >= Tend) continue;         // after every row of the block
+    // 3. scores of the 16 rows against the wave's 16 keys
+    f32x4_t sc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-    for (uint32_t kk = 0; kk < hd; kk += 4) {
-      const float a = Qs[(16 * w + c) * FA_QS + kk + j];
-#pragma unroll
-      for (int kt = 0; kt < 4; kt++)
-        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Ks[(kt * 16 + c) * FA_QS + kk + j], sc[kt], 0, 0, 0);
-    }
-    // 4. online softmax per row (row 4j + r of the wave: lanes of group j)
-    float mx[4];
+    for (uint32_t kk = 0; kk < hd; kk += 4)
+      sc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[c * FA_QS + kk + j], Ks[(16 * w + c) * FA_QS + kk + j], sc, 0, 0,
+                                                0);
+    // 4. online softmax per row (row 4j + r: the 16 lanes of group j)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const uint32_t pos = p0 + wr0 + 4 * j + r;
-      float v = -__builtin_inff();
-#pragma unroll
-      for (int kt = 0; kt < 4; kt++) {
-        const uint32_t t = t0 + 16 * kt + c;
-        const float sv = t <= pos ? sc[kt][r] * scale : -__builtin_inff();
-        sc[kt][r] = sv;
-        v = sv > v ? sv : v;
-      }
+      const uint32_t pos = p0 + s0 + 4 * j + r;
+      const float sv = k0 + c <= pos ? sc[r] * scale : -__builtin_inff();
+      float v = sv;
 #pragma unroll
       for (int d = 1; d < 16; d <<= 1) {
         const float u = __shfl_xor(v, d);
         v = u > v ? u : v;
       }
-      mx[r] = v;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float mn = mx[r] > m[r] ? mx[r] : m[r];  // finite: key 0 is in the first tile of every row
+      const float mn = v > m[r] ? v : m[r];  // -inf while every key so far is masked for this row
       const float alpha = m[r] == -__builtin_inff() ? 0.f : __expf(m[r] - mn);
-      float rs = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; kt++) {
-        const float pv = sc[kt][r] == -__builtin_inff() ? 0.f : __expf(sc[kt][r] - mn);
-        sc[kt][r] = pv;
-        rs += pv;
-      }
+      const float pv = sv == -__builtin_inff() ? 0.f : __expf(sv - mn);
+      float rs = pv;
 #pragma unroll
       for (int d = 1; d < 16; d <<= 1) rs += __shfl_xor(rs, d);
       l[r] = __builtin_fmaf(l[r], alpha, rs);
       m[r] = mn;
 #pragma unroll
       for (int t = 0; t < NT; t++) o[t][r] *= alpha;
+      P[(4 * j + r) * FA_PS + c] = pv;
     }
-    // 5. P to LDS (row-major 16 x 64), read back as the A operand of P V
-    float* P = Ps[w];
-#pragma unroll
-    for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) P[(4 * j + r) * FA_PS + 16 * kt + c] = sc[kt][r];
+    // 5. P (16 rows x 16 keys) read back as the A operand of P V
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-#pragma unroll 4
-    for (uint32_t kk = 0; kk < FA_BK; kk += 4) {
+#pragma unroll
+    for (uint32_t kk = 0; kk < 16; kk += 4) {
       const float a = P[c * FA_PS + kk + j];
 #pragma unroll
       for (int t = 0; t < NT; t++)
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Vs[(kk + j) * FA_VS + 16 * t + c], o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Vs[(16 * w + kk + j) * FA_VS + 16 * t + c], o[t], 0, 0, 0);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // P reads done before the next tile's P writes
+    __builtin_amdgcn_wave_barrier();
   }
-  // 6. out = O / l
+  // 6. combine the waves' partials: out = sum_w e^(m_w - M) O_w / sum_w e^(m_w - M) l_w
+  __syncthreads();  // every wave is done with the K/V tile: KV holds the O partials now
+  float* Os = KV;
+  if (c == 0)
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const uint32_t s = wr0 + 4 * j + r;
-    if (s >= S) continue;
-    const float inv = 1.0f / l[r];
+    for (int r = 0; r < 4; r++) {
+      MLs[w][0][4 * j + r] = m[r];
+      MLs[w][1][4 * j + r] = l[r];
+    }
 #pragma unroll
-    for (int t = 0; t < NT; t++) out[(size_t)s * Wq + h * hd + 16 * t + c] = o[t][r] * inv;
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) Os[(w * 16 + 4 * j + r) * hd + 16 * t + c] = o[t][r];
+  __syncthreads();
+  for (uint32_t i = tid; i < nrow * hd; i += 256) {
+    const uint32_t r = i / hd, e = i % hd;
+    float M = MLs[0][0][r];
+#pragma unroll
+    for (int ww = 1; ww < 4; ww++) M = MLs[ww][0][r] > M ? MLs[ww][0][r] : M;  // finite: key 0 is in wave 0
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ww++) {
+      const float mw = MLs[ww][0][r];
+      const float f = mw == -__builtin_inff() ? 0.f : __expf(mw - M);
+      den = __builtin_fmaf(f, MLs[ww][1][r], den);
+      num = __builtin_fmaf(f, Os[(ww * 16 + r) * hd + e], num);
+    }
+    out[(size_t)(s0 + r) * Wq + h * hd + e] = num / den;
   }
 }
 

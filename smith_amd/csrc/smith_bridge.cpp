@@ -1274,7 +1274,8 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   if (!S) return 0;
   if (S > 1 && head_dim % 16 == 0) {
     // prompt rows: rope + append every row's key/value, then flash attention
-    // on the f32 matrix cores over the caches (64 query rows per workgroup)
+    // on the f32 matrix cores over the caches (16 query rows per workgroup,
+    // its four waves splitting the keys)
     uint32_t Wq = n_heads * head_dim;
     void* aargs[] = {&qkv, &ld, &pos_ptr, &Wq, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &kcache, &vcache,
                      &max_seq};
@@ -1283,7 +1284,7 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
                      &kcache, &vcache, &max_seq, &out};
     char name[48];
     snprintf(name, sizeof name, "smith_attention_prefill_hd%u", head_dim / 16);
-    return launch(c, name, dim3(n_heads, (S + 63) / 64), dim3(256), fargs);
+    return launch(c, name, dim3(n_heads, (S + 15) / 16), dim3(256), fargs);
   }
   const uint32_t nsplit = 8;  // ATT_SPLIT in llama_kernels.hip
   size_t slots = (size_t)S * n_heads;
