@@ -700,42 +700,19 @@ DEF_GEMM2_FMT(q50t, GT_Q50)
 DEF_GEMM2_FMT(q4kt, GT_Q4K)
 DEF_GEMM2_FMT(q6kt, GT_Q6K)
 
+template <bool PERM>
+__device__ __forceinline__ void prep_a_row(const float* __restrict__ A, const float* __restrict__ gamma, float eps,
+                                           _Float16* __restrict__ A16, uint32_t K);
+
 // A16 as smith_gemm_prep_a, with each 8-element chunk in the slot order
 // {0,4,1,5,2,6,3,7} of the gemm2 weight conversion.
 extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a_perm(const float* __restrict__ A,
                                                                         const float* __restrict__ gamma, float eps,
                                                                         _Float16* __restrict__ A16, uint32_t K) {
-  __shared__ float red[4];
-  const uint32_t m = blockIdx.x, tid = threadIdx.x;
-  const float* a = A + (size_t)m * K;
-  float rms = 1.f;
-  if (gamma) {
-    float ss = 0.f;
-    for (uint32_t k = 4 * tid; k < K; k += 1024) {
-      const float4 v = *(const float4*)(a + k);
-      ss = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, ss))));
-    }
-    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    rms = 1.0f / __builtin_sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
-  }
-  for (uint32_t k = 8 * tid; k < K; k += 2048) {
-    float4 v0 = *(const float4*)(a + k), v1 = *(const float4*)(a + k + 4);
-    if (gamma) {
-      const float4 g0 = *(const float4*)(gamma + k), g1 = *(const float4*)(gamma + k + 4);
-      v0 = make_float4(v0.x * rms * g0.x, v0.y * rms * g0.y, v0.z * rms * g0.z, v0.w * rms * g0.w);
-      v1 = make_float4(v1.x * rms * g1.x, v1.y * rms * g1.y, v1.z * rms * g1.z, v1.w * rms * g1.w);
-    }
-    // slots (0,4) (1,5) (2,6) (3,7)
-    uint4 o;
-    o.x = pack_h2(v0.x, v1.x);
-    o.y = pack_h2(v0.y, v1.y);
-    o.z = pack_h2(v0.z, v1.z);
-    o.w = pack_h2(v0.w, v1.w);
-    *(uint4*)(A16 + (size_t)m * K + k) = o;
-  }
+  prep_a_row<true>(A, gamma, eps, A16, K);
 }
+
+#define RED_BATCH 8
 
 extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint32_t ks, float* __restrict__ C,
                                              uint32_t M, uint32_t N, const float* __restrict__ R, uint32_t epi) {
@@ -745,14 +722,29 @@ extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint3
     if (epi == 2) {
       const size_t i = 2 * o;  // (gate, up) at columns 2c, 2c+1 of one row
       float g = 0.f, u = 0.f;
-      for (uint32_t y = 0; y < ks; y++) {
-        g += ws[y * MN + i];
-        u += ws[y * MN + i + 1];
+      for (uint32_t y0 = 0; y0 < ks; y0 += RED_BATCH) {  // a batch of split reads in flight, summed in order
+        float2 t[RED_BATCH];
+#pragma unroll
+        for (uint32_t b = 0; b < RED_BATCH; b++)
+          t[b] = y0 + b < ks ? *(const float2*)(ws + (y0 + b) * MN + i) : make_float2(0.f, 0.f);
+#pragma unroll
+        for (uint32_t b = 0; b < RED_BATCH; b++)
+          if (y0 + b < ks) {
+            g += t[b].x;
+            u += t[b].y;
+          }
       }
       C[o] = silu_mul_g(g, u);
     } else {
       float v = 0.f;
-      for (uint32_t y = 0; y < ks; y++) v += ws[y * MN + o];
+      for (uint32_t y0 = 0; y0 < ks; y0 += RED_BATCH) {
+        float t[RED_BATCH];
+#pragma unroll
+        for (uint32_t b = 0; b < RED_BATCH; b++) t[b] = y0 + b < ks ? ws[(y0 + b) * MN + o] : 0.f;
+#pragma unroll
+        for (uint32_t b = 0; b < RED_BATCH; b++)
+          if (y0 + b < ks) v += t[b];
+      }
       C[o] = epi == 1 ? R[o] + v : v;
     }
   }
@@ -760,33 +752,91 @@ extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint3
 
 // A16[m][k] = f16(A[m][k] * rms_m * gamma[k]) (gamma != null: RMSNorm,
 // rmsnorm.metal:15-47) or f16(A[m][k]).  One workgroup per row, 256 threads.
-extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a(const float* __restrict__ A,
-                                                                   const float* __restrict__ gamma, float eps,
-                                                                   _Float16* __restrict__ A16, uint32_t K) {
+// One row of A (blockIdx.x) to f16 by 256 threads, in chunks of 8192
+// elements: every load of a chunk is issued before the first is used, and a
+// row of <= 8192 elements is read once (norm and conversion from registers).
+// PERM: each thread takes 8 consecutive elements and writes them in the slot
+// order {0,4,1,5,2,6,3,7}; else 4 consecutive elements.  K % 8 == 0.
+template <bool PERM>
+__device__ __forceinline__ void prep_a_row(const float* __restrict__ A, const float* __restrict__ gamma, float eps,
+                                           _Float16* __restrict__ A16, uint32_t K) {
+  constexpr uint32_t CH = 8192, U = 8;  // 8 float4 per thread per chunk
   __shared__ float red[4];
   const uint32_t m = blockIdx.x, tid = threadIdx.x;
   const float* a = A + (size_t)m * K;
+  _Float16* d = A16 + (size_t)m * K;
+  // element offset of float4 u of this thread within a chunk
+  auto off = [&](uint32_t u) -> uint32_t { return PERM ? 8 * tid + 2048 * (u / 2) + 4 * (u % 2) : 4 * tid + 1024 * u; };
+  float4 v[U];
+  auto load = [&](uint32_t base) {
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t k = base + off(u);
+      v[u] = k < K ? *(const float4*)(a + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto store = [&](uint32_t base, float rms) {
+    float4 g[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t k = base + off(u);
+      g[u] = gamma && k < K ? *(const float4*)(gamma + k) : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      v[u] = gamma ? make_float4(v[u].x * rms * g[u].x, v[u].y * rms * g[u].y, v[u].z * rms * g[u].z,
+                                 v[u].w * rms * g[u].w)
+                   : v[u];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; u += PERM ? 2 : 1) {
+      const uint32_t k = base + off(u);
+      if (k >= K) continue;
+      if (PERM) {  // slots (0,4) (1,5) (2,6) (3,7)
+        uint4 o;
+        o.x = pack_h2(v[u].x, v[u + 1].x);
+        o.y = pack_h2(v[u].y, v[u + 1].y);
+        o.z = pack_h2(v[u].z, v[u + 1].z);
+        o.w = pack_h2(v[u].w, v[u + 1].w);
+        *(uint4*)(d + k) = o;
+      } else {
+        uint2 o;
+        o.x = pack_h2(v[u].x, v[u].y);
+        o.y = pack_h2(v[u].z, v[u].w);
+        *(uint2*)(d + k) = o;
+      }
+    }
+  };
+  auto sumsq = [&]() {
+    float ss = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++)
+      ss = __builtin_fmaf(v[u].x, v[u].x,
+                          __builtin_fmaf(v[u].y, v[u].y, __builtin_fmaf(v[u].z, v[u].z, __builtin_fmaf(v[u].w, v[u].w, ss))));
+    return ss;
+  };
+  load(0);
   float rms = 1.f;
   if (gamma) {
-    float ss = 0.f;
-    for (uint32_t k = 4 * tid; k < K; k += 1024) {
-      const float4 v = *(const float4*)(a + k);
-      ss = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.w, v.w, ss))));
+    float ss = sumsq();
+    for (uint32_t base = CH; base < K; base += CH) {  // rows past one chunk: a first pass for the norm
+      load(base);
+      ss += sumsq();
     }
-    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+    for (int dd = 32; dd >= 1; dd >>= 1) ss += __shfl_xor(ss, dd);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     rms = 1.0f / __builtin_sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
+    if (K > CH) load(0);
   }
-  for (uint32_t k = 4 * tid; k < K; k += 1024) {
-    float4 v = *(const float4*)(a + k);
-    if (gamma) {
-      const float4 g = *(const float4*)(gamma + k);
-      v = make_float4(v.x * rms * g.x, v.y * rms * g.y, v.z * rms * g.z, v.w * rms * g.w);
-    }
-    uint2 o;
-    o.x = pack_h2(v.x, v.y);
-    o.y = pack_h2(v.z, v.w);
-    *(uint2*)(A16 + (size_t)m * K + k) = o;
+  for (uint32_t base = 0; base < K; base += CH) {
+    if (base) load(base);
+    store(base, rms);
   }
+}
+
+extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a(const float* __restrict__ A,
+                                                                   const float* __restrict__ gamma, float eps,
+                                                                   _Float16* __restrict__ A16, uint32_t K) {
+  prep_a_row<false>(A, gamma, eps, A16, K);
 }

@@ -209,7 +209,9 @@ def _greedy_state(ctx, dim, wq, wk, count, pos):
     device.upload(st["toks"], np.full(64, -7, np.int32))
     device.upload(st["cnt"], np.array([count], np.int32))
     device.upload(st["pos"], np.array([pos], np.int32))
-    device.check(device.lib.smith_set_i32(ctx, st["rr"], -1))
+    row = np.zeros(4 + wq + wk, np.float32)
+    row[:1] = np.array([-1], np.int32).view(np.float32)  # no position yet; header pads stay zero
+    device.upload(st["rr"], row)
     return st
 
 
