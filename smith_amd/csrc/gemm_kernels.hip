@@ -107,7 +107,29 @@ __device__ __forceinline__ WRec load_wrec(const uint8_t* __restrict__ B, const u
   return r;
 }
 
-// the 32 dequantized weights of a record as 16 packed f16 pairs (k order)
+// Q4 records (Q4S, Q4_0: w = s * (q - z)) in packed f16: elements 16h ..
+// 16h+15 as 8 f16 pairs, each 8-element chunk in the slot order
+// {0,4,1,5,2,6,3,7} (A is prepared in the same order).  Nibbles b and b+4 of
+// a dword land in the low mantissa bits of 0x6400 (f16 1024 + q, exact),
+// 1024 comes off exactly, and one fma applies the scale and -scale*zero
+// (both rounded to f16; the product is exact inside the fma).
+__device__ __forceinline__ void q4_pairs(const WRec& r, uint32_t h, uint32_t (&o)[8]) {
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  const _Float16 sh = (_Float16)r.s, ch = (_Float16)(-r.s * r.z);
+  const h2v s2 = {sh, sh}, c2 = {ch, ch}, k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const uint32_t d[2] = {h ? r.q.z : r.q.x, h ? r.q.w : r.q.y};
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const uint32_t u = ((d[i] >> (4 * b)) & 0x000F000Fu) | 0x64006400u;
+      const h2v q = __builtin_bit_cast(h2v, u) - k1024;
+      o[4 * i + b] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, s2, c2));
+    }
+  }
+}
+
+// the 32 dequantized weights of a record as 16 packed f16 pairs (k order; Q4 formats in the slot order of q4_pairs)
 template <int FMT>
 __device__ __forceinline__ void dequant_wrec(const WRec& r, uint32_t (&o)[16]) {
   if constexpr (FMT >= GT_Q41) {
@@ -137,16 +159,13 @@ __device__ __forceinline__ void dequant_wrec(const WRec& r, uint32_t (&o)[16]) {
       o[2 * i + 1] = pack_h2(r.s * v2, r.s * v3);
     }
   } else {
-    const float c = -r.s * r.z;
-    const uint32_t d[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    uint32_t a[8], b[8];
+    q4_pairs(r, 0, a);
+    q4_pairs(r, 1, b);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t lo = d[i] & 0x0F0F0F0Fu, hi = (d[i] >> 4) & 0x0F0F0F0Fu;  // byte b: elements 2b / 2b+1
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        const float ql = (float)((lo >> (8 * b)) & 0xFFu), qh = (float)((hi >> (8 * b)) & 0xFFu);
-        o[4 * i + b] = pack_h2(__builtin_fmaf(ql, r.s, c), __builtin_fmaf(qh, r.s, c));
-      }
+    for (int i = 0; i < 8; i++) {
+      o[i] = a[i];
+      o[8 + i] = b[i];
     }
   }
 }
@@ -174,17 +193,7 @@ __device__ __forceinline__ void dequant_half(const WRec& r, uint32_t h, uint32_t
       o[2 * ii + 1] = pack_h2(r.s * v2, r.s * v3);
     }
   } else {
-    const float c = -r.s * r.z;
-    const uint32_t d[2] = {h ? r.q.z : r.q.x, h ? r.q.w : r.q.y};
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const uint32_t lo = d[i] & 0x0F0F0F0Fu, hi = (d[i] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-      for (int b = 0; b < 4; b++) {
-        const float ql = (float)((lo >> (8 * b)) & 0xFFu), qh = (float)((hi >> (8 * b)) & 0xFFu);
-        o[4 * i + b] = pack_h2(__builtin_fmaf(ql, r.s, c), __builtin_fmaf(qh, r.s, c));
-      }
-    }
+    q4_pairs(r, h, o);
   }
 }
 

@@ -406,7 +406,10 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
     void* pd = c->a16;
     uint32_t pK = K;
     void* args[] = {&pa, &pg, &pe, &pd, &pK};
-    if (launch(c, g2 ? "smith_gemm_prep_a_perm" : "smith_gemm_prep_a", dim3(M), dim3(256), args)) return -1;
+    // the DMA-staged kernels and the register-staged Q4S / Q4_0 ones take A
+    // in the permuted slot order of their packed-f16 weight conversion
+    const bool perm = g2 || fmt == FQ4S || fmt == FQ40 || fmt == FQ40T;
+    if (launch(c, perm ? "smith_gemm_prep_a_perm" : "smith_gemm_prep_a", dim3(M), dim3(256), args)) return -1;
   }
   // tile choice: the biggest tile that still gives about one tile per CU
   // (bigger tiles carry more MFMA work per K stage to cover load latency);
