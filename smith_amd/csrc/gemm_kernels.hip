@@ -723,15 +723,51 @@ extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a_perm(const f
 
 #define RED_BATCH 8
 
+// Sum of the K-split partials in split order (deterministic), then the
+// epilogue: 2 = SwiGLU of the (gate, up) column pairs, 1 = + residual.
+// Four consecutive partials per thread with 16-byte loads when the sizes
+// and pointers allow it, else one per thread.
 extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint32_t ks, float* __restrict__ C,
                                              uint32_t M, uint32_t N, const float* __restrict__ R, uint32_t epi) {
   const size_t MN = (size_t)M * N;
   const size_t nout = epi == 2 ? MN / 2 : MN;
-  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < nout; o += (size_t)gridDim.x * blockDim.x) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const bool vec = (MN & 3) == 0 && ((size_t)C & (epi == 2 ? 7 : 15)) == 0 && ((size_t)ws & 15) == 0 &&
+                   (epi != 1 || ((size_t)R & 15) == 0);
+  if (vec) {
+    for (size_t qd = (size_t)blockIdx.x * blockDim.x + threadIdx.x; 4 * qd < MN; qd += stride) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (uint32_t y0 = 0; y0 < ks; y0 += RED_BATCH) {  // a batch of split reads in flight, summed in order
+        float4 t[RED_BATCH];
+#pragma unroll
+        for (uint32_t b = 0; b < RED_BATCH; b++)
+          t[b] = y0 + b < ks ? *(const float4*)(ws + (y0 + b) * MN + 4 * qd) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (uint32_t b = 0; b < RED_BATCH; b++)
+          if (y0 + b < ks) {
+            v.x += t[b].x;
+            v.y += t[b].y;
+            v.z += t[b].z;
+            v.w += t[b].w;
+          }
+      }
+      if (epi == 2) {  // (gate, up) at columns 2c, 2c+1 of one row
+        *(float2*)(C + 2 * qd) = make_float2(silu_mul_g(v.x, v.y), silu_mul_g(v.z, v.w));
+      } else {
+        if (epi == 1) {
+          const float4 r = *(const float4*)(R + 4 * qd);
+          v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+        }
+        *(float4*)(C + 4 * qd) = v;
+      }
+    }
+    return;
+  }
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < nout; o += stride) {
     if (epi == 2) {
       const size_t i = 2 * o;  // (gate, up) at columns 2c, 2c+1 of one row
       float g = 0.f, u = 0.f;
-      for (uint32_t y0 = 0; y0 < ks; y0 += RED_BATCH) {  // a batch of split reads in flight, summed in order
+      for (uint32_t y0 = 0; y0 < ks; y0 += RED_BATCH) {
         float2 t[RED_BATCH];
 #pragma unroll
         for (uint32_t b = 0; b < RED_BATCH; b++)
@@ -760,8 +796,8 @@ extern "C" __global__ void smith_gemm_reduce(const float* __restrict__ ws, uint3
 }
 
 // A16[m][k] = f16(A[m][k] * rms_m * gamma[k]) (gamma != null: RMSNorm,
-// rmsnorm.metal:15-47) or f16(A[m][k]).  One workgroup per row, 256 threads.
-// One row of A (blockIdx.x) to f16 by 256 threads, in chunks of 8192
+// rmsnorm.metal:15-47) or f16(A[m][k]).  One row of A (blockIdx.x) to f16
+// by 256 threads, in chunks of 8192
 // elements: every load of a chunk is issued before the first is used, and a
 // row of <= 8192 elements is read once (norm and conversion from registers).
 // PERM: each thread takes 8 consecutive elements and writes them in the slot

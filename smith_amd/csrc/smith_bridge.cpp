@@ -458,8 +458,8 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
   const float* cws = c->ws;
   uint32_t pks = ks;
   void* rargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi};
-  size_t nout = (size_t)M * N / (ep.mode == 2 ? 2 : 1);
-  return launch(c, "smith_gemm_reduce", dim3((unsigned)std::min<size_t>((nout + 255) / 256, 65536)), dim3(256), rargs);
+  const size_t per = (size_t)M * N % 4 == 0 ? (size_t)M * N / 4 : (size_t)M * N / (ep.mode == 2 ? 2 : 1);
+  return launch(c, "smith_gemm_reduce", dim3((unsigned)std::min<size_t>((per + 255) / 256, 65536)), dim3(256), rargs);
 }
 
 int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,

@@ -243,7 +243,7 @@ def test_config4_prefill_gemm(N, K):
 
 # ---------------- M >= 256: 256x256 tiles with K splits ----------------
 
-@pytest.mark.parametrize("M,K,N", [(300, 4096, 300), (257, 1024, 520), (512, 14336, 96)])
+@pytest.mark.parametrize("M,K,N", [(300, 4096, 300), (257, 1024, 520), (512, 14336, 96), (257, 2048, 18)])
 def test_gemm_big_tiles_ragged(M, K, N):
     """M >= 256 runs 256x256 tiles with enough K splits to fill the chip
     (8 / 2 / 8 splits here) over ragged row and column tiles, Q4S and Q8."""
