@@ -305,7 +305,9 @@ int smith_randn(void* ctx, float* out, uint64_t n, uint64_t seed, uint64_t offse
 
 /* ---- HIP graphs: capture the context stream, replay it ----
  * Ops enqueued between begin and end are recorded, not run; their scratch
- * must already be allocated (run the same ops once before capturing). */
+ * must already be allocated (run the same ops once before capturing).
+ * Scratch that a later, bigger op replaces stays allocated until
+ * smith_destroy, so a graph captured earlier stays valid. */
 int smith_graph_begin(void* ctx);
 void* smith_graph_end(void* ctx);
 int smith_graph_launch(void* ctx, void* graph);

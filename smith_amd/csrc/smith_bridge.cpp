@@ -65,6 +65,9 @@ struct Ctx {
   uint32_t* att_cnt = nullptr;
   size_t att_cnt_n = 0;
   bool capturing = false;
+  // scratch buffers replaced by bigger ones: a captured graph may still name
+  // them, so they are freed only with the context
+  std::vector<void*> retired;
   // per-launch HIP event pairs of op-level kernels while profiling is on
   bool profile = false;
   struct Rec {
@@ -181,7 +184,7 @@ int ensure(Ctx* c, void** p, size_t* have, size_t need) {
     return fail(c, "smith: scratch of %zu bytes needed while capturing a graph; run the op once before capture",
                 need);
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (*p) HIPCHK(c, hipFree(*p));
+  if (*p) c->retired.push_back(*p);  // a captured graph may still use it
   *p = nullptr;
   *have = 0;
   size_t sz = (need + 0xFFFFF) & ~(size_t)0xFFFFF;
@@ -194,7 +197,7 @@ int ensure_counters(Ctx* c, size_t n) {
   if (n <= c->counters_n) return 0;
   if (c->capturing) return fail(c, "smith: split-K counters needed while capturing a graph; run the op once first");
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  if (c->counters) HIPCHK(c, hipFree(c->counters));
+  if (c->counters) c->retired.push_back(c->counters);  // a captured graph may still use them
   c->counters = nullptr;
   c->counters_n = 0;
   size_t cap = std::max<size_t>(n, 4096);
@@ -547,6 +550,7 @@ void smith_destroy(void* ctx) {
   if (c->ws) hipFree(c->ws);
   if (c->counters) hipFree(c->counters);
   if (c->amx) hipFree(c->amx);
+  for (void* r : c->retired) hipFree(r);
   for (auto& r : c->recs) {
     hipEventDestroy(r.a);
     hipEventDestroy(r.b);
@@ -1295,7 +1299,7 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   if (slots > c->att_cnt_n) {
     if (c->capturing) return fail(c, "smith_attention: counters needed while capturing; run once first");
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    if (c->att_cnt) HIPCHK(c, hipFree(c->att_cnt));
+    if (c->att_cnt) c->retired.push_back(c->att_cnt);  // a captured graph may still use them
     c->att_cnt = nullptr;
     c->att_cnt_n = 0;
     size_t cap = std::max<size_t>(slots, 4096);
