@@ -53,6 +53,17 @@ def test_prefill_and_decode_logits(q4):
         assert normwise_rel_err(g, w) <= TOL, i
 
 
+def test_repeated_prefill_is_deterministic(q4):
+    """The same prompt into the same caches three times: the logits agree
+    bit for bit (fixed split-K and reduction orders), and with the oracle."""
+    m = loadGGUF(q4)
+    prompt = [3, 77, 150, 9, 210, 44, 1, 8, 99]
+    caches = m.createCache()
+    runs = [m.forwardPrefill(prompt, caches)["logits"] for _ in range(3)]
+    assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[0], runs[2])
+    assert normwise_rel_err(runs[2], LO.LlamaOracle(q4).forward(prompt, 0)) <= TOL
+
+
 def test_generate_greedy_graph_and_sync_paths(q4):
     m = loadGGUF(q4)
     prompt = [11, 22, 33, 44, 55]
