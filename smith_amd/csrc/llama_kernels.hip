@@ -539,11 +539,27 @@ DEF_ATT_PREFILL(8)
 #define ATTP_STRIDE 132  // floats per partial: m, l, 2 pad, o[128] (16-byte aligned)
 #define ROPE_ROW_HDR 4   // rope row: int32 position tag, 3 pad, then cos_q, sin_q, cos_k, sin_k
 
+struct AttPShared {
+  float qr[128] __attribute__((aligned(16)));
+  float Kt[ATTP_ROWS][132] __attribute__((aligned(16)));  // 16-byte rows: 4-float reads
+  float Vt[ATTP_ROWS][128] __attribute__((aligned(16)));
+  float sc[ATTP_ROWS] __attribute__((aligned(16)));
+};
+
+// Sum over each aligned group of 8 lanes, left in all 8: two quad
+// permutations and a half-row mirror (DPP moves: ALU latency, no LDS trip).
+__device__ __forceinline__ float sum8_dpp(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));  // half-row mirror
+  return v;
+}
+
 extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     const float* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, uint32_t nH, uint32_t nKV, uint32_t hd,
     const float* __restrict__ cosT, const float* __restrict__ sinT, const float* __restrict__ rrow,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts) {
-  __shared__ AttShared sh;
+  __shared__ AttPShared sh;
   __shared__ float kn[128], vn[128];
   __shared__ float ored[2][128];
   const uint32_t rep = nH / nKV;
@@ -622,10 +638,7 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
           kv = make_float4(kn[4 * c4], kn[4 * c4 + 1], kn[4 * c4 + 2], kn[4 * c4 + 3]);
           vv = make_float4(vn[4 * c4], vn[4 * c4 + 1], vn[4 * c4 + 2], vn[4 * c4 + 3]);
         }
-        sh.Kt[r][4 * c4] = kv.x;
-        sh.Kt[r][4 * c4 + 1] = kv.y;
-        sh.Kt[r][4 * c4 + 2] = kv.z;
-        sh.Kt[r][4 * c4 + 3] = kv.w;
+        *(float4*)&sh.Kt[r][4 * c4] = kv;
         *(float4*)&sh.Vt[r][4 * c4] = vv;
       }
     }
@@ -642,37 +655,57 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
       }
     }
     {
-      const uint32_t r = tid / 8, sub = tid % 8;
+      // score of row r: lanes (r, sub) take elements 16 sub .. 16 sub + 15
+      // (four 16-byte reads of q and of the key row, all issued together)
+      const uint32_t r = tid / 8, sub = tid % 8, c0 = 16 * sub;
       float d = 0.f;
+      if (c0 < hd) {
+        float4 qv[4], kv[4];
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const uint32_t c = sub + 8 * i;
-        if (c < hd) d = __builtin_fmaf(sh.qr[c], sh.Kt[r][c], d);
+        for (int i = 0; i < 4; i++) {
+          qv[i] = *(const float4*)&sh.qr[c0 + 4 * i];
+          kv[i] = *(const float4*)&sh.Kt[r][c0 + 4 * i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (c0 + 4 * i < hd) {  // hd % 4 == 0
+            d = __builtin_fmaf(qv[i].x, kv[i].x, d);
+            d = __builtin_fmaf(qv[i].y, kv[i].y, d);
+            d = __builtin_fmaf(qv[i].z, kv[i].z, d);
+            d = __builtin_fmaf(qv[i].w, kv[i].w, d);
+          }
       }
-      d += __shfl_xor(d, 1);
-      d += __shfl_xor(d, 2);
-      d += __shfl_xor(d, 4);
+      d = sum8_dpp(d);
       if (sub == 0) sh.sc[r] = tb + r <= p0 ? d * scale : -__builtin_inff();
     }
     __syncthreads();
-    const float sl = sh.sc[tid & 31];
-    float tm = sl;
+    // every thread reads the 32 scores (broadcast reads) and forms the
+    // tile's max, weights and weight sum itself
+    float sv[ATTP_ROWS];
 #pragma unroll
-    for (int k = 16; k >= 1; k >>= 1) {
-      const float ov = __shfl_xor(tm, k);
-      tm = ov > tm ? ov : tm;
+    for (int i = 0; i < ATTP_ROWS / 4; i++) {
+      const float4 v4 = *(const float4*)&sh.sc[4 * i];
+      sv[4 * i] = v4.x;
+      sv[4 * i + 1] = v4.y;
+      sv[4 * i + 2] = v4.z;
+      sv[4 * i + 3] = v4.w;
     }
+    const uint32_t ec = ee < hd ? ee : 0;
+    float vv[ATTP_ROWS / 2];
+#pragma unroll
+    for (int rr = 0; rr < ATTP_ROWS / 2; rr++) vv[rr] = sh.Vt[2 * rr + part][ec];
+    float tm = sv[0];
+#pragma unroll
+    for (int i = 1; i < ATTP_ROWS; i++) tm = sv[i] > tm ? sv[i] : tm;
     const float mn = tm > m ? tm : m;
     const float alpha = __expf(m - mn);  // first tile: m = -inf -> 0
-    const float pl = __expf(sl - mn);    // masked rows: exp(-inf) = 0
-    float ps = pl;
-#pragma unroll
-    for (int k = 16; k >= 1; k >>= 1) ps += __shfl_xor(ps, k);
-    float acc = 0.f;
+    float ps = 0.f, acc = 0.f;
 #pragma unroll
     for (int rr = 0; rr < ATTP_ROWS / 2; rr++) {
-      const uint32_t row = 2 * rr + part;
-      acc = __builtin_fmaf(__shfl(pl, (int)row), sh.Vt[row][ee < hd ? ee : 0], acc);
+      const float p0e = __expf(sv[2 * rr] - mn), p1e = __expf(sv[2 * rr + 1] - mn);  // masked rows: 0
+      ps += p0e;
+      ps += p1e;
+      acc = __builtin_fmaf(part ? p1e : p0e, vv[rr], acc);
     }
     l = l * alpha + ps;
     o = o * alpha + acc;
