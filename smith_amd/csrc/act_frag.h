@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lanes.h"
+
 __host__ __device__ constexpr size_t act_bytes(uint32_t K) { return (size_t)K * 4 + (size_t)(K / 8) * 12; }
 
 // All 8 lanes of an aligned 8-lane group call this together, lane L holding
@@ -45,12 +47,9 @@ __device__ __forceinline__ void act_emit8(uint8_t* __restrict__ act, uint32_t K,
   float c1 = __builtin_fmaf(lf * off, 1.0f / 2048.0f, hf * off);
   float sm = __builtin_fmaf(lf, 1.0f / 2048.0f, hf);
   float ss = v * v;
-#pragma unroll
-  for (int d = 1; d < 8; d <<= 1) {
-    c1 += __shfl_xor(c1, d);
-    sm += __shfl_xor(sm, d);
-    ss += __shfl_xor(ss, d);
-  }
+  c1 = sum8_lanes(c1);
+  sm = sum8_lanes(sm);
+  ss = sum8_lanes(ss);
   if ((o & 7) == 0) {
     const uint32_t T = K / 8, t = o >> 3;
     float* part = (float*)(act + (size_t)K * 4);

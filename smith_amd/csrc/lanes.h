@@ -1,0 +1,35 @@
+// Cross-lane sums without an LDS round trip: DPP moves for lane ^ 1 / ^ 2 and
+// the 8- and 16-lane groups, v_permlane16_swap / v_permlane32_swap (gfx950)
+// for lane ^ 16 / ^ 32.  Every lane of a group ends with the same value (each
+// step adds a pair of values in an order-independent way).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// v + v of lane ^ 1, lane ^ 2 (DPP quad permutations [1,0,3,2] / [2,3,0,1])
+__device__ __forceinline__ float add_xor1(float v) { return v + dpp_f32<0xB1>(v); }
+__device__ __forceinline__ float add_xor2(float v) { return v + dpp_f32<0x4E>(v); }
+// sum over each aligned group of 8 / 16 lanes (half-row / row mirror last)
+__device__ __forceinline__ float sum8_lanes(float v) {
+  v = add_xor2(add_xor1(v));
+  return v + dpp_f32<0x141>(v);
+}
+__device__ __forceinline__ float sum16_lanes(float v) {
+  v = sum8_lanes(v);
+  return v + dpp_f32<0x140>(v);
+}
+// v + v of lane ^ 16 / lane ^ 32 (the two rows / halves swapped whole)
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+// sum over the whole wave (64 lanes)
+__device__ __forceinline__ float sum64_lanes(float v) { return add_xor32(add_xor16(sum16_lanes(v))); }

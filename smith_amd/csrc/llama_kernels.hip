@@ -546,14 +546,6 @@ struct AttPShared {
   float sc[ATTP_ROWS] __attribute__((aligned(16)));
 };
 
-// Sum over each aligned group of 8 lanes, left in all 8: two quad
-// permutations and a half-row mirror (DPP moves: ALU latency, no LDS trip).
-__device__ __forceinline__ float sum8_dpp(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));   // quad [1,0,3,2]
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));   // quad [2,3,0,1]
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));  // half-row mirror
-  return v;
-}
 
 extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     const float* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, uint32_t nH, uint32_t nKV, uint32_t hd,
@@ -675,7 +667,7 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
             d = __builtin_fmaf(qv[i].w, kv[i].w, d);
           }
       }
-      d = sum8_dpp(d);
+      d = sum8_lanes(d);
       if (sub == 0) sh.sc[r] = tb + r <= p0 ? d * scale : -__builtin_inff();
     }
     __syncthreads();

@@ -345,14 +345,11 @@ __device__ __forceinline__ void qprep_body(const float* __restrict__ A, u32x4* _
   }
   // reduce the four K slices of the group (lanes tid^1, tid^2 are the same
   // row/group because kq is the fastest index)
-#pragma unroll
-  for (int d = 1; d < 4; d <<= 1) {
-    hi_c1 += __shfl_xor(hi_c1, d);
-    hi_s += __shfl_xor(hi_s, d);
-    if (HILO) {
-      lo_c1 += __shfl_xor(lo_c1, d);
-      lo_s += __shfl_xor(lo_s, d);
-    }
+  hi_c1 = add_xor2(add_xor1(hi_c1));
+  hi_s = add_xor2(add_xor1(hi_s));
+  if (HILO) {
+    lo_c1 = add_xor2(add_xor1(lo_c1));
+    lo_s = add_xor2(add_xor1(lo_s));
   }
   if (!active) return;
   uint32_t rb = m / rows_per_rb, r = m % rows_per_rb;
@@ -661,8 +658,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   if (gamma) {
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-      float v = nss[m];
-      for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+      const float v = sum64_lanes(nss[m]);
       if (lane == 0) nred[m][wave] = v;
     }
     __syncthreads();
@@ -709,10 +705,8 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     float c1 = __builtin_fmaf(c1l, 1.0f / 2048.0f, c1h);
     float sm = __builtin_fmaf(sl, 1.0f / 2048.0f, sh_);
     // the four mfma slices of (group, row) are adjacent threads
-    c1 += __shfl_xor(c1, 1);
-    sm += __shfl_xor(sm, 1);
-    c1 += __shfl_xor(c1, 2);
-    sm += __shfl_xor(sm, 2);
+    c1 = add_xor2(add_xor1(c1));
+    sm = add_xor2(add_xor1(sm));
     if (is_q40(FMT)) c1 = __builtin_fmaf(8.0f, sm, c1);
     if (ch < (uint32_t)NCH) {
       u32x4 hp, lp;
@@ -769,8 +763,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 #pragma unroll
     for (int m = 0; m < MR; m++) {
       float v = acc[ct][m];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v = add_xor32(add_xor16(v));
       if (j == 0) red[wk][m][wn * 16 * CT + ct * 16 + c] = v;
     }
   __syncthreads();
@@ -1141,14 +1134,11 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
           sl += lf;
         }
       }
-#pragma unroll
-      for (int d = 1; d < 4; d <<= 1) {
-        c1h += __shfl_xor(c1h, d);
-        sh_ += __shfl_xor(sh_, d);
-        if (HILO) {
-          c1l += __shfl_xor(c1l, d);
-          sl += __shfl_xor(sl, d);
-        }
+      c1h = add_xor2(add_xor1(c1h));
+      sh_ = add_xor2(add_xor1(sh_));
+      if (HILO) {
+        c1l = add_xor2(add_xor1(c1l));
+        sl = add_xor2(add_xor1(sl));
       }
       if (item < (uint32_t)NITEM) {
         u32x4 hp, lp;
@@ -1651,8 +1641,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
 #pragma unroll
   for (int ct = 0; ct < CT; ct++) {
     float v = acc[ct];
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
+    v = add_xor32(add_xor16(v));
     if (j == 0) red[wk][ct * 16 + c] = v;
   }
   __syncthreads();
@@ -1684,8 +1673,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   }
   float rms = 1.0f;
   if (norm) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) ssum += __shfl_xor(ssum, d);
+    ssum = sum64_lanes(ssum);
     rms = 1.0f / __builtin_sqrtf(ssum / (float)K + eps);
   }
   v *= rms;
