@@ -33,3 +33,32 @@ __device__ __forceinline__ float add_xor32(float v) {
 }
 // sum over the whole wave (64 lanes)
 __device__ __forceinline__ float sum64_lanes(float v) { return add_xor32(add_xor16(sum16_lanes(v))); }
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint64_t umax64_pair(uint64_t a, uint32_t hi, uint32_t lo) {
+  const uint64_t b = ((uint64_t)hi << 32) | lo;
+  return a > b ? a : b;
+}
+// maximum of a 64-bit key over the whole wave, in every lane
+__device__ __forceinline__ uint64_t max64_lanes(uint64_t k) {
+#define MAX64_DPP(CTRL) k = umax64_pair(k, dpp_u32<CTRL>((uint32_t)(k >> 32)), dpp_u32<CTRL>((uint32_t)k))
+  MAX64_DPP(0xB1);
+  MAX64_DPP(0x4E);
+  MAX64_DPP(0x141);
+  MAX64_DPP(0x140);
+#undef MAX64_DPP
+  {
+    const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
+    const auto l = __builtin_amdgcn_permlane16_swap((uint32_t)k, (uint32_t)k, false, false);
+    k = umax64_pair(umax64_pair(0, h[0], l[0]), h[1], l[1]);
+  }
+  {
+    const auto h = __builtin_amdgcn_permlane32_swap((uint32_t)(k >> 32), (uint32_t)(k >> 32), false, false);
+    const auto l = __builtin_amdgcn_permlane32_swap((uint32_t)k, (uint32_t)k, false, false);
+    k = umax64_pair(umax64_pair(0, h[0], l[0]), h[1], l[1]);
+  }
+  return k;
+}

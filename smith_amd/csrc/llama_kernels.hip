@@ -779,14 +779,7 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t n) {
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-__device__ __forceinline__ uint64_t wave_max64(uint64_t k) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)k, d), hi = __shfl_xor((uint32_t)(k >> 32), d);
-    k = umax64(k, ((uint64_t)hi << 32) | lo);
-  }
-  return k;
-}
+__device__ __forceinline__ uint64_t wave_max64(uint64_t k) { return max64_lanes(k); }
 
 // The rope row of position np (tag np), written when the tables hold it;
 // threads tid, tid + nt, ... of the caller.
@@ -906,7 +899,7 @@ extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int q = 0; q < 8; q++) ss = __builtin_fmaf(xv[q], xv[q], ss);
     for (uint32_t i = tid + 4096; i < K; i += 512) ss = __builtin_fmaf(x[i], x[i], ss);
-    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+    ss = sum64_lanes(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     float tot = 0.f;
