@@ -929,10 +929,20 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
           bf[t] = __builtin_bit_cast(half8, u);
         }
       }
+      // scale / zero of record (group g+t, column c) from lane group t: the
+      // same 4x4 lane-group transpose with every register holding the own value
+      uint32_t sx[4], zx[4];
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        float s = __shfl(rr.s, (int)(c + 16 * t));
-        float z = FMT == FMT_Q4S ? __shfl(rr.z, (int)(c + 16 * t)) : 0.f;
+        sx[t] = __float_as_uint(rr.s);
+        zx[t] = __float_as_uint(rr.z);
+      }
+      xpose4(sx[0], sx[1], sx[2], sx[3]);
+      if (FMT == FMT_Q4S) xpose4(zx[0], zx[1], zx[2], zx[3]);
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        float s = __uint_as_float(sx[t]);
+        float z = FMT == FMT_Q4S ? __uint_as_float(zx[t]) : 0.f;
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
           f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, afr[st][t][rb]), bf[t],
