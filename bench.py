@@ -33,7 +33,7 @@ ROTATE_BYTES = 400 << 20
 # HBM bytes per config-1 GEMV launch from two rocprofv3 --pmc passes
 # (the committed qgemv1 config-1 HBM traffic profile): FETCH_SIZE 6273.5 KiB x 1.996
 # (factor from a 12,582,912 B device copy) + WRITE_SIZE 16.0 KiB x 1.0.
-TRAFFIC_CFG1 = 12838686
+TRAFFIC_CFG1 = 12829235
 
 
 def log(*a):
