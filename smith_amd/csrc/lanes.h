@@ -22,6 +22,18 @@ __device__ __forceinline__ float sum16_lanes(float v) {
   v = sum8_lanes(v);
   return v + dpp_f32<0x140>(v);
 }
+// maximum over each aligned group of 16 lanes, in all 16
+template <int CTRL>
+__device__ __forceinline__ float max_dpp(float v) {
+  const float u = dpp_f32<CTRL>(v);
+  return u > v ? u : v;
+}
+__device__ __forceinline__ float max16_lanes(float v) {
+  v = max_dpp<0xB1>(v);
+  v = max_dpp<0x4E>(v);
+  v = max_dpp<0x141>(v);
+  return max_dpp<0x140>(v);
+}
 // v + v of lane ^ 16 / lane ^ 32 (the two rows / halves swapped whole)
 __device__ __forceinline__ float add_xor16(float v) {
   const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

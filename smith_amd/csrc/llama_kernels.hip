@@ -430,18 +430,11 @@ __device__ __forceinline__ void attention_prefill_body(
     for (int r = 0; r < 4; r++) {
       const uint32_t pos = p0 + s0 + 4 * j + r;
       const float sv = k0 + c <= pos ? sc[r] * scale : -__builtin_inff();
-      float v = sv;
-#pragma unroll
-      for (int d = 1; d < 16; d <<= 1) {
-        const float u = __shfl_xor(v, d);
-        v = u > v ? u : v;
-      }
+      const float v = max16_lanes(sv);
       const float mn = v > m[r] ? v : m[r];  // -inf while every key so far is masked for this row
       const float alpha = m[r] == -__builtin_inff() ? 0.f : __expf(m[r] - mn);
       const float pv = sv == -__builtin_inff() ? 0.f : __expf(sv - mn);
-      float rs = pv;
-#pragma unroll
-      for (int d = 1; d < 16; d <<= 1) rs += __shfl_xor(rs, d);
+      const float rs = sum16_lanes(pv);
       l[r] = __builtin_fmaf(l[r], alpha, rs);
       m[r] = mn;
 #pragma unroll
