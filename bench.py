@@ -1,7 +1,7 @@
 """Benchmark of the quantized-weight matmul path on one MI355X.
 
 Headline (value): matmulQ4 decode GEMV, M=1, Smith weight [K=4096, N=4096]
-quantized with quantizeQ4, weights resident in HBM.
+quantized with quantizeQ4 (benchmark configuration 1), weights resident in HBM.
 A step = one matmulQ4 call (activation prep + MFMA GEMV).  The K timed steps
 rotate over >= 400 MB of distinct weight copies so the 256 MB MALL cannot
 serve them.  value = algorithmic bytes per step / time per step (GB/s);

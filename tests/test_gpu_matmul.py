@@ -186,7 +186,7 @@ def test_q4_0_repack_and_matmul(N, K):
         assert e <= tol_for(M, K), (M, N, K, e)
 
 
-# ---------------- BASELINE configs at full size ----------------
+# ---------------- the benchmark configurations at full size ----------------
 
 def test_config1_q4_gemv_4096():
     K = N = 4096
