@@ -193,10 +193,17 @@ int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, ui
  * *pos_ptr .. *pos_ptr+S-1 (gguf_cache.js:128-157, 212-231).  qkv rows are
  * [q | k | v] with stride ld; caches are [n_kv_heads, max_seq, head_dim];
  * head_dim <= 128 and a multiple of 4.  act_out (S == 1): also the act of
- * the output row for the output projection. */
+ * the output row for the output projection.
+ * rope_cos / rope_sin hold rope_len entries each.  The position lives in
+ * device memory, so its bound is checked on the device: when
+ * *pos_ptr + S > max_seq or (*pos_ptr + S) * (n_heads*head_dim/2) > rope_len
+ * (the whole-row RoPE of a q row would read past the table, where the
+ * reference reads out of bounds, rope.metal:29-36) the kernels touch no
+ * cache or table entry, and the next synchronising call (smith_sync,
+ * smith_copy_d2h) returns -1 with the positions in smith_last_error. */
 int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
                     uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
-                    float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out);
+                    uint32_t rope_len, float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out);
 /* Single-row attention (S == 1, position *pos_ptr) that leaves the
  * combination of its key splits to the output projection: parts receives,
  * per head and split, (m, l, pad, pad, o[head_dim]) in 132-float records
@@ -205,10 +212,12 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
  * that smith_argmax_embed fills with the cos / sin table entries of the next
  * position (int32 tag = that position in the first word); when the tag is
  * *pos_ptr the RoPE reads them instead of the table (one memory round trip
- * less), otherwise the table.  head_dim <= 128, % 32. */
+ * less), otherwise the table.  head_dim <= 128, % 32.  Position bound
+ * (*pos_ptr + 1 against max_seq and rope_len) checked on the device as in
+ * smith_attention. */
 int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, uint32_t n_heads, uint32_t n_kv_heads,
-                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, const float* rope_row,
-                          float* kcache, float* vcache, uint32_t max_seq, float* parts);
+                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, uint32_t rope_len,
+                          const float* rope_row, float* kcache, float* vcache, uint32_t max_seq, float* parts);
 /* smith_linear_q4_0_t_act whose input is smith_attention_parts' partials
  * (K = n_heads * head_dim; the splits are combined per head first). */
 int smith_linear_q4_0_t_attn(void* ctx, const float* parts, const int32_t* pos_ptr, uint32_t head_dim,

@@ -68,17 +68,25 @@ def read_gguf(path):
     return buf, meta, tensors, data0
 
 
-def _tensor_f32(buf, data0, shape, t, off):
-    """dequantizeTensor, gguf.js:343-394."""
+def _tensor_f32(buf, data0, shape, t, off, out=None, stage=None):
+    """dequantizeTensor, gguf.js:343-394, widened to f64.  `out` (f64) and
+    `stage` (f32), when given, are arrays of numel elements reused across
+    calls, so a layer-at-a-time forward does not fault in fresh pages for
+    every layer."""
     numel = int(np.prod(shape))
     bs, bpb = _BLOCK[t]
     nbytes = -(-numel // bs) * bpb
     raw = np.asarray(buf[data0 + off:data0 + off + nbytes])
     if t == F32:
-        return raw.view(np.float32).astype(np.float64)
-    if t == F16:
-        return raw.view(np.float16).astype(np.float64)
-    return O.dequantize_tensor(t, raw, numel).astype(np.float64)
+        src = raw.view(np.float32)
+    elif t == F16:
+        src = raw.view(np.float16)
+    else:
+        src = O.dequantize_tensor(t, raw, numel, out=stage)
+    if out is None:
+        return src.astype(np.float64)
+    np.copyto(out, src)
+    return out
 
 
 def precompute_rope(hd, max_seq, base):
@@ -111,11 +119,28 @@ def rmsnorm(x, g, eps):
 
 
 def silu(x):
+    """shaders/swiglu.metal:12-21: g / (1 + exp(-g))."""
     return x / (1.0 + np.exp(-x))
 
 
+def swiglu(gate, up):
+    """shaders/swiglu.metal:12-21: out = silu(gate) * up (gate is the first
+    operand, gguf_cache.js:168-170 passes ffn_gate's product first)."""
+    return silu(gate) * up
+
+
+def attend(q, K, V, scale):
+    """Decode attention of one query row over the cached keys
+    (gguf_cache.js:149-154): scores = K q * scale, softmax over all T keys,
+    output = weights @ V.  K, V [T, hd]."""
+    sc = (K @ q) * scale
+    w = np.exp(sc - sc.max())
+    w /= w.sum()
+    return w @ V
+
+
 class LlamaOracle:
-    def __init__(self, path):
+    def __init__(self, path, lazy=None):
         buf, meta, tensors, data0 = read_gguf(path)
         arch = meta["general.architecture"]
         assert arch == "llama"
@@ -136,30 +161,51 @@ class LlamaOracle:
         self.cos, self.sin = precompute_rope(self.hd, self.max_seq, g("rope.freq_base", 10000))
         T = {name: (shape, t, off) for name, shape, t, off in tensors}
 
-        def dense(name):
+        scratch = {}
+
+        def reuse(role, numel, dtype):
+            a = scratch.get((role, dtype))
+            if a is None or a.size != numel:
+                a = scratch[(role, dtype)] = np.empty(numel, dtype)
+            return a
+
+        def dense(name, role=None):
             shape, t, off = T[name]
-            return _tensor_f32(buf, data0, shape, t, off)
+            if role is None:
+                return _tensor_f32(buf, data0, shape, t, off)
+            numel = int(np.prod(shape))
+            return _tensor_f32(buf, data0, shape, t, off, reuse(role, numel, np.float64),
+                               reuse("stage%d" % numel, numel, np.float32))
 
         def linear(name, n_in, n_out):
             # gguf_loader.js:238-257: [rows, cols] listing; transpose when the
             # Smith shape [in, out] equals [cols, rows], else flat copy
             shape, t, off = T[name]
-            data = _tensor_f32(buf, data0, shape, t, off)
+            data = dense(name, name.split(".")[2] if self.lazy else None)
             rows, cols = shape
             if n_in == cols and n_out == rows:
-                return data.reshape(rows, cols).T.copy()
+                w = data.reshape(rows, cols).T
+                return w if self.lazy else w.copy()
             return data.reshape(n_in, n_out)
 
         self.E = dense("token_embd.weight").reshape(self.vocab, self.dim)
-        self.blocks = []
-        for l in range(self.L):
+        # A model whose f64 weights would not fit comfortably in host memory
+        # (config 5: 3.5 G parameters) is decoded one layer at a time inside
+        # forward(), into arrays reused from layer to layer; small models
+        # keep every layer decoded.
+        per_layer = self.dim * (2 * self.dim + 2 * self.kvd + 3 * self.ffn)
+        self.lazy = per_layer * self.L > (64 << 20) if lazy is None else bool(lazy)
+
+        def block(l):
             p = "blk.%d." % l
-            self.blocks.append(dict(
+            return dict(
                 g1=dense(p + "attn_norm.weight"), g2=dense(p + "ffn_norm.weight"),
                 q=linear(p + "attn_q.weight", self.dim, self.dim), k=linear(p + "attn_k.weight", self.dim, self.kvd),
                 v=linear(p + "attn_v.weight", self.dim, self.kvd), o=linear(p + "attn_output.weight", self.dim, self.dim),
                 gate=linear(p + "ffn_gate.weight", self.dim, self.ffn), up=linear(p + "ffn_up.weight", self.dim, self.ffn),
-                down=linear(p + "ffn_down.weight", self.ffn, self.dim)))
+                down=linear(p + "ffn_down.weight", self.ffn, self.dim))
+        self._block = block
+        self.blocks = None if self.lazy else [block(l) for l in range(self.L)]
         self.gF = dense("output_norm.weight")
         if "output.weight" in T:
             # lmHead [dim, vocab] gets the flat data untransposed (gguf_loader.js:256-259)
@@ -169,13 +215,15 @@ class LlamaOracle:
         self.reset()
 
     def reset(self):
+        # np.zeros maps untouched pages lazily: only the positions written
+        # take host memory
         self.kc = [np.zeros((self.nKV, self.max_seq, self.hd)) for _ in range(self.L)]
         self.vc = [np.zeros((self.nKV, self.max_seq, self.hd)) for _ in range(self.L)]
 
     def _layer(self, l, x, start):
         """x [S, dim] at positions start..start+S-1 (gguf_cache.js:116-172 and
         :199-247: keys/values of earlier positions from the cache, causal)."""
-        b = self.blocks[l]
+        b = self._block(l) if self.lazy else self.blocks[l]
         S = x.shape[0]
         n1 = rmsnorm(x, b["g1"], self.eps)
         q = rope_rows(n1 @ b["q"], start, self.cos, self.sin)
@@ -192,13 +240,10 @@ class LlamaOracle:
             qh = q[:, h * self.hd:(h + 1) * self.hd]
             for s in range(S):
                 T = start + s + 1
-                sc = (self.kc[l][kv, :T] @ qh[s]) * scale
-                w = np.exp(sc - sc.max())
-                w /= w.sum()
-                att[s, h * self.hd:(h + 1) * self.hd] = w @ self.vc[l][kv, :T]
+                att[s, h * self.hd:(h + 1) * self.hd] = attend(qh[s], self.kc[l][kv, :T], self.vc[l][kv, :T], scale)
         x2 = x + att @ b["o"]
         n2 = rmsnorm(x2, b["g2"], self.eps)
-        return x2 + (silu(n2 @ b["gate"]) * (n2 @ b["up"])) @ b["down"]
+        return x2 + swiglu(n2 @ b["gate"], n2 @ b["up"]) @ b["down"]
 
     def forward(self, tokens, start):
         """Logits [S, vocab] for tokens at positions start.. (cache updated)."""

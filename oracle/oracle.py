@@ -173,11 +173,14 @@ def dequant_q6_k_block(blk):
     return _block("oracle_dequant_q6_k_block", 256, blk)
 
 
-def dequantize_tensor(ggml_type, data, numel):
+def dequantize_tensor(ggml_type, data, numel, out=None):
     """dequantizeTensor, src/gguf.js:343-394 (F32, F16, BF16, Q4_0, Q4_1,
-    Q5_0, Q8_0, Q4_K, Q6_K)."""
+    Q5_0, Q8_0, Q4_K, Q6_K).  `out`: an optional f32 array of numel
+    elements to decode into."""
     data = np.ascontiguousarray(data, dtype=np.uint8)
-    out = np.empty(numel, dtype=np.float32)
+    if out is None:
+        out = np.empty(numel, dtype=np.float32)
+    assert out.dtype == np.float32 and out.size == numel and out.flags.c_contiguous
     if lib().oracle_dequantize_tensor(ggml_type, _p(data), numel, _p(out)):
         raise ValueError("unsupported type %d" % ggml_type)
     return out

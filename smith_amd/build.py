@@ -32,26 +32,45 @@ def _run(cmd):
     subprocess.check_call(cmd)
 
 
+def _kernel_cmds():
+    # a plain gfx950 ELF code object (no offload bundle) for hipModuleLoad
+    return [[os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
+             "-c", os.path.join(CSRC, src), "-o", dst]
+            for src, dst in (("smith_kernels.hip", HSACO), ("llama_kernels.hip", HSACO_LLAMA),
+                             ("gemm_kernels.hip", HSACO_GEMM))]
+
+
+def _bridge_cmd():
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
+            "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include"),
+            os.path.join(CSRC, "smith_bridge.cpp"), "-o", LIBSMITH,
+            "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc",
+            "-Wl,-rpath," + os.path.join(ROCM, "lib")]
+
+
 def build_kernels():
     os.makedirs(LIBDIR, exist_ok=True)
-    # a plain gfx950 ELF code object (no offload bundle) for hipModuleLoad
-    for src, dst in (("smith_kernels.hip", HSACO), ("llama_kernels.hip", HSACO_LLAMA), ("gemm_kernels.hip", HSACO_GEMM)):
-        _run([os.path.join(ROCM, "bin", "hipcc"), *HIP_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
-              "-c", os.path.join(CSRC, src), "-o", dst])
+    for cmd in _kernel_cmds():
+        _run(cmd)
 
 
 def build_bridge():
     os.makedirs(LIBDIR, exist_ok=True)
-    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
-          "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include"),
-          os.path.join(CSRC, "smith_bridge.cpp"), "-o", LIBSMITH,
-          "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc",
-          "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+    _run(_bridge_cmd())
 
 
 def build():
-    build_kernels()
-    build_bridge()
+    """Every code object and the bridge, compiled concurrently (independent
+    translation units); fails if any of them fails."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    cmds = _kernel_cmds() + [_bridge_cmd()]
+    procs = []
+    for cmd in cmds:
+        print("+", " ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd)))
+    bad = [cmd for cmd, p in procs if p.wait() != 0]
+    if bad:
+        raise subprocess.CalledProcessError(1, bad[0])
 
 
 if __name__ == "__main__":

@@ -70,6 +70,38 @@ __device__ __forceinline__ float rope_elem(const float* __restrict__ row, uint32
 }
 
 // ---------------------------------------------------------------------------
+// Device-side bound of the positions a launch touches: rows p0 .. p0+S-1
+// (p0 = *pos_ptr, read on the device) must lie inside the KV cache
+// (p0 + S <= maxSeq) and inside the RoPE tables for whole-row indexing of
+// rows W wide (entries pos*(W/2) + i, so (p0 + S) * (W/2) <= rope_len).  The
+// reference's whole-row RoPE reads past its table for positions with
+// pos*(dim/2) >= maxSeqLen*headDim/2 (rope.metal:29-36 as gguf_cache.js:130
+// applies it); here such a launch touches neither the tables nor the caches.
+// The condition is the same for every workgroup, so all of them leave before
+// their first position-dependent access (no barrier or split counter is left
+// half-used).  Workgroup (0,0,0) records (code, p0, S) in err -- host-mapped
+// memory the bridge reads at its next synchronisation -- unless an earlier
+// failure is already recorded there.
+// ---------------------------------------------------------------------------
+#define POS_ERR_KV_APPEND 1u
+#define POS_ERR_ATTENTION 2u
+#define POS_ERR_PREFILL 3u
+#define POS_ERR_PART 4u
+
+__device__ __forceinline__ bool pos_in_range(int32_t p0i, uint32_t S, uint32_t maxSeq, uint32_t W, uint32_t rope_len,
+                                             uint32_t* __restrict__ err, uint32_t code) {
+  const uint64_t end = (uint64_t)(uint32_t)p0i + S;
+  if (p0i >= 0 && end <= maxSeq && end * (W / 2) <= rope_len) return true;
+  if (err && threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 &&
+      __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0u) {
+    __hip_atomic_store(err + 1, (uint32_t)p0i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(err + 2, S, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  return false;
+}
+
+// ---------------------------------------------------------------------------
 // One key split of one query row, shared by the attention kernels (256
 // threads): keys t0 .. t1-1, 32-row K/V tiles staged in LDS; rows t < p0
 // come from the caches, rows t >= p0 (this launch's rows) from qkv row
@@ -197,8 +229,14 @@ __device__ __forceinline__ void att_split(AttShared& sh, const float* __restrict
 extern "C" __global__ void smith_kv_append(const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr,
                                            uint32_t Wq, uint32_t nKV, uint32_t hd, const float* __restrict__ cosT,
                                            const float* __restrict__ sinT, float* __restrict__ kcache,
-                                           float* __restrict__ vcache, uint32_t maxSeq) {
-  const uint32_t s = blockIdx.x, pos = (uint32_t)pos_ptr[0] + s;
+                                           float* __restrict__ vcache, uint32_t maxSeq, uint32_t rope_len,
+                                           uint32_t* __restrict__ err) {
+  const int32_t p0i = pos_ptr[0];
+  // bounded by the q row width as well, so a launch sequence that fails in
+  // the attention kernel after this one has not appended anything either
+  const uint32_t Wmax = Wq > nKV * hd ? Wq : nKV * hd;
+  if (!pos_in_range(p0i, gridDim.x, maxSeq, Wmax, rope_len, err, POS_ERR_KV_APPEND)) return;
+  const uint32_t s = blockIdx.x, pos = (uint32_t)p0i + s;
   const uint32_t Wk = nKV * hd;
   const float* krow = qkv + (size_t)s * ld + Wq;
   for (uint32_t i = threadIdx.x; i < Wk; i += blockDim.x) {
@@ -234,13 +272,16 @@ __device__ __forceinline__ void attention_body(
     const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
     uint32_t nKV, uint32_t hd, const float* __restrict__ cosT, const float* __restrict__ sinT,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out,
-    float* __restrict__ ws, uint32_t* __restrict__ counters, uint8_t* __restrict__ act_out) {
+    float* __restrict__ ws, uint32_t* __restrict__ counters, uint8_t* __restrict__ act_out, uint32_t rope_len,
+    uint32_t* __restrict__ err) {
   __shared__ AttShared sh;
   __shared__ float ored[2][128];
   __shared__ int s_last;
   const uint32_t h = blockIdx.x, s = blockIdx.y, z = blockIdx.z;
   const uint32_t tid = threadIdx.x;
-  const uint32_t p0 = (uint32_t)pos_ptr[0];
+  const int32_t p0i = pos_ptr[0];
+  if (!pos_in_range(p0i, S, maxSeq, nH * hd, rope_len, err, POS_ERR_ATTENTION)) return;
+  const uint32_t p0 = (uint32_t)p0i;
   const uint32_t pos = p0 + s;
   const uint32_t T = pos + 1;
   const uint32_t rep = nH / nKV, kvh = h / rep;
@@ -326,16 +367,17 @@ __device__ __forceinline__ void attention_body(
   const float *__restrict__ qkv, uint32_t ld, const int32_t *__restrict__ pos_ptr, uint32_t S, uint32_t nH,    \
       uint32_t nKV, uint32_t hd, const float *__restrict__ cosT, const float *__restrict__ sinT,               \
       float *__restrict__ kcache, float *__restrict__ vcache, uint32_t maxSeq, float *__restrict__ out,        \
-      float *__restrict__ ws, uint32_t *__restrict__ counters, uint8_t *__restrict__ act_out
+      float *__restrict__ ws, uint32_t *__restrict__ counters, uint8_t *__restrict__ act_out, uint32_t rope_len, \
+      uint32_t *__restrict__ err
 // rows' keys formed here from qkv (and appended to the caches)
 extern "C" __global__ __launch_bounds__(256) void smith_attention(ATT_ARGS) {
   attention_body<false>(qkv, ld, pos_ptr, S, nH, nKV, hd, cosT, sinT, kcache, vcache, maxSeq, out, ws, counters,
-                        act_out);
+                        act_out, rope_len, err);
 }
 // every key already in the caches (smith_kv_append ran first)
 extern "C" __global__ __launch_bounds__(256) void smith_attention_cached(ATT_ARGS) {
   attention_body<true>(qkv, ld, pos_ptr, S, nH, nKV, hd, cosT, sinT, kcache, vcache, maxSeq, out, ws, counters,
-                       act_out);
+                       act_out, rope_len, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -366,7 +408,8 @@ template <int NT>  // head_dim / 16
 __device__ __forceinline__ void attention_prefill_body(
     const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
     uint32_t nKV, const float* __restrict__ cosT, const float* __restrict__ sinT, const float* __restrict__ kcache,
-    const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out) {
+    const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out, uint32_t rope_len,
+    uint32_t* __restrict__ err) {
   constexpr uint32_t hd = 16 * NT;
   __shared__ __attribute__((aligned(16))) float Qs[FA_BQ * FA_QS];
   __shared__ __attribute__((aligned(16))) float KV[FA_BK * FA_QS + FA_BK * FA_VS];  // then the waves' O
@@ -377,7 +420,9 @@ __device__ __forceinline__ void attention_prefill_body(
   const uint32_t h = blockIdx.x, s0 = blockIdx.y * FA_BQ;
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint32_t c = lane & 15, j = lane >> 4;
-  const uint32_t p0 = (uint32_t)pos_ptr[0];
+  const int32_t p0i = pos_ptr[0];
+  if (!pos_in_range(p0i, S, maxSeq, nH * hd, rope_len, err, POS_ERR_PREFILL)) return;
+  const uint32_t p0 = (uint32_t)p0i;
   const uint32_t rep = nH / nKV, kvh = h / rep;
   const uint32_t Wq = nH * hd;
   const float scale = 1.0f / __builtin_sqrtf((float)hd);
@@ -490,8 +535,9 @@ __device__ __forceinline__ void attention_prefill_body(
   extern "C" __global__ __launch_bounds__(256) void smith_attention_prefill_hd##NT(                              \
       const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,   \
       uint32_t nKV, const float* __restrict__ cosT, const float* __restrict__ sinT,                              \
-      const float* __restrict__ kcache, const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out) { \
-    attention_prefill_body<NT>(qkv, ld, pos_ptr, S, nH, nKV, cosT, sinT, kcache, vcache, maxSeq, out);           \
+      const float* __restrict__ kcache, const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out, \
+      uint32_t rope_len, uint32_t* __restrict__ err) {                                                            \
+    attention_prefill_body<NT>(qkv, ld, pos_ptr, S, nH, nKV, cosT, sinT, kcache, vcache, maxSeq, out, rope_len, err); \
   }
 // named by head_dim / 16
 DEF_ATT_PREFILL(1)
@@ -543,7 +589,8 @@ struct AttPShared {
 extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     const float* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, uint32_t nH, uint32_t nKV, uint32_t hd,
     const float* __restrict__ cosT, const float* __restrict__ sinT, const float* __restrict__ rrow,
-    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts) {
+    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts,
+    uint32_t rope_len, uint32_t* __restrict__ err) {
   __shared__ AttPShared sh;
   __shared__ float kn[128], vn[128];
   __shared__ float ored[2][128];
@@ -584,6 +631,7 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
 
   // 2. the position: split count, RoPE of q and of the new k (rope_elem's
   //    whole-row pairing), the cache append
+  if (!pos_in_range(p0i, 1, maxSeq, Wq, rope_len, err, POS_ERR_PART)) return;
   const uint32_t p0 = (uint32_t)p0i, T = p0 + 1;
   const uint32_t ntile = (T + ATTP_ROWS - 1) / ATTP_ROWS;
   const uint32_t nsplit = ntile < ATTP_MAXSPLIT ? ntile : ATTP_MAXSPLIT;

@@ -65,6 +65,11 @@ struct Ctx {
   uint32_t* att_cnt = nullptr;
   size_t att_cnt_n = 0;
   bool capturing = false;
+  // device-side position bound failures (attention, KV append): host-mapped
+  // words {code, p0, S} the kernels store into, read at every synchronising
+  // call (pos_err_host) and passed to kernels as pos_err_dev
+  uint32_t* pos_err_host = nullptr;
+  uint32_t* pos_err_dev = nullptr;
   // scratch buffers replaced by bigger ones: a captured graph may still name
   // them, so they are freed only with the context
   std::vector<void*> retired;
@@ -191,6 +196,21 @@ int ensure(Ctx* c, void** p, size_t* have, size_t need) {
   HIPCHK(c, hipMalloc(p, sz));
   *have = sz;
   return 0;
+}
+
+// Called after the stream has drained: reports (once) a position bound
+// failure that a kernel recorded on the device since the last check.
+int check_pos_err(Ctx* c) {
+  volatile uint32_t* e = c->pos_err_host;
+  if (!e || e[0] == 0) return 0;
+  static const char* who[] = {"?", "smith_kv_append", "smith_attention", "smith_attention (prefill)",
+                              "smith_attention_parts"};
+  const uint32_t code = e[0], p0 = e[1], S = e[2];
+  e[1] = e[2] = 0;
+  e[0] = 0;
+  return fail(c, "%s: positions %d .. %d lie outside the KV cache or the whole-row RoPE table (device bound "
+              "check); the launch read and wrote no cache or table entry",
+              who[code < 5 ? code : 0], (int32_t)p0, (int32_t)(p0 + S) - 1);
 }
 
 int ensure_counters(Ctx* c, size_t n) {
@@ -519,10 +539,14 @@ void* smith_init(void) {
   if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return nullptr;
   Ctx* c = new Ctx();
   if (hipSetDevice(0) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess) {
+      hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess ||
+      hipHostMalloc((void**)&c->pos_err_host, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+      hipHostGetDevicePointer((void**)&c->pos_err_dev, c->pos_err_host, 0) != hipSuccess) {
+    if (c->pos_err_host) hipHostFree(c->pos_err_host);
     delete c;
     return nullptr;
   }
+  memset(c->pos_err_host, 0, 256);
   return c;
 }
 
@@ -564,6 +588,7 @@ void smith_destroy(void* ctx) {
   hipEventDestroy(c->t0);
   hipEventDestroy(c->t1);
   hipStreamDestroy(c->stream);
+  if (c->pos_err_host) hipHostFree(c->pos_err_host);
   delete c;
 }
 
@@ -659,12 +684,12 @@ uint64_t smith_allocated_size(void* ctx) {
 int64_t smith_test_release(void* ctx) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
-  uint64_t before = c->allocated;
+  // bytes freed by the release (gpu_bridge.m: after_alloc - after_release)
   void* p = smith_alloc(ctx, 1 << 20, SMITH_SHARED);
   if (!p) return -1;
   uint64_t mid = c->allocated;
   smith_release_buffer(p);
-  return (int64_t)(mid - c->allocated) + (int64_t)(c->allocated - before);
+  return (int64_t)(mid - c->allocated);
 }
 
 int64_t smith_test_release_after_use(void* ctx) {
@@ -698,6 +723,7 @@ int smith_copy_d2h(void* ctx, void* dst, const void* src, uint64_t off, uint64_t
   if (!bytes) return 0;
   HIPCHK(c, hipMemcpyAsync(dst, (const char*)src + off, bytes, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (check_pos_err(c)) return -1;
   return 0;
 }
 
@@ -739,7 +765,7 @@ int smith_sync(void* ctx) {
   if (!c) return -1;
   if (set_device(c)) return -1;
   HIPCHK(c, hipStreamSynchronize(c->stream));
-  return 0;
+  return check_pos_err(c);
 }
 
 // ---------------- code objects ----------------
@@ -770,8 +796,9 @@ void* smith_compile_source(void* ctx, const char* source, char** error_out) {
     if (error_out) *error_out = strdup("hiprtcCreateProgram failed");
     return nullptr;
   }
-  const char* opts[] = {"--offload-arch=gfx950", "-O3"};
-  hiprtcResult r = hiprtcCompileProgram(prog, 2, opts);
+  // no packed-f32 VALU instructions, as for the library's own code objects
+  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  hiprtcResult r = hiprtcCompileProgram(prog, 6, opts);
   if (r != HIPRTC_SUCCESS) {
     size_t n = 0;
     hiprtcGetProgramLogSize(prog, &n);
@@ -1269,7 +1296,7 @@ int smith_embed(void* ctx, const float* E, const int32_t* tokens, float* out, ui
 
 int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos_ptr, uint32_t S, uint32_t n_heads,
                     uint32_t n_kv_heads, uint32_t head_dim, const float* rope_cos, const float* rope_sin,
-                    float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out) {
+                    uint32_t rope_len, float* kcache, float* vcache, uint32_t max_seq, float* out, void* act_out) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
   if (act_out && (S != 1 || head_dim % 8 || (n_heads * head_dim) % 32))
@@ -1277,18 +1304,21 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   if (!n_kv_heads || n_heads % n_kv_heads)
     return fail(c, "smith_attention: %u heads not a multiple of %u kv heads", n_heads, n_kv_heads);
   if (head_dim > 128 || head_dim % 4) return fail(c, "smith_attention: head_dim %u unsupported (<= 128, % 4)", head_dim);
+  if (!rope_cos || !rope_sin || !kcache || !vcache || !qkv || !pos_ptr || !out)
+    return fail(c, "smith_attention: null buffer");
   if (set_device(c)) return -1;
   if (!S) return 0;
+  uint32_t* perr = c->pos_err_dev;
   if (S > 1 && head_dim % 16 == 0) {
     // prompt rows: rope + append every row's key/value, then flash attention
     // on the f32 matrix cores over the caches (16 query rows per workgroup,
     // its four waves splitting the keys)
     uint32_t Wq = n_heads * head_dim;
     void* aargs[] = {&qkv, &ld, &pos_ptr, &Wq, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &kcache, &vcache,
-                     &max_seq};
+                     &max_seq, &rope_len, &perr};
     if (launch(c, "smith_kv_append", dim3(S), dim3(256), aargs)) return -1;
     void* fargs[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &rope_cos, &rope_sin,
-                     &kcache, &vcache, &max_seq, &out};
+                     &kcache, &vcache, &max_seq, &out, &rope_len, &perr};
     char name[48];
     snprintf(name, sizeof name, "smith_attention_prefill_hd%u", head_dim / 16);
     return launch(c, name, dim3(n_heads, (S + 15) / 16), dim3(256), fargs);
@@ -1315,19 +1345,19 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
     // attention workgroups read all keys from the caches
     uint32_t Wq = n_heads * head_dim;
     void* aargs[] = {&qkv, &ld, &pos_ptr, &Wq, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &kcache, &vcache,
-                     &max_seq};
+                     &max_seq, &rope_len, &perr};
     if (launch(c, "smith_kv_append", dim3(S), dim3(256), aargs)) return -1;
     appended = 1;
   }
   void* args[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin,
-                  &kcache, &vcache, &max_seq, &out, &pws, &pcnt, &act_out};
+                  &kcache, &vcache, &max_seq, &out, &pws, &pcnt, &act_out, &rope_len, &perr};
   return launch(c, appended ? "smith_attention_cached" : "smith_attention", dim3(n_heads, S, nsplit), dim3(256),
                 args);
 }
 
 int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, uint32_t n_heads, uint32_t n_kv_heads,
-                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, const float* rope_row,
-                          float* kcache, float* vcache, uint32_t max_seq, float* parts) {
+                          uint32_t head_dim, const float* rope_cos, const float* rope_sin, uint32_t rope_len,
+                          const float* rope_row, float* kcache, float* vcache, uint32_t max_seq, float* parts) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
   if (!n_kv_heads || n_heads % n_kv_heads)
@@ -1337,8 +1367,9 @@ int smith_attention_parts(void* ctx, const float* qkv, const int32_t* pos_ptr, u
   if (set_device(c)) return -1;
   if ((n_heads * head_dim) % 2 || (n_kv_heads * head_dim) % 2)
     return fail(c, "smith_attention_parts: q / k row widths must be even (RoPE pairs)");
+  uint32_t* perr = c->pos_err_dev;
   void* args[] = {&qkv, &pos_ptr, &n_heads, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &rope_row,
-                  &kcache, &vcache, &max_seq, &parts};
+                  &kcache, &vcache, &max_seq, &parts, &rope_len, &perr};
   return launch(c, "smith_attention_part", dim3(n_heads, 8), dim3(256), args);  // ATTP_MAXSPLIT splits
 }
 

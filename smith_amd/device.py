@@ -81,7 +81,7 @@ SYMBOLS = {
     "smith_linear_q4_0": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
     "smith_repack_q4_0_t_into": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32]),
     "smith_linear_q4_0_t": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
-    "smith_attention_parts": (_INT, [_P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _P, _U32, _P]),
+    "smith_attention_parts": (_INT, [_P, _P, _P, _U32, _U32, _U32, _P, _P, _U32, _P, _P, _P, _U32, _P]),
     "smith_linear_q4_0_t_attn": (_INT, [_P, _P, _P, _U32, _P, _P, _P, _U32, _U32, _P, _U32, _P, _P]),
     "smith_linear_q4_0_t_act": (_INT, [_P, _P, ctypes.c_int, ctypes.c_float, _P, _P, _P, _U32, _U32, _P, _U32, _P,
                                        _P]),
@@ -102,7 +102,7 @@ SYMBOLS = {
     "smith_linear_q8": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),
     "smith_rmsnorm": (_INT, [_P, _P, _P, _P, _U32, _U32, ctypes.c_float]),
     "smith_embed": (_INT, [_P, _P, _P, _P, _U32, _U32, _P, _P]),
-    "smith_attention": (_INT, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _U32, _P, _P]),
+    "smith_attention": (_INT, [_P, _P, _U32, _P, _U32, _U32, _U32, _U32, _P, _P, _U32, _P, _P, _U32, _P, _P]),
     "smith_repack_lmhead_q4_0": (_INT, [_P, _P, _P, _P, _U32, _U32]),
     "smith_lmhead_q4_0_nb": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _P, _U32, _U32]),
     "smith_lmhead_q4_0_greedy": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _P, _P,

@@ -42,7 +42,8 @@ class _Reader:
 
     def string(self):
         n = self.scalar("<Q")
-        s = bytes(self.buf[self.pos:self.pos + n]).decode("utf-8")
+        # invalid UTF-8 becomes U+FFFD, as TextDecoder does (gguf.js:74)
+        s = bytes(self.buf[self.pos:self.pos + n]).decode("utf-8", errors="replace")
         self.pos += n
         return s
 

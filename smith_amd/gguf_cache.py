@@ -111,7 +111,7 @@ class _Engine:
             blk["qkv"](x, qkv, M, gamma=blk["ln1Gamma"].ptr, eps=eps)
             device.check(device.lib.smith_attention(
                 ctx, qkv, self.qkv_ld, self.pos.ptr, M, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
-                rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, None),
+                rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0], cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, None),
                 "attention")
             blk["outProj"](attn, x2, M, resid=x, epilogue=1)
             blk["gateUp"](x2, h, M, gamma=blk["ln2Gamma"].ptr, eps=eps, epilogue=2)
@@ -132,13 +132,13 @@ class _Engine:
                 parts = self.att_parts.ptr
                 device.check(device.lib.smith_attention_parts(
                     ctx, qkv, self.pos.ptr, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"], rope["cos"].ptr,
-                    rope["sin"].ptr, self.rope_row.ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], parts),
+                    rope["sin"].ptr, rope["sin"].shape[0], self.rope_row.ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], parts),
                     "attention")
                 blk["outProj"].attn(parts, self.pos.ptr, cfg["headDim"], x2, x, 1, ax2, blk["ln2Gamma"].ptr)
             else:
                 device.check(device.lib.smith_attention(
                     ctx, qkv, self.qkv_ld, self.pos.ptr, 1, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
-                    rope["cos"].ptr, rope["sin"].ptr, cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, aa),
+                    rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0], cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, aa),
                     "attention")
                 blk["outProj"].act(aa, False, 0.0, x2, resid=x, epilogue=1, act_out=ax2,
                                    gamma_out=blk["ln2Gamma"].ptr)

@@ -5,9 +5,9 @@ smith_quantize_q4_0: ggml q4_0 rounding in the reference decoder's
 interleaved nibble order) and streamed to the file one tensor at a time.
 mix="q4_k_m" writes the llama.cpp Q4_K_M type mix instead (Q4_K q/k/o/gate/
 up and token_embd, Q6_K v/down and output.weight) with seeded random block
-fields -- nibbles, 6-bit scales/mins, int8 scales uniform, f16 scales chosen
-for weights of about N(0, 0.02) size: a random init in quantized form, for
-throughput measurement.
+fields -- nibbles, 6-bit scales, int8 scales uniform, each Q4_K min equal to
+its scale with dmin = 7.5 d so the weights have zero mean, f16 scales chosen
+for weights of about N(0, 0.02) size: a random init in quantized form.
 Layout choices (so the reference's own loader would read the same model):
   * linear weights are listed [out, in] with blocks along `in`
     (gguf_loader.js:243-253 transposes such a listing into Smith's [in, out]);
@@ -66,7 +66,15 @@ def _kquant_producer(ggml, rows, cols, seed):
         if ggml == G.GGML_TYPE["Q4_K"]:
             b = rng.integers(0, 256, (nb, 144), dtype=np.uint8)
             b[:, 0:2] = _f16_bytes(1.0e-4, nb)   # d: 63 * 15 * 1e-4 ~ 0.09 full scale
-            b[:, 2:4] = _f16_bytes(5.0e-5, nb)   # dmin
+            b[:, 2:4] = _f16_bytes(7.5e-4, nb)   # dmin = 7.5 d
+            # every sub-block's 6-bit min equal to its 6-bit scale: bytes 4-7
+            # repeat bytes 0-3 and each of bytes 8-11 carries the same nibble
+            # twice, so w = d*sc*q - 7.5*d*sc = d*sc*(q - 7.5) has zero mean
+            # over the uniform nibbles (uniform mins would give every weight a
+            # positive offset and a degenerate model)
+            b[:, 8:12] = b[:, 4:8]
+            lo = b[:, 12:16] & 0x0F
+            b[:, 12:16] = lo | (lo << 4)
         else:
             b = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
             b[:, 208:210] = _f16_bytes(2.0e-5, nb)  # d: 127 * 32 * 2e-5 ~ 0.08 full scale

@@ -1,8 +1,8 @@
 """GPU parity of smith_attention for prompt rows (S > 1: KV append + the
 f32-MFMA flash attention) and single rows (S == 1), against a float64
 reference built from the Llama oracle's RoPE (whole-row indexing,
-oracle/llama_oracle.py rope_rows) and causal GQA softmax attention
-(gguf_cache.js:128-157, 212-231).  Keys before p0 come from caches filled
+oracle/llama_oracle.py rope_rows) and its causal GQA softmax attention
+(attend; gguf_cache.js:128-157, 212-231).  Keys before p0 come from caches filled
 with random rows, so chunked prefill is covered.
 
 Bar: normwise 1e-5 (f32 products and sums throughout; softmax exponentials
@@ -34,10 +34,8 @@ def _ref(q_all, k_new, v_new, kc, vc, p0, nH, nKV, hd, cos, sin):
     for s in range(S):
         T = p0 + s + 1
         for h in range(nH):
-            kv = h // rep
-            sc = K[kv, :T] @ q[s, h * hd:(h + 1) * hd] / np.sqrt(hd)
-            p = np.exp(sc - sc.max())
-            out[s, h * hd:(h + 1) * hd] = (p / p.sum()) @ V[kv, :T]
+            kv = h // rep  # the oracle's pinned attention (two-key closed form in test_llama_oracle)
+            out[s, h * hd:(h + 1) * hd] = LO.attend(q[s, h * hd:(h + 1) * hd], K[kv, :T], V[kv, :T], 1 / np.sqrt(hd))
     return out, K, V
 
 
@@ -64,8 +62,8 @@ def test_attention_matches_reference(S, p0, nH, nKV, hd):
     pos = device.alloc(4)
     device.upload(pos, np.array([p0], np.int32))
     out = device.alloc(S * Wq * 4)
-    device.check(device.lib.smith_attention(ctx, b["qkv"], ld, pos, S, nH, nKV, hd, b["cos"], b["sin"], b["kc"],
-                                            b["vc"], maxSeq, out, None))
+    device.check(device.lib.smith_attention(ctx, b["qkv"], ld, pos, S, nH, nKV, hd, b["cos"], b["sin"], cos.size,
+                                            b["kc"], b["vc"], maxSeq, out, None))
     device.sync()
     got = device.download(out, S * Wq * 4, np.float32).reshape(S, Wq)
     q64 = qkv.astype(np.float64)
@@ -138,8 +136,8 @@ def test_attention_parts_matches_reference(p0, nH, nKV, hd, rope):
         rr = device.alloc(row.nbytes)
         device.upload(rr, row)
     parts = device.alloc(nH * MAXSPLIT * STRIDE * 4)
-    device.check(device.lib.smith_attention_parts(ctx, b["qkv"], pos, nH, nKV, hd, b["cos"], b["sin"], rr, b["kc"],
-                                                  b["vc"], maxSeq, parts))
+    device.check(device.lib.smith_attention_parts(ctx, b["qkv"], pos, nH, nKV, hd, b["cos"], b["sin"], cos.size, rr,
+                                                  b["kc"], b["vc"], maxSeq, parts))
     device.sync()
     got = _combine(device.download(parts, nH * MAXSPLIT * STRIDE * 4, np.float32).reshape(-1, STRIDE), p0, nH, hd)
     q64 = qkv.astype(np.float64)
@@ -188,3 +186,52 @@ def test_argmax_embed_writes_rope_row():
     want = np.concatenate([cos[p * hq:(p + 1) * hq], sin[p * hq:(p + 1) * hq], cos[p * hk:(p + 1) * hk],
                            sin[p * hk:(p + 1) * hk]]).astype(np.float32)
     assert np.array_equal(row[4:], want)
+
+
+# ---------------- device-side position bounds ----------------
+
+@pytest.mark.parametrize("entry,S", [("attention", 16), ("attention", 1), ("parts", 1)])
+@pytest.mark.parametrize("case", ["short_table", "past_cache", "negative"])
+def test_position_bounds_fail_cleanly(entry, S, case):
+    """A position outside the KV cache, or one whose whole-row RoPE would
+    read past the tables (here one entry short), makes the launch touch no
+    cache or table entry and the next synchronising call report it; the
+    error is reported once, and a valid call afterwards works."""
+    nH, nKV, hd, maxSeq = 4, 2, 64, 64
+    Wq, Wk = nH * hd, nKV * hd
+    ld = Wq + 2 * Wk
+    p0 = {"short_table": 10, "past_cache": maxSeq - S + 1, "negative": -1}[case]
+    cos, sin = LO.precompute_rope(hd, maxSeq * nH, 10000.0)  # ample: every row's whole-row entries
+    n_tab = cos.size if case != "short_table" else (p0 + S) * (Wq // 2) - 1
+    print("bounds case", entry, S, case, p0, n_tab, flush=True)
+    qkv = prng.randn((S, ld), 60)
+    kc = prng.randn((nKV, maxSeq, hd), 61)
+    vc = prng.randn((nKV, maxSeq, hd), 62)
+    ctx = device.ops_ctx()
+    b = {}
+    for name, a in (("qkv", qkv), ("cos", cos[:n_tab]), ("sin", sin[:n_tab]), ("kc", kc), ("vc", vc)):
+        a = np.ascontiguousarray(a, np.float32)
+        b[name] = device.alloc(a.nbytes)
+        device.upload(b[name], a)
+    pos = device.alloc(4)
+    device.upload(pos, np.array([p0], np.int32))
+    out = device.alloc(S * Wq * 4)
+    parts = device.alloc(nH * MAXSPLIT * STRIDE * 4)
+
+    def call(p):
+        if entry == "attention":
+            return device.lib.smith_attention(ctx, b["qkv"], ld, p, S, nH, nKV, hd, b["cos"], b["sin"], n_tab,
+                                              b["kc"], b["vc"], maxSeq, out, None)
+        return device.lib.smith_attention_parts(ctx, b["qkv"], p, nH, nKV, hd, b["cos"], b["sin"], n_tab, None,
+                                                b["kc"], b["vc"], maxSeq, parts)
+    assert call(pos) == 0  # enqueued: the position is only known on the device
+    assert device.lib.smith_sync(ctx) != 0
+    msg = device.lib.smith_last_error(ctx).decode()
+    assert "outside the KV cache or the whole-row RoPE table" in msg and str(p0) in msg, msg
+    device.sync()  # reported once
+    assert np.array_equal(device.download(b["kc"], kc.nbytes, np.float32).reshape(kc.shape), kc)
+    assert np.array_equal(device.download(b["vc"], vc.nbytes, np.float32).reshape(vc.shape), vc)
+    # a position inside both bounds runs normally afterwards
+    device.upload(pos, np.array([0], np.int32))
+    assert call(pos) == 0
+    device.sync()

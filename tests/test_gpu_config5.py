@@ -1,0 +1,85 @@
+"""Config 5 at its stated workload: a seeded synthetic 32-layer Llama GGUF
+(dim 3072, 24/8 heads, head_dim 128, FFN 9216, vocab 32000,
+context_length 8192), a seeded 128-token prompt and 128 greedy tokens
+(gguf_cache.js:309-371, generate.js:70-76), for the Q4_0 linears and for the
+Q4_K_M type mix.  The GGUF seed and the prompt are those bench.py measures.
+
+The GPU's greedy graph path produces the tokens; the oracle then runs the
+whole teacher-forced sequence (prompt + the first 127 generated tokens) as
+one causal forward, decoding one layer of weights at a time, which gives the
+logits of all 128 steps at once.  Bars:
+  * every step's GPU logits (prefill, then host-driven forwardDecode along
+    the same tokens) within 1e-2 normwise of the oracle's;
+  * every generated token equal to the oracle's argmax at that step, except
+    where the oracle's top two logits are closer than twice the step's
+    largest logit error (then either may win within the tolerance).
+"""
+import sys
+import time
+
+import numpy as np
+import pytest
+
+from oracle import llama_oracle as LO
+from oracle.oracle import normwise_rel_err
+from smith_amd import prng
+from smith_amd.gguf_loader import loadGGUF
+from smith_amd.synthetic_gguf import CONFIG5, build_llama_gguf
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+PROMPT, NEW = 128, 128
+
+
+def _progress(msg):
+    # outside pytest's capture, so a long oracle run shows it is alive
+    print("[config5] " + msg, file=sys.__stderr__, flush=True)
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("mix", ["q4_0", "q4_k_m"])
+def test_config5_full_workload(tmp_path_factory, mix):
+    c = CONFIG5
+    path = str(tmp_path_factory.mktemp("c5") / ("c5_%s.gguf" % mix))
+    t0 = time.time()
+    build_llama_gguf(path, dim=c["dim"], layers=c["layers"], heads=c["heads"], kv_heads=c["kv_heads"],
+                     ffn=c["ffn"], vocab=c["vocab"], context=c["context"], seed=1, mix=mix)
+    m = loadGGUF(path)
+    prompt = [int(x) for x in prng.randint(PROMPT, c["vocab"], 7)]
+    out = m.generate(prompt, {"maxTokens": NEW, "temperature": 0})
+    assert out[:PROMPT] == prompt and len(out) == PROMPT + NEW
+    gen = out[PROMPT:]
+    caches = m.createCache()
+    gpu = [m.forwardPrefill(prompt, caches)["logits"][-1]]
+    for i in range(NEW - 1):
+        gpu.append(m.forwardDecode(gen[i], PROMPT + i, caches)["logits"][0])
+    del m, caches
+    _progress("%s: GPU generate + %d host-driven steps in %.1f s; %d distinct tokens"
+              % (mix, NEW, time.time() - t0, len(set(gen))))
+
+    t0 = time.time()
+    ref = LO.LlamaOracle(path)
+    assert ref.lazy
+    ref_logits = ref.forward(prompt + gen[:NEW - 1], 0)[PROMPT - 1:]
+    _progress("%s: oracle forward of %d tokens in %.1f s" % (mix, PROMPT + NEW - 1, time.time() - t0))
+    assert ref_logits.shape == (NEW, c["vocab"])
+
+    errs = [normwise_rel_err(g, r) for g, r in zip(gpu, ref_logits)]
+    _progress("%s: logits error max %.2e (step %d), median %.2e, last %.2e"
+              % (mix, max(errs), int(np.argmax(errs)), float(np.median(errs)), errs[-1]))
+    assert max(errs) <= TOL, (mix, int(np.argmax(errs)), max(errs))
+    flips = 0
+    for i, (t, g, r) in enumerate(zip(gen, gpu, ref_logits)):
+        # the graph path's token is the argmax of the host-driven path's
+        # logits (same kernels up to the fused LM head), up to a near tie
+        gs = np.sort(g)[-2:]
+        assert t == int(np.argmax(g)) or gs[1] - gs[0] <= 1e-6 * abs(gs[1]), (mix, i, t, int(np.argmax(g)))
+        if t != int(np.argmax(r)):
+            # a token may differ from the oracle's only where the oracle's top
+            # two logits are closer than twice this step's largest logit error
+            # (within that error either can be the larger one)
+            flips += 1
+            rs = np.sort(r)[-2:]
+            assert rs[1] - rs[0] <= 2 * np.max(np.abs(g - r)), (mix, i, t, int(np.argmax(r)), rs[1] - rs[0])
+    _progress("%s: %d of %d tokens differ from the oracle's argmax (each a near tie)" % (mix, flips, NEW))

@@ -12,6 +12,11 @@
   lm-head layout    output.weight flat data read as [dim, vocab]: an F32
                     output.weight holding E^T equals weight tying
   GGUF parsing      the product writer's file read back by the oracle reader
+  silu / SwiGLU     silu(0) = 0, silu(1) = sigmoid(1), silu(-x) = silu(x) - x,
+                    the limits; silu(gate) * up on an asymmetric pair, and the
+                    layer's FFN wiring on a hand-built layer (gate != up)
+  attention         two keys at head_dim 4: weights e^(s_i / sqrt(4)) / sum,
+                    directly and through a hand-built layer (causal row 0)
 """
 import os
 
@@ -111,3 +116,84 @@ def test_lm_head_layout_matches_tying(tmp_path):
     la = LO.LlamaOracle(a).forward(toks, 0)
     lb = LO.LlamaOracle(b).forward(toks, 0)
     assert np.max(np.abs(la - lb)) < 1e-9
+
+
+# --- SwiGLU and attention pins (closed forms and hand-computed numbers) ---
+SIG1 = 0.7310585786300049  # sigmoid(1) = 1 / (1 + e^-1)
+
+
+def test_silu_closed_forms():
+    assert LO.silu(np.array(0.0)) == 0.0
+    assert np.isclose(LO.silu(np.array(1.0)), SIG1, rtol=0, atol=1e-15)
+    x = np.array([0.3, 1.7, 4.0, 11.0])
+    assert np.allclose(LO.silu(-x), LO.silu(x) - x, rtol=0, atol=1e-14)  # silu(-x) = silu(x) - x
+    assert np.isclose(LO.silu(np.array(40.0)), 40.0, rtol=1e-15)  # silu(x) -> x
+    assert abs(LO.silu(np.array(-40.0))) < 1e-15  # silu(x) -> 0 for x -> -inf
+
+
+def test_swiglu_operand_order():
+    # silu(gate) * up: silu(2) * 3 = 3 * 2 / (1 + e^-2); the swapped form gives silu(3) * 2
+    got = LO.swiglu(np.array([2.0]), np.array([3.0]))[0]
+    assert np.isclose(got, 5.284782467867515, rtol=0, atol=1e-12)
+    assert not np.isclose(got, LO.swiglu(np.array([3.0]), np.array([2.0]))[0], atol=1e-3)
+
+
+def test_attend_two_keys_scale():
+    # hd = 4: scale 1/sqrt(4) = 0.5; scores 2 and 4 -> 1 and 2; weights e^1/(e^1+e^2), e^2/(e^1+e^2)
+    q = np.array([2.0, 0, 0, 0])
+    K = np.array([[1.0, 1, 1, 1], [2.0, 0, 0, 0]])
+    V = np.array([[1.0, 0, 5, 0], [0.0, 1, 0, 7]])
+    out = LO.attend(q, K, V, 0.5)
+    w0, w1 = 1 - SIG1, SIG1  # e/(e+e^2) = 1/(1+e) = 1 - sigmoid(1)
+    assert np.allclose(out, [w0, w1, 5 * w0, 7 * w1], rtol=0, atol=1e-15)
+
+
+def _toy(dim, ffn, blocks):
+    """A one-layer, one-head model built in memory (RoPE switched off by an
+    all-cos-1 table, eps 0) so a layer's output can be written down by hand."""
+    m = object.__new__(LO.LlamaOracle)
+    m.dim, m.L, m.nH, m.nKV, m.hd, m.kvd, m.ffn = dim, 1, 1, 1, dim, dim, ffn
+    m.eps, m.max_seq, m.lazy = 0.0, 8, False
+    m.cos, m.sin = np.ones(8 * dim), np.zeros(8 * dim)
+    m.blocks = [blocks]
+    m.reset()
+    return m
+
+
+def test_layer_attention_scale_and_causality():
+    """Two positions, identity q/k/v/o, FFN off: row 0 attends only to key 0
+    (out = 2 x0); row 1 mixes values 0 and 1 with softmax weights of the
+    scores q1.k / sqrt(hd) = (2, 4) / 2.  A 1/hd scale, a missing scale or a
+    non-causal mask each give other numbers."""
+    I4, Z = np.eye(4), np.zeros((4, 2))
+    m = _toy(4, 2, dict(g1=np.ones(4), g2=np.ones(4), q=I4, k=I4, v=I4, o=I4, gate=Z, up=Z, down=np.zeros((2, 4))))
+    x = np.array([[1.0, 1, 1, 1], [2.0, 0, 0, 0]])  # both rows have rms 1
+    y = m._layer(0, x, 0)
+    assert np.allclose(y[0], 2 * x[0], rtol=0, atol=1e-15)
+    w0, w1 = 1 - SIG1, SIG1
+    assert np.allclose(y[1], x[1] + w0 * x[0] + w1 * x[1], rtol=0, atol=1e-15)
+
+
+def test_layer_swiglu_wiring():
+    """Attention off (zero v), x = (3, 4, 0, 0) so rmsnorm gives (1.2, 1.6, 0, 0);
+    gate = (1.2, 1.6), up = (0.5, 2.0); down scatters the two FFN outputs to
+    elements 0 and 2: out = x + (silu(1.2) * 0.5, 0, silu(1.6) * 2.0, 0)."""
+    Z4 = np.zeros((4, 4))
+    gate = np.zeros((4, 2)); gate[0, 0] = 1; gate[1, 1] = 1
+    up = np.zeros((4, 2)); up[0, 0] = 0.5 / 1.2; up[1, 1] = 2.0 / 1.6
+    down = np.zeros((2, 4)); down[0, 0] = 1; down[1, 2] = 1
+    m = _toy(4, 2, dict(g1=np.ones(4), g2=np.ones(4), q=Z4, k=Z4, v=Z4, o=Z4, gate=gate, up=up, down=down))
+    x = np.array([[3.0, 4, 0, 0]])
+    y = m._layer(0, x, 0)[0]
+    s12 = 1.2 / (1 + np.exp(-1.2)) * 0.5
+    s16 = 1.6 / (1 + np.exp(-1.6)) * 2.0
+    assert np.allclose(y, [3 + s12, 4, s16, 0], rtol=0, atol=1e-14)
+
+
+def test_layer_at_a_time_decode_equals_resident_weights(tiny):
+    """The layer-at-a-time weight decoding used for config-5-sized models
+    gives the same logits as keeping every layer decoded."""
+    toks = [5, 17, 3, 88]
+    a = LO.LlamaOracle(tiny, lazy=False).forward(toks, 0)
+    b = LO.LlamaOracle(tiny, lazy=True).forward(toks, 0)
+    assert np.max(np.abs(a - b)) <= 1e-12 * np.max(np.abs(a))  # BLAS order only
