@@ -123,6 +123,20 @@ int smith_quantize_q8(void* ctx, const float* w, void* out, uint32_t K, uint32_t
 int smith_matmul_q4(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
                     uint32_t K, uint32_t groups);
 
+/* smith_matmul_q4 without any allocation.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels and results as smith_matmul_q4, but the split-K partials,
+ * counters and activation staging live in a static 32 MiB device array per
+ * GPU (held until the process ends): 64 KiB of counters, 4 MiB of
+ * activation staging, the rest split-K partials.  A shape whose scratch does
+ * not fit returns -1 with the sizes in smith_last_error (e.g. the M >= 256
+ * prefill GEMM at K = 14336); no hipMalloc / hipFree is ever called.  Calls
+ * that overlap on one GPU (two contexts or streams at once) race on the
+ * array. */
+int smith_matmul_q4_noalloc(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
+                            uint32_t K, uint32_t groups);
+
 /* matmulQ8 (src/ops/quantize.js:99-118): out[M,N] = a[M,K] . deq(wq). */
 int smith_matmul_q8(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
                     uint32_t K, uint32_t groups);

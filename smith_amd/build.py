@@ -3,7 +3,7 @@
   smith_amd/lib/smith_kernels.hsaco   hipcc --offload-device-only --offload-arch=gfx950
   smith_amd/lib/smith_llama.hsaco     (the GGUF decode-path kernels, same flags)
   smith_amd/lib/smith_gemm.hsaco      (the prefill MFMA GEMM, same flags)
-  smith_amd/lib/libsmith.so           g++ host code against libamdhip64
+  smith_amd/lib/libsmith.so           hipcc -x hip: host code against libamdhip64 (+ static device scratch)
 
 Run as `python -m smith_amd.build`; __graft_entry__.build() calls build().
 """
@@ -41,8 +41,10 @@ def _kernel_cmds():
 
 
 def _bridge_cmd():
-    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-result",
-            "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROCM, "include"),
+    # compiled as HIP: besides the host code it holds the static device
+    # scratch of smith_matmul_q4_noalloc (a gfx950 code object with no kernels)
+    return [os.path.join(ROCM, "bin", "hipcc"), "-x", "hip", *HIP_FLAGS, "-fPIC", "-shared", "-Wall",
+            "-Wno-unused-result", "-Wno-unused-value", "-I" + os.path.join(ROCM, "include"),
             os.path.join(CSRC, "smith_bridge.cpp"), "-o", LIBSMITH,
             "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc",
             "-Wl,-rpath," + os.path.join(ROCM, "lib")]

@@ -65,6 +65,9 @@ struct Ctx {
   uint32_t* att_cnt = nullptr;
   size_t att_cnt_n = 0;
   bool capturing = false;
+  // set while an entry point that must not allocate runs on the static
+  // scratch (its name, for the error when a region is too small)
+  const char* no_alloc = nullptr;
   // device-side position bound failures (attention, KV append): host-mapped
   // words {code, p0, S} the kernels store into, read at every synchronising
   // call (pos_err_host) and passed to kernels as pos_err_dev
@@ -185,6 +188,9 @@ int launch(Ctx* c, const char* name, dim3 grid, dim3 block, void** args, unsigne
 // stream so no enqueued kernel still uses the old allocation.
 int ensure(Ctx* c, void** p, size_t* have, size_t need) {
   if (need <= *have) return 0;
+  if (c->no_alloc)
+    return fail(c, "%s: needs a %zu-byte scratch region, the static scratch region holds %zu bytes (use the "
+                "allocating entry point for this size)", c->no_alloc, need, *have);
   if (c->capturing)
     return fail(c, "smith: scratch of %zu bytes needed while capturing a graph; run the op once before capture",
                 need);
@@ -215,6 +221,8 @@ int check_pos_err(Ctx* c) {
 
 int ensure_counters(Ctx* c, size_t n) {
   if (n <= c->counters_n) return 0;
+  if (c->no_alloc)
+    return fail(c, "%s: needs %zu split-K counters, the static scratch holds %zu", c->no_alloc, n, c->counters_n);
   if (c->capturing) return fail(c, "smith: split-K counters needed while capturing a graph; run the op once first");
   HIPCHK(c, hipStreamSynchronize(c->stream));
   if (c->counters) c->retired.push_back(c->counters);  // a captured graph may still use them
@@ -531,6 +539,41 @@ struct SmithEncoder {
   bool failed = false;
 };
 
+// Static device scratch of smith_matmul_q4_noalloc (for callers that cannot
+// allocate: code under HIP graph capture, serving loops, harnesses that
+// forbid hipMalloc).  Each GPU the library runs on holds its own copy until
+// the process ends.  Host code never passes `scratch` itself to a kernel (in
+// host code the name is a host-side stand-in, not a device address): the
+// device address comes from hipGetSymbolAddress, once per device at set-up,
+// into g_scratch_dev[device].
+//   [0, 64 KiB)            split-K counters (16384 x u32; zero at load and
+//                          after every launch: each kernel's last workgroup
+//                          resets the counters it used)
+//   [64 KiB, +4 MiB)       activation fragments (M > 8 GEMV prep; f16 A of
+//                          the M >= 64 GEMM)
+//   [4 MiB + 64 KiB, 32 MiB)  split-K partials
+constexpr size_t NOALLOC_BYTES = 32u << 20;
+constexpr size_t NOALLOC_CNT_BYTES = 64u << 10;
+constexpr size_t NOALLOC_PREP_BYTES = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static void* g_scratch_dev[NOALLOC_MAX_DEVICES];
+
+// Once per device, with that device current: the device address of its copy
+// of `scratch`, and its counter region cleared (outside any capture).
+static int noalloc_setup(Ctx* c) {
+  if (c->device < 0 || c->device >= NOALLOC_MAX_DEVICES)
+    return fail(c, "smith: device %d beyond the static scratch table", c->device);
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_scratch_dev[c->device]) return 0;
+  void* ptr = nullptr;
+  HIPCHK(c, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  HIPCHK(c, hipMemset(ptr, 0, NOALLOC_CNT_BYTES));
+  HIPCHK(c, hipDeviceSynchronize());
+  g_scratch_dev[c->device] = ptr;
+  return 0;
+}
+
 extern "C" {
 
 // ---------------- lifecycle ----------------
@@ -547,6 +590,11 @@ void* smith_init(void) {
     return nullptr;
   }
   memset(c->pos_err_host, 0, 256);
+  if (noalloc_setup(c)) {
+    hipHostFree(c->pos_err_host);
+    delete c;
+    return nullptr;
+  }
   return c;
 }
 
@@ -1044,6 +1092,35 @@ int smith_matmul_q4(void* ctx, const float* a, const void* wq, float* out, uint3
   if (groups != (K + 31) / 32)
     return fail(c, "matmulQ4: groups %u does not match ceil(K/32) for K=%u", groups, K);
   return qmatmul(c, FQ4S, a, wq, nullptr, out, M, N, K, groups);
+}
+
+int smith_matmul_q4_noalloc(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
+                            uint32_t K, uint32_t groups) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (groups != (K + 31) / 32)
+    return fail(c, "matmulQ4: groups %u does not match ceil(K/32) for K=%u", groups, K);
+  if (set_device(c)) return -1;
+  uint8_t* base = (uint8_t*)g_scratch_dev[c->device];
+  if (!base) return fail(c, "smith_matmul_q4_noalloc: static scratch not set up on device %d", c->device);
+  // run the allocating entry point's kernels on the static regions: every
+  // ensure() below finds its region big enough or fails (no_alloc set)
+  struct Saved {
+    void* prep; size_t prep_bytes; void* a16; size_t a16_bytes; float* ws; size_t ws_bytes;
+    uint32_t* counters; size_t counters_n;
+  } sv = {c->prep, c->prep_bytes, c->a16, c->a16_bytes, c->ws, c->ws_bytes, c->counters, c->counters_n};
+  c->counters = (uint32_t*)base;
+  c->counters_n = NOALLOC_CNT_BYTES / sizeof(uint32_t);
+  c->prep = c->a16 = base + NOALLOC_CNT_BYTES;
+  c->prep_bytes = c->a16_bytes = NOALLOC_PREP_BYTES;
+  c->ws = (float*)(base + NOALLOC_CNT_BYTES + NOALLOC_PREP_BYTES);
+  c->ws_bytes = NOALLOC_BYTES - NOALLOC_CNT_BYTES - NOALLOC_PREP_BYTES;
+  c->no_alloc = "smith_matmul_q4_noalloc";
+  const int rc = qmatmul(c, FQ4S, a, wq, nullptr, out, M, N, K, groups);
+  c->no_alloc = nullptr;
+  c->prep = sv.prep, c->prep_bytes = sv.prep_bytes, c->a16 = sv.a16, c->a16_bytes = sv.a16_bytes;
+  c->ws = sv.ws, c->ws_bytes = sv.ws_bytes, c->counters = sv.counters, c->counters_n = sv.counters_n;
+  return rc;
 }
 
 int smith_matmul_q8(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N, uint32_t K,

@@ -72,6 +72,7 @@ SYMBOLS = {
     "smith_quantize_q4": (_INT, [_P, _P, _P, _U32, _U32]),
     "smith_quantize_q8": (_INT, [_P, _P, _P, _U32, _U32]),
     "smith_matmul_q4": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
+    "smith_matmul_q4_noalloc": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "smith_matmul_q8": (_INT, [_P, _P, _P, _P, _U32, _U32, _U32, _U32]),
     "smith_repack_q4_0": (_INT, [_P, _P, _P, _P, _U32, _U32]),
     "smith_matmul_q4_0": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32]),
