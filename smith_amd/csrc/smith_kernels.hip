@@ -461,8 +461,20 @@ struct Rec {
   u32x4 q8b;      // Q8: int8 16..31 (+ one spare dword for the 2-byte shift)
   uint32_t q8c;
   uint32_t sh;
-  float s, z;
+  float s, z;     // Q4S: scale, zero (0 for a record outside the weight)
+  uint32_t sb;    // Q4_0: the f16 scale's raw bits, converted where used
+  bool ok;        // Q4_0: record inside the weight
 };
+
+// The record's scale.  Q4_0 scales stay raw 16-bit load results until the
+// post-step: converting them where they are loaded made every wave wait for
+// its scale loads before issuing the nibble loads behind them.
+template <int FMT>
+__device__ __forceinline__ float rec_scale(const Rec<FMT>& r) {
+  if (FMT == FMT_Q40 || FMT == FMT_Q40T)
+    return r.ok ? (float)__builtin_bit_cast(_Float16, (uint16_t)r.sb) : 0.f;
+  return r.s;
+}
 
 template <int FMT>
 __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
@@ -483,10 +495,14 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
     uint32_t nn = n < N ? n : N - 1, gg = g < G ? g : G - 1;
     rec = ((size_t)(nn >> 4) * G + gg) * 16 + (nn & 15);
     r.q = *(const u32x4*)(B + rec * 16);
-    r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
+    r.sb = D[rec];
+    r.ok = ok;
+    return r;
   } else if (FMT == FMT_Q40) {
     r.q = *(const u32x4*)(B + rec * 16);
-    r.s = (float)__builtin_bit_cast(_Float16, D[rec]);
+    r.sb = D[rec];
+    r.ok = ok;
+    return r;
   } else {
     // the 36 bytes from the dword holding the record's first byte, in two
     // 128-bit loads + one dword (global loads need dword alignment only):
@@ -552,9 +568,12 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   constexpr int KB = GPW * WK;         // groups per block
   constexpr int BC = 16 * CT * WN;     // block columns
   constexpr int NT = 64 * WK * WN;     // threads
-  constexpr int NCH = KB * MR * 4;     // prep chunks: (group, row, mfma slice)
-  constexpr int CPT = (NCH + NT - 1) / NT;
-  __shared__ u32x4 fragL[KB][2 * MR + 1][4];  // [group][row u][mfma i]; row 2*MR stays zero
+  // prep chunks (group, row, mfma slice) of one wave's own GPW groups: each
+  // wave converts exactly the activations its MFMAs read, so the fragments
+  // need only a wave-level barrier (no workgroup barrier before the MFMAs)
+  constexpr int NCHW = GPW * MR * 4;
+  constexpr int CPT = (NCHW + 63) / 64;
+  __shared__ u32x4 fragL[KB][2 * MR][4];  // [group][row u][mfma i]
   __shared__ float2 cL[KB][MR];           // (C1, S) with hi + lo/2048 folded
   __shared__ float red[WK][MR][BC];
   __shared__ float nred[MR][WK * WN];
@@ -580,10 +599,10 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   if (gamma) {
 #pragma unroll
     for (int cc = 0; cc < CPT; cc++) {
-      uint32_t ch = threadIdx.x + cc * NT;
-      uint32_t i = ch & 3, gl = (ch >> 2) / MR;
+      uint32_t ch = lane + cc * 64;
+      uint32_t i = ch & 3, gl = wk * GPW + (ch >> 2) / MR;
       uint32_t k0 = (gb + gl) * 32 + 8 * i;
-      bool in = ch < (uint32_t)NCH && k0 + 8 <= K;
+      bool in = ch < (uint32_t)NCHW && k0 + 8 <= K;
       const float4* gp = (const float4*)(gamma + (in ? k0 : 0));
       float4 g0 = gp[0], g1 = gp[1];
       gv[cc][0] = g0.x; gv[cc][1] = g0.y; gv[cc][2] = g0.z; gv[cc][3] = g0.w;
@@ -592,10 +611,10 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   }
 #pragma unroll
   for (int cc = 0; cc < CPT; cc++) {
-    uint32_t ch = threadIdx.x + cc * NT;
-    uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
+    uint32_t ch = lane + cc * 64;
+    uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = wk * GPW + (ch >> 2) / MR;
     uint32_t k0 = (gb + gl) * 32 + 8 * i;
-    bool ok = ch < (uint32_t)NCH && m < M && k0 + 8 <= K;
+    bool ok = ch < (uint32_t)NCHW && m < M && k0 + 8 <= K;
     if (ok) {
       const float4* ap = (const float4*)(A + (size_t)m * K + k0);
       float4 x0 = ap[0], x1 = ap[1];
@@ -605,29 +624,14 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         uint32_t k = k0 + e;
-        av[cc][e] = (ch < (uint32_t)NCH && m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
+        av[cc][e] = (ch < (uint32_t)NCHW && m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
       }
     }
   }
 
   // 2. weights: every record of this wave, all loads in flight
   Rec<FMT> wr[S][CT];
-  if (FMT == FMT_Q40T && n0 + 16 * CT <= N && gw + 4 * S <= G) {
-    // interior wave of the tile-major layout: one base address, the records
-    // of step st / tile ct at fixed offsets (1 KB per step of 4 groups)
-    const size_t rec0 = ((size_t)(n0 >> 4) * G + gw + j) * 16 + c;
-    const uint8_t* pb = B + rec0 * 16;
-    const uint16_t* pd = D + rec0;
-#pragma unroll
-    for (int st = 0; st < S; st++)
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++) {
-        wr[st][ct].q = *(const u32x4*)(pb + (size_t)ct * G * 256 + st * 1024);
-        wr[st][ct].s = (float)__builtin_bit_cast(_Float16, pd[(size_t)ct * G * 16 + st * 64]);
-        wr[st][ct].z = 0.f;
-        wr[st][ct].sh = 0;
-      }
-  } else {
+  {
 #pragma unroll
     for (int st = 0; st < S; st++)
 #pragma unroll
@@ -653,7 +657,6 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   }
 
   // 4. activations -> f16 hi/lo fragments + (C1, S) in LDS
-  for (uint32_t e = threadIdx.x; e < (uint32_t)KB * 4; e += NT) fragL[e >> 2][2 * MR][e & 3] = (u32x4){0u, 0u, 0u, 0u};
   float rms[MR];
   if (gamma) {
 #pragma unroll
@@ -670,8 +673,8 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     }
 #pragma unroll
     for (int cc = 0; cc < CPT; cc++) {
-      uint32_t ch = threadIdx.x + cc * NT;
-      uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
+      uint32_t ch = lane + cc * 64;
+      uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = wk * GPW + (ch >> 2) / MR;
       uint32_t k0 = (gb + gl) * 32 + 8 * i;
       float r = 0.f;
 #pragma unroll
@@ -682,8 +685,8 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   }
 #pragma unroll
   for (int cc = 0; cc < CPT; cc++) {
-    uint32_t ch = threadIdx.x + cc * NT;
-    uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = (ch >> 2) / MR;
+    uint32_t ch = lane + cc * 64;
+    uint32_t i = ch & 3, m = (ch >> 2) % MR, gl = wk * GPW + (ch >> 2) / MR;
     float c1h = 0.f, sh_ = 0.f, c1l = 0.f, sl = 0.f;
     _Float16 hv[8], lv[8];
 #pragma unroll
@@ -708,7 +711,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     c1 = add_xor2(add_xor1(c1));
     sm = add_xor2(add_xor1(sm));
     if (is_q40(FMT)) c1 = __builtin_fmaf(8.0f, sm, c1);
-    if (ch < (uint32_t)NCH) {
+    if (ch < (uint32_t)NCHW) {
       u32x4 hp, lp;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -720,23 +723,41 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
       if (i == 0) cL[gl][m] = make_float2(c1, sm);
     }
   }
-  __syncthreads();
+  // LDS operations of one wave complete in order
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // 5. MFMAs: lane (r = lane%16, j) feeds A row r from K slice j only
   const uint32_t r = lane & 15;
   const bool a_active = (r >> 2) == j && (r & 3) < 2 * MR;
-  const uint32_t ru = a_active ? (r & 3) : 2 * MR;  // inactive rows read the zero row
+  const uint32_t ru = r & 3;  // read by active lanes only
   float acc[CT][MR];
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
 #pragma unroll
     for (int m = 0; m < MR; m++) acc[ct][m] = 0.f;
+  // A fragments of every step into registers first.  Only the 2*MR lanes
+  // per lane group whose MFMA row carries an activation row read LDS (the
+  // exec-masked reads move 1/8 of the bytes a read by all 64 lanes would);
+  // the rest hold zeros.
+  u32x4 afr[S][4];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) afr[st][i] = (u32x4){0u, 0u, 0u, 0u};
+  if (a_active) {
+#pragma unroll
+    for (int st = 0; st < S; st++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) afr[st][i] = fragL[wk * GPW + 4 * st + j][ru][i];
+  }
 #pragma unroll
   for (int st = 0; st < S; st++) {
     const uint32_t gl = wk * GPW + 4 * st + j;
     half8 af[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) af[i] = __builtin_bit_cast(half8, fragL[gl][ru][i]);
+    for (int i = 0; i < 4; i++) af[i] = __builtin_bit_cast(half8, afr[st][i]);
     float2 cv[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) cv[m] = cL[gl][m];
@@ -746,7 +767,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 #pragma unroll
       for (int i = 0; i < 4; i++)
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], rec_to_f16<FMT>(wr[st][ct], i), p, 0, 0, 0);
-      float s = wr[st][ct].s, z = wr[st][ct].z;
+      float s = rec_scale(wr[st][ct]), z = wr[st][ct].z;
 #pragma unroll
       for (int m = 0; m < MR; m++) {
         float t = __builtin_fmaf(p[2 * m + 1], 1.0f / 2048.0f, p[2 * m]) - cv[m].x;
@@ -934,7 +955,7 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
       uint32_t sx[4], zx[4];
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        sx[t] = __float_as_uint(rr.s);
+        sx[t] = __float_as_uint(rec_scale(rr));
         zx[t] = __float_as_uint(rr.z);
       }
       xpose4(sx[0], sx[1], sx[2], sx[3]);
@@ -1017,6 +1038,8 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 // 9216 in one block); _c2: two 16-column tiles per wave (wide N).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_w16, FMT, 1, 1, 16, 1, 2)       \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64_w16, FMT, 1, 1, 16, 1, 1)        \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96, FMT, 1, 1, 8, 1, 3)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288, FMT, 1, 1, 8, 1, 9)            \
@@ -1230,7 +1253,8 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
       }
       // scale (and zero) of group t for this lane's column: register t after
       // the same transpose of four copies
-      uint32_t sv[4] = {__float_as_uint(rr.s), __float_as_uint(rr.s), __float_as_uint(rr.s), __float_as_uint(rr.s)};
+      const float rs = rec_scale(rr);
+      uint32_t sv[4] = {__float_as_uint(rs), __float_as_uint(rs), __float_as_uint(rs), __float_as_uint(rs)};
       xpose4(sv[0], sv[1], sv[2], sv[3]);
       uint32_t zv[4] = {0u, 0u, 0u, 0u};
       if (FMT == FMT_Q4S) {
