@@ -2,17 +2,20 @@
 
 Headline (value): matmulQ4 decode GEMV, M=1, Smith weight [K=4096, N=4096]
 quantized with quantizeQ4 (benchmark configuration 1), weights resident in HBM.
-A step = one matmulQ4 call (activation prep + MFMA GEMV).  The K timed steps
+A step = one matmulQ4 call (one fused MFMA GEMV launch).  The timed steps
 rotate over >= 400 MB of distinct weight copies so the 256 MB MALL cannot
-serve them.  value = algorithmic bytes per step / time per step (GB/s);
-roofline.achieved = algorithmic bytes / average duration of the GEMV kernel,
-from HIP events recorded around every GEMV launch on the stream it runs on.
+serve them; one rotation of steps is captured as a HIP graph and replayed,
+so the time per step is the device's (host launch cost out of the loop);
+the same steps launched one by one from Python are reported beside it.
+value = algorithmic bytes per step / time per step (GB/s); with one kernel
+per step, roofline.achieved is the same figure.  headline_q4_0 repeats the
+measurement on GGUF Q4_0 blocks (the GGUF decode layout).
 
-Also measured in the same run (under "configs"): Q4_0 GEMV (GGUF format),
-Q8 GEMV [4096 x 14336] (config 2), the Q4 batched-decode sweep (config 3, on
-quantizeQ4 records and on GGUF Q4_0 blocks),
-the Q4 prefill shapes (config 4), and the CPU baseline: the oracle's
-dequantize + f32 matmul (single thread) on a bounded sample of config 1.
+Also measured in the same run (under "configs"): Q8 GEMV [4096 x 14336]
+(config 2), the Q4 batched-decode sweep (config 3, on quantizeQ4 records and
+on GGUF Q4_0 blocks), the Q4 prefill shapes (config 4), the end-to-end
+config-5 decode, and the CPU baselines: the oracle's dequantize + f32 matmul
+(single thread) on a bounded sample of config 1.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -30,10 +33,12 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 400 << 20
-# HBM bytes per config-1 GEMV launch from two rocprofv3 --pmc passes
-# (the committed qgemv1 config-1 HBM traffic profile): FETCH_SIZE 6273.5 KiB x 1.996
-# (factor from a 12,582,912 B device copy) + WRITE_SIZE 16.0 KiB x 1.0.
+# HBM bytes per config-1 GEMV launch from two rocprofv3 --pmc passes over
+# this kernel (FETCH_SIZE, then WRITE_SIZE, per dispatch), FETCH_SIZE scaled
+# by the factor a plain device copy of known size gives; the profile named in
+# TRAFFIC_SOURCE holds the commands and the figures.
 TRAFFIC_CFG1 = 12829235
+TRAFFIC_SOURCE = "profiles/qgemv1_q4s_m1_cfg1_hbm_traffic.md"
 
 
 def log(*a):
@@ -76,12 +81,12 @@ class Weights:
 
 
 def time_steps(D, step, steps, warmup, rotation=1, graph=False):
-    """ms per step over `steps` back-to-back calls, HIP events on the library
-    stream around the whole timed region, and the number of kernel launches
-    one step makes (counted in a separate, untimed pass).  graph=True: one
-    weight rotation of steps (`rotation` calls, each its own launches with
-    its own weight copy) is captured once as a HIP graph and the graph is
-    replayed until `steps` steps ran (launch-bound loops go through graphs)."""
+    """ms per step over exactly `steps` calls, HIP events on the library
+    stream around the timed region, and the number of kernel launches one
+    step makes (counted in a separate, untimed pass).  graph=True: the
+    `steps` calls (step i on weight copy i % rotation, each its own launches)
+    are captured once as a HIP graph, replayed once untimed, then replayed
+    once timed (launch-bound loops go through graphs)."""
     for i in range(warmup):
         step(i)
     D.sync()
@@ -89,7 +94,7 @@ def time_steps(D, step, steps, warmup, rotation=1, graph=False):
     if graph:
         D.check(D.lib.smith_graph_begin(D.ops_ctx()), "graph begin")
         try:
-            for i in range(rotation):
+            for i in range(steps):
                 step(i)
         finally:
             g = D.lib.smith_graph_end(D.ops_ctx())
@@ -99,14 +104,10 @@ def time_steps(D, step, steps, warmup, rotation=1, graph=False):
         D.sync()
     D.timer_start()
     if g is not None:
-        reps = -(-steps // rotation)
-        for _ in range(reps):
-            D.check(D.lib.smith_graph_launch(D.ops_ctx(), g), "graph launch")
-        ran = reps * rotation
+        D.check(D.lib.smith_graph_launch(D.ops_ctx(), g), "graph launch")
     else:
         for i in range(steps):
             step(i)
-        ran = steps
     ms = D.timer_stop()
     if g is not None:
         D.lib.smith_graph_destroy(g)
@@ -114,7 +115,7 @@ def time_steps(D, step, steps, warmup, rotation=1, graph=False):
     step(0)
     _, launches = D.profile_read("")
     D.profile_kernels(False)
-    return ms / ran, {"launches_per_step": launches, "steps_timed": ran, "graph": g is not None}
+    return ms / steps, {"launches_per_step": launches, "steps_timed": steps, "graph": g is not None}
 
 
 _Q4S_CACHE = {}
@@ -142,7 +143,7 @@ def bench_q4s(D, S, prng, M, K, N, steps, warmup, graph=False):
     return ms, kt, alg_bytes(q4s_bytes(K, N), M, K, N)
 
 
-def bench_q8(D, S, prng, M, K, N, steps, warmup):
+def bench_q8(D, S, prng, M, K, N, steps, warmup, graph=False):
     q = S.quantizeQ8(prng.randn((K, N), 1, std=0.02))
     W = Weights(D, q["buffer"], q["totalBytes"])
     a = S.tensor(prng.randn((M, K), 0))
@@ -154,13 +155,13 @@ def bench_q8(D, S, prng, M, K, N, steps, warmup):
     def step(i):
         D.lib.smith_matmul_q8(ctx, a.buffer, bufs[i % len(bufs)], out.buffer, M, N, K, G)
 
-    ms, kt = time_steps(D, step, steps, warmup)
+    ms, kt = time_steps(D, step, steps, warmup, graph=graph)
     for b in bufs[1:]:
         D.release_buffer(b)
     return ms, kt, alg_bytes(q8_bytes(K, N), M, K, N)
 
 
-def bench_q40(D, S, prng, M, K, N, steps, warmup):
+def bench_q40(D, S, prng, M, K, N, steps, warmup, graph=False):
     """GGUF Q4_0 blocks as the GGUF decode path holds them: nibble and scale
     planes in 16-column tile-major order (smith_repack_q4_0_t_into), through
     smith_linear_q4_0_t (the same GEMV kernels as matmulQ4 for M <= 32)."""
@@ -180,7 +181,7 @@ def bench_q40(D, S, prng, M, K, N, steps, warmup):
         j = i % len(W.bufs)
         D.lib.smith_linear_q4_0_t(ctx, a.buffer, W.bufs[j], W.extra[j][0], out.buffer, M, N, K, None, 0.0, None, 0)
 
-    ms, kt = time_steps(D, step, steps, warmup)
+    ms, kt = time_steps(D, step, steps, warmup, rotation=len(W.bufs), graph=graph)
     for b in W.bufs[1:]:
         D.release_buffer(b)
     for eb, _ in W.extra[1:]:
@@ -316,6 +317,37 @@ def calibrate(D, steps):
     return res
 
 
+def bench_sweeps(D, S, prng):
+    """Config 2 and the config-3 sweeps (Q4S records and GGUF Q4_0 blocks),
+    each point graph-replayed."""
+    configs = {}
+    sub = 100  # sweep points: enough graph-replayed steps to amortise the graph launch
+    ms8, kt8, b8 = bench_q8(D, S, prng, 1, 4096, 14336, sub, 5, graph=True)
+    configs["cfg2_q8_gemv_M1_K4096_N14336"] = {
+        "GBps": round(b8 / ms8 / 1e6, 1), "pct_hbm_peak": round(b8 / ms8 / 1e6 / HBM_PEAK_GBS * 100, 2),
+        "us_step": round(ms8 * 1e3, 2), "kernels_per_step": kt8["launches_per_step"]}
+    log("cfg2:", configs["cfg2_q8_gemv_M1_K4096_N14336"])
+    sweep = {}
+    for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
+        for M in (1, 4, 8, 16, 32):
+            msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, sub, 5, graph=True)
+            sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = {
+                "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
+                "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
+    configs["cfg3_q4s_batched_decode"] = sweep
+    log("cfg3:", json.dumps(sweep))
+    sweep40 = {}  # the same sweep on GGUF Q4_0 blocks (18 B per 32 weights, tile-major planes)
+    for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
+        for M in (1, 4, 8, 16, 32):
+            msx, ktx, bx = bench_q40(D, S, prng, M, Kk, Nn, sub, 5, graph=True)
+            sweep40["M%d_N%d_K%d" % (M, Nn, Kk)] = {
+                "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
+                "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
+    configs["cfg3_q4_0_batched_decode"] = sweep40
+    log("cfg3 q4_0:", json.dumps(sweep40))
+    return configs
+
+
 def e2e_weight_bytes(mix):
     """HBM bytes of weights one decode token streams at config 5."""
     c = __import__("smith_amd.synthetic_gguf", fromlist=["CONFIG5"]).CONFIG5
@@ -379,6 +411,7 @@ def main():
     ap.add_argument("--calibrate", action="store_true", help="print the platform floor (empty kernel, streaming read)")
     ap.add_argument("--e2e-only", action="store_true", help="only the config-5 end-to-end decode")
     ap.add_argument("--cfg4-only", action="store_true", help="only the config-4 prefill GEMMs")
+    ap.add_argument("--cfg3-only", action="store_true", help="only the config-2/3 GEMV sweep")
     ap.add_argument("--gguf", default="/tmp/smith_config5.gguf", help="synthetic config-5 GGUF path (written if absent)")
     ap.add_argument("--mix", default="q4_0", choices=["q4_0", "q4_k_m"], help="config-5 weight types for --e2e-only")
     args = ap.parse_args()
@@ -403,48 +436,31 @@ def main():
     if args.cfg4_only:
         print(json.dumps({"cfg4_q4s_prefill": bench_cfg4(D, S, prng)}), flush=True)
         return
+    if args.cfg3_only:
+        print(json.dumps(bench_sweeps(D, S, prng)), flush=True)
+        return
     K = N = 4096
-    # back-to-back stream launches (the value); the same steps replayed from a
-    # captured HIP graph reported beside them
-    ms, kt, nbytes = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup)
-    ms_graph, _, _ = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup, graph=True)
+    # The value: matmulQ4 steps captured once as a HIP graph (one launch per
+    # step, each step on its own weight copy) and replayed, so the figure is
+    # the device's per-step time; the same steps launched one by one from
+    # Python (ctypes -> bridge -> hipModuleLaunchKernel, ~4 us of host time
+    # per call) are reported beside it
+    ms_stream, kt, nbytes = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup)
+    ms, ktg, _ = bench_q4s(D, S, prng, 1, K, N, args.steps, args.warmup, graph=True)
     assert kt["launches_per_step"] == 1, kt  # the M=1 path is one fused kernel
     value = nbytes / (ms * 1e-3) / 1e9
-    # one kernel per step: the timed-region average is that kernel's average
-    # launch-to-launch duration (including the gap between back-to-back launches)
+    # one kernel per step: the timed region's average is that kernel's
+    # average launch-to-launch duration on the library stream
     achieved = value
-    log("cfg1 q4s M=1: %.2f us/step = %.0f GB/s stream, %.2f us/step graph (%d kernel/step)"
-        % (ms * 1e3, value, ms_graph * 1e3, kt["launches_per_step"]))
+    ms40_stream, kt40, b40 = bench_q40(D, S, prng, 1, K, N, args.steps, args.warmup)
+    ms40, _, _ = bench_q40(D, S, prng, 1, K, N, args.steps, args.warmup, graph=True)
+    v40 = b40 / (ms40 * 1e-3) / 1e9
+    log("cfg1 q4s M=1: %.2f us/step graph = %.0f GB/s, %.2f us/step stream; q4_0: %.2f us graph = %.0f GB/s, %.2f stream"
+        % (ms * 1e3, value, ms_stream * 1e3, ms40 * 1e3, v40, ms40_stream * 1e3))
 
     configs = {}
     if not args.quick:
-        sub = max(20, args.steps // 4)
-        ms40, kt40, b40 = bench_q40(D, S, prng, 1, K, N, sub, 5)
-        configs["cfg1_q4_0_gemv_M1_4096x4096"] = {
-            "GBps": round(b40 / ms40 / 1e6, 1), "us_step": round(ms40 * 1e3, 2), "kernels_per_step": kt40["launches_per_step"]}
-        ms8, kt8, b8 = bench_q8(D, S, prng, 1, 4096, 14336, sub, 5)
-        configs["cfg2_q8_gemv_M1_K4096_N14336"] = {
-            "GBps": round(b8 / ms8 / 1e6, 1), "pct_hbm_peak": round(b8 / ms8 / 1e6 / HBM_PEAK_GBS * 100, 2),
-            "us_step": round(ms8 * 1e3, 2), "kernels_per_step": kt8["launches_per_step"]}
-        log("cfg2:", configs["cfg2_q8_gemv_M1_K4096_N14336"])
-        sweep = {}
-        for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
-            for M in (1, 4, 8, 16, 32):
-                msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, sub, 5)
-                sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = {
-                    "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
-                    "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
-        configs["cfg3_q4s_batched_decode"] = sweep
-        log("cfg3:", json.dumps(sweep))
-        sweep40 = {}  # the same sweep on GGUF Q4_0 blocks (18 B per 32 weights, tile-major planes)
-        for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
-            for M in (1, 4, 8, 16, 32):
-                msx, ktx, bx = bench_q40(D, S, prng, M, Kk, Nn, sub, 5)
-                sweep40["M%d_N%d_K%d" % (M, Nn, Kk)] = {
-                    "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
-                    "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
-        configs["cfg3_q4_0_batched_decode"] = sweep40
-        log("cfg3 q4_0:", json.dumps(sweep40))
+        configs.update(bench_sweeps(D, S, prng))
         pre = bench_cfg4(D, S, prng)
         configs["cfg4_q4s_prefill"] = pre
         log("cfg4:", json.dumps(pre))
@@ -471,20 +487,31 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
-        "ms_per_step_graph_replay": round(ms_graph, 6),
+        "ms_per_step_stream_launches": round(ms_stream, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (Q4S weights; exact f16 hi/lo MFMA, f32 accumulation)",
+        "dtype": "f32 in/out; Q4S weights exact in f16 MFMA operands; activations as f16 hi + lo*2048 pairs "
+                 "(~22 bits of each f32 kept) at M<=8, plain f16 at M 9-32; f32 accumulation",
         "data": "synthetic (SplitMix64/Box-Muller seeded: a~N(0,1) seed 0, W~N(0,0.02) seed 1)",
         "config": {"workload": "config 1: matmulQ4 GEMV M=1, Smith weight [K=4096, N=4096] quantizeQ4 (Q4S, "
                                "24 B/32 weights); weights rotated over >= 400 MB of copies",
                    "M": 1, "K": K, "N": N, "format": "Q4S", "algorithmic_bytes_per_step": nbytes,
-                   "timing": "HIP events around %d back-to-back stream launches" % kt["steps_timed"]},
+                   "timing": "HIP events on the library stream around %d steps replayed from a captured HIP graph "
+                             "(one kernel launch per step)" % ktg["steps_timed"]},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1,
-                     "kernel": "smith_qgemv1_q4s_m1_k128", "kernel_us": round(ms * 1e3, 3)},
+                     "traffic_source": TRAFFIC_SOURCE,
+                     "kernel": "smith_qgemv1_q4s_m1_k128", "step_us": round(ms * 1e3, 3)},
+        "headline_q4_0": {
+            "workload": "config 1 on GGUF Q4_0 blocks (18 B/32 weights, tile-major nibble/scale planes as the "
+                        "GGUF loader holds them), smith_linear_q4_0_t M=1, K=N=4096",
+            "value": round(v40, 2), "unit": "GB/s", "ms_per_step": round(ms40, 6),
+            "ms_per_step_stream_launches": round(ms40_stream, 6), "algorithmic_bytes_per_step": b40,
+            "roofline": {"bound": "hbm", "achieved": round(v40, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(v40 / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "smith_qgemv1_q40t_m1_k128", "step_us": round(ms40 * 1e3, 3)}},
         "cpu_baseline": cpu,
         "configs": configs,
     }

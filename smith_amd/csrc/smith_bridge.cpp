@@ -309,14 +309,18 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
     void* args[] = {&pa, &frag, &cst, &pM, &pK, &pG, &pRB};
     if (launch(c, name, dim3((unsigned)((threads + 255) / 256)), dim3(256), args)) return -1;
   }
-  const uint32_t bc = 32, kb = 32, nthreads = 512;  // CT=2, S=1, WK=8
+  // 32 columns per block (CT=2, S=1, WK=8), or 16 (the _c1 variants) when
+  // 32-column blocks would leave CUs idle (e.g. N = 1024: 128 -> 256 blocks)
+  const uint32_t kb = 32, nthreads = 512;
+  const uint32_t ksplit = (G + kb - 1) / kb;
+  const bool c1 = (uint64_t)((N + 31) / 32) * ksplit < 256;
+  const uint32_t bc = c1 ? 16 : 32;
   uint32_t gx = (N + bc - 1) / bc;
-  uint32_t ksplit = (G + kb - 1) / kb;
   if (ksplit > 1) {
     if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
     if (ensure_counters(c, gx)) return -1;
   }
-  snprintf(name, sizeof name, "smith_qgemv3_%s_m%u", tag, bucket);
+  snprintf(name, sizeof name, "smith_qgemv3_%s_m%u%s", tag, bucket, c1 ? "_c1" : "");
   const void* pB = B;
   const void* pD = D;
   float* pC = out;
@@ -351,7 +355,10 @@ int qgemv4_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
     const char* e = getenv("SMITH_QGEMV4_KB");
     return e ? atoi(e) : 0;
   }();
-  const uint32_t bc = 64;
+  // 64 columns per block; 32-column blocks (the _n32 variants, M <= 8) when
+  // even 16-group K splits leave fewer than ~200 blocks (e.g. N = 1024)
+  const bool n32 = M <= 8 && (uint64_t)((N + 63) / 64) * ((G + 15) / 16) < 200;
+  const uint32_t bc = n32 ? 32 : 64;
   const uint32_t gx = (N + bc - 1) / bc;
   uint32_t kb = force_kb == 16 ? 16 : 32;
   if (kb == 32 && (uint64_t)gx * ((G + 31) / 32) < 200) kb = 16;
@@ -361,7 +368,7 @@ int qgemv4_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
     if (ensure_counters(c, gx)) return -1;
   }
   char name[64];
-  snprintf(name, sizeof name, "smith_qgemv4_%s_%s_k%u", tag, rows, kb);
+  snprintf(name, sizeof name, "smith_qgemv4_%s_%s_k%u%s", tag, rows, kb, n32 ? "_n32" : "");
   const float* pa = a;
   const void* pB = B;
   const void* pD = D;

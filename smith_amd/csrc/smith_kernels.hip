@@ -324,12 +324,24 @@ __device__ __forceinline__ void qprep_body(const float* __restrict__ A, u32x4* _
   const float off_q4[8] = {1024.f, 1024.f, 64.f, 64.f, 1024.f, 1024.f, 64.f, 64.f};
   float hi_c1 = 0.f, hi_s = 0.f, lo_c1 = 0.f, lo_s = 0.f;
   _Float16 hv[8], lv[8];
+  // the slice's 8 elements, loaded together (two 16-byte loads when the
+  // slice lies inside an aligned row) before any of them is converted
+  float av[8];
+  const uint32_t k0 = g * 32 + kq * 8;
+  if (active && m < M && k0 + 8 <= K && K % 4 == 0) {
+    const float4* ap = (const float4*)(A + (size_t)m * K + k0);
+    const float4 x0 = ap[0], x1 = ap[1];
+    av[0] = x0.x; av[1] = x0.y; av[2] = x0.z; av[3] = x0.w;
+    av[4] = x1.x; av[5] = x1.y; av[6] = x1.z; av[7] = x1.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) av[e] = (active && m < M && k0 + e < K) ? A[(size_t)m * K + k0 + e] : 0.0f;
+  }
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     int e = FMT == FMT_Q8 ? perm_q8[j] : perm_q4[j];
     float off = FMT == FMT_Q8 ? 1152.f : off_q4[j];
-    uint32_t k = g * 32 + kq * 8 + e;
-    float a = (active && m < M && k < K) ? A[(size_t)m * K + k] : 0.0f;
+    float a = av[e];
     _Float16 h = (_Float16)a;
     hv[j] = h;
     float hf = (float)h;
@@ -1056,7 +1068,11 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   DEF_QGEMV3(smith_qgemv3_##TAG##_m4, FMT, 1, true, 4, 2, 1, 8, 1)        \
   DEF_QGEMV3(smith_qgemv3_##TAG##_m8, FMT, 1, true, 4, 2, 1, 8, 1)        \
   DEF_QGEMV3(smith_qgemv3_##TAG##_m16, FMT, 1, false, 4, 2, 1, 8, 1)      \
-  DEF_QGEMV3(smith_qgemv3_##TAG##_m32, FMT, 2, false, 4, 2, 1, 8, 1)
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m32, FMT, 2, false, 4, 2, 1, 8, 1)      \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m4_c1, FMT, 1, true, 4, 1, 1, 8, 1)     \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m8_c1, FMT, 1, true, 4, 1, 1, 8, 1)     \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m16_c1, FMT, 1, false, 4, 1, 1, 8, 1)   \
+  DEF_QGEMV3(smith_qgemv3_##TAG##_m32_c1, FMT, 2, false, 4, 1, 1, 8, 1)
 
 // ---------------------------------------------------------------------------
 // Batched decode GEMV for 2 < M <= 32 in ONE launch (activation prep fused).
@@ -1341,6 +1357,8 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
 #define DEF_QGEMV4_FMT(TAG, FMT)                                         \
   DEF_QGEMV4(smith_qgemv4_##TAG##_h8_k32, FMT, 1, true, 1, 4, 2, 4)      \
   DEF_QGEMV4(smith_qgemv4_##TAG##_h8_k16, FMT, 1, true, 1, 2, 2, 4)      \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_h8_k32_n32, FMT, 1, true, 1, 2, 4, 2)  \
+  DEF_QGEMV4(smith_qgemv4_##TAG##_h8_k16_n32, FMT, 1, true, 1, 1, 4, 2)  \
   DEF_QGEMV4(smith_qgemv4_##TAG##_p16_k32, FMT, 1, false, 1, 4, 2, 4)    \
   DEF_QGEMV4(smith_qgemv4_##TAG##_p16_k16, FMT, 1, false, 1, 2, 2, 4)    \
   DEF_QGEMV4(smith_qgemv4_##TAG##_p32_k32, FMT, 2, false, 1, 4, 2, 4)    \
@@ -1379,7 +1397,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   constexpr int GPW = 4 * S;
   constexpr int BC = 16 * CT;
   constexpr int GMAX = 4 * S * WK;
-  __shared__ u32x4 fragL[8 * GMAX + 4];  // [g][hi/lo][slice] + one zero fragment
+  __shared__ u32x4 fragL[8 * GMAX];  // [g][hi/lo][slice]
   __shared__ float red[WK][BC];
   constexpr bool NEED_S = F != FMT_Q40T;  // the affine term needs the group sums S
   constexpr bool HALVES = F == GT_Q6K;    // separate scales for elements 0-15 / 16-31
@@ -1402,9 +1420,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   const u32x4* frag = (const u32x4*)act;
   const float* c1p = (const float*)(act + (size_t)K * 4);
   constexpr int NT = 64 * WK;
-  constexpr int CPT = (8 * GMAX + NT - 1) / NT;   // frag words per thread (this block's groups)
   constexpr int SPL = (4 * GMAX + 63) / 64;       // part sums of squares per lane
-  u32x4 fv[CPT];
   float c1[S], c1b[S], sg[S], sgb[S];  // (C1, S) of the group, or of its halves (HALVES)
   float ssv[SPL];
   // SRC 1: split partials of this block's parts (part = 8 elements)
@@ -1412,10 +1428,16 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   float4 oa[PPT][ATTP_MAXSPLIT], ob[PPT][ATTP_MAXSPLIT];
   float mlv[2 * ATTP_MAXSPLIT];
   uint32_t nsplit = 1, h0 = 0;
+  // SRC 0: each wave copies the act fragments of its own GPW groups (8 per
+  // group: hi/lo x 4 slices) to its LDS slice with coalesced loads; after a
+  // wave-level barrier only the lanes whose MFMA row carries an activation
+  // row (2 of 16 per lane group) read their operands, the others hold zeros
+  constexpr int FPW = (8 * GPW + 63) / 64;  // fragment words per lane
+  u32x4 fv[FPW];
   if (SRC == 0) {
 #pragma unroll
-    for (int q = 0; q < CPT; q++) {
-      const uint32_t e = 8 * gb + threadIdx.x + q * NT;
+    for (int q = 0; q < FPW; q++) {
+      const uint32_t e = 8 * gw + lane + 64 * q;
       fv[q] = frag[e < 8 * G ? e : 8 * G - 1];  // clamped: branch-free issue
     }
 #pragma unroll
@@ -1513,14 +1535,16 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         }
       }
   }
-  if (threadIdx.x < 4) fragL[8 * GMAX + threadIdx.x] = (u32x4){0u, 0u, 0u, 0u};
   float ssum = 0.f;
   if (SRC == 0) {
 #pragma unroll
-    for (int q = 0; q < CPT; q++) {
-      const uint32_t e = threadIdx.x + q * NT;
-      if (e < 8 * GMAX) fragL[e] = fv[q];
+    for (int q = 0; q < FPW; q++) {
+      const uint32_t e = lane + 64 * q;
+      if (e < 8u * GPW) fragL[8 * wk * GPW + e] = fv[q];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (ksplit == 1)
 #pragma unroll
       for (int q = 0; q < SPL; q++) ssum += lane + 64 * q < T ? ssv[q] : 0.f;
@@ -1594,8 +1618,8 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         if (NEED_S) sL[pl] = sp_;
       }
     }
+    __syncthreads();
   }
-  __syncthreads();
   if (SRC == 1) {
 #pragma unroll
     for (int st = 0; st < S; st++) {
@@ -1613,18 +1637,22 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     }
   }
 
-  // 3. MFMAs and the exact per-group post-step (inactive lanes read zeros)
-  uint32_t abase[S];
-#pragma unroll
-  for (int st = 0; st < S; st++) {
-    const uint32_t g = gw + 4 * st + j;
-    abase[st] = a_active && g < G ? ((g - gb) * 2 + (r & 3)) * 4 : 8 * GMAX;
-  }
+  // 3. MFMAs and the exact per-group post-step
   float acc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ct++) acc[ct] = 0.f;
 #pragma unroll
   for (int st = 0; st < S; st++) {
+    // this step's A operands: LDS reads by the active lanes only (the
+    // others' rows are zero), just before the MFMAs that take them
+    u32x4 afr[4] = {(u32x4){0u, 0u, 0u, 0u}, (u32x4){0u, 0u, 0u, 0u}, (u32x4){0u, 0u, 0u, 0u},
+                    (u32x4){0u, 0u, 0u, 0u}};
+    {
+      const uint32_t g = gw + 4 * st + j;
+      if (a_active && g < G)
+#pragma unroll
+        for (int i = 0; i < 4; i++) afr[i] = fragL[((g - gb) * 2 + (r & 3)) * 4 + i];
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
       const uint32_t g = gw + 4 * st + j, n = n0 + 16 * ct + c;
@@ -1635,7 +1663,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         rr.q = wq[st][ct];
 #pragma unroll
         for (int i = 0; i < 4; i++)
-          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fragL[abase[st] + i]),
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, afr[i]),
                                                      rec_to_f16<FMT_Q40T>(rr, i), p, 0, 0, 0);
         const float sc = in ? (float)__builtin_bit_cast(_Float16, wd[st][ct]) : 0.f;
         const float t = __builtin_fmaf(p[1], 1.0f / 2048.0f, p[0]) - c1[st];
@@ -1644,7 +1672,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         // sum of a*(s*q + c) = s*X + (8s + c)*S with X = P - C1 (C1 carries
         // the +8S of the act): per group, or per 16-element half (Q6_K)
         const GtW<F>& w = gw_[st][ct];
-        const u32x4* fa = fragL + abase[st];
+        const u32x4* fa = afr;
         f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f}, p2 = (f32x4){0.f, 0.f, 0.f, 0.f};
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[0]), gt_to_f16<F, 0>(w), p, 0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, fa[1]), gt_to_f16<F, 1>(w), p, 0, 0, 0);
