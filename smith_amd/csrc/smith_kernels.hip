@@ -1791,6 +1791,8 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   DEF_AGEMV(smith_agemv_##TAG##_k144, F, 1, 3, 12)            \
   DEF_AGEMV(smith_agemv_##TAG##_k192, F, 1, 6, 8)             \
   DEF_AGEMV(smith_agemv_##TAG##_k288, F, 1, 9, 8)             \
+  DEF_AGEMV(smith_agemv_##TAG##_k96_c2, F, 2, 3, 8)           \
+  DEF_AGEMV(smith_agemv_##TAG##_k288_w12, F, 1, 6, 12)        \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k64, F, 1, 4, 4)      \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k96, F, 1, 3, 8)      \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k128, F, 1, 4, 8)     \
