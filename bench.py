@@ -37,7 +37,8 @@ ROTATE_BYTES = 400 << 20
 # this kernel (FETCH_SIZE, then WRITE_SIZE, per dispatch), FETCH_SIZE scaled
 # by the factor a plain device copy of known size gives; the profile named in
 # TRAFFIC_SOURCE holds the commands and the figures.
-TRAFFIC_CFG1 = 12829235
+TRAFFIC_CFG1 = 12805588
+TRAFFIC_CFG1_Q40 = 9670308
 TRAFFIC_SOURCE = "profiles/qgemv1_q4s_m1_cfg1_hbm_traffic.md"
 
 
@@ -510,7 +511,8 @@ def main():
             "value": round(v40, 2), "unit": "GB/s", "ms_per_step": round(ms40, 6),
             "ms_per_step_stream_launches": round(ms40_stream, 6), "algorithmic_bytes_per_step": b40,
             "roofline": {"bound": "hbm", "achieved": round(v40, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(v40 / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(v40 / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1_Q40,
+                         "traffic_source": TRAFFIC_SOURCE,
                          "kernel": "smith_qgemv1_q40t_m1_k128", "step_us": round(ms40 * 1e3, 3)}},
         "cpu_baseline": cpu,
         "configs": configs,
