@@ -404,9 +404,7 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
     if (ensure_counters(c, gx)) return -1;
   }
   char name[64];
-  static const char* v1sfx = getenv("SMITH_QGEMV1_SFX");
-  if (v1sfx && *v1sfx) threads = 1024;
-  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s%s", tag, M, kb, c2 ? "_c2" : "", v1sfx ? v1sfx : "");
+  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s", tag, M, kb, c2 ? "_c2" : "");
   const float* pa = a;
   const void* pB = B;
   const void* pD = D;

@@ -1050,8 +1050,6 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 // 9216 in one block); _c2: two 16-column tiles per wave (wide N).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_w16, FMT, 1, 1, 16, 1, 2)       \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64_w16, FMT, 1, 1, 16, 1, 1)        \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96, FMT, 1, 1, 8, 1, 3)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288, FMT, 1, 1, 8, 1, 9)            \
