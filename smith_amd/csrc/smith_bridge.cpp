@@ -1273,7 +1273,8 @@ int act_gemv(Ctx* c, const char* fn, Fmt fmt, const void* act_in, int norm, floa
   // 1.25 per CU (config-5 decode 948 -> 973-980 tok/s with both)
   uint32_t gxx = gx, thr = threads;
   if (kb == 288) {
-    strncat(name, "_w12", sizeof name - strlen(name) - 1);
+    // without a norm (the down projection): the variant that has no norm code
+    strncat(name, norm ? "_w12" : "_w12_nn", sizeof name - strlen(name) - 1);
     thr = 768;
   } else if (kb == 96 && gx > 256 && gx <= 512 && gx % 2 == 0) {
     strncat(name, "_c2", sizeof name - strlen(name) - 1);

@@ -1384,7 +1384,9 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
 #define ATTP_MAXSPLIT 8  // as llama_kernels.hip
 #define ATTP_ROWS 32
 #define ATTP_STRIDE 132
-template <int F, int CT, int S, int WK, int SRC>
+// NONORM: a variant for callers that never pass a norm (the residual
+// projections), without the sum-of-squares loads and the norm code
+template <int F, int CT, int S, int WK, int SRC, bool NONORM = false>
 __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, const uint8_t* __restrict__ B,
                                            const uint16_t* __restrict__ D, float* __restrict__ C, uint32_t N,
                                            uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,
@@ -1461,11 +1463,12 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     }
     // sums of squares for the RMSNorm (one block covers K; with a K split the
     // finishing block reads them at the end)
+    if (!NONORM)
 #pragma unroll
-    for (int q = 0; q < SPL; q++) {
-      const uint32_t t = lane + 64 * q;
-      ssv[q] = c1p[2 * T + (t < T ? t : T - 1)];
-    }
+      for (int q = 0; q < SPL; q++) {
+        const uint32_t t = lane + 64 * q;
+        ssv[q] = c1p[2 * T + (t < T ? t : T - 1)];
+      }
   } else {
     const uint32_t T1 = (uint32_t)pos_ptr[0] + 1;
     nsplit = (T1 + ATTP_ROWS - 1) / ATTP_ROWS;
@@ -1533,6 +1536,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
         }
       }
   }
+
   float ssum = 0.f;
   if (SRC == 0) {
 #pragma unroll
@@ -1543,7 +1547,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (ksplit == 1)
+    if (!NONORM && ksplit == 1)
 #pragma unroll
       for (int q = 0; q < SPL; q++) ssum += lane + 64 * q < T ? ssv[q] : 0.f;
   } else {
@@ -1732,6 +1736,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       for (uint32_t t = lane; t < T; t += 64) ssum += c1p[2 * T + t];
   }
   float rms = 1.0f;
+  if (NONORM) norm = 0;
   if (norm) {
     ssum = sum64_lanes(ssum);
     rms = 1.0f / __builtin_sqrtf(ssum / (float)K + eps);
@@ -1756,14 +1761,14 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   }
 }
 
-#define DEF_AGEMV(NAME, F, CT, S, WK)                                                                         \
+#define DEF_AGEMV(NAME, F, CT, S, WK, ...)                                                                    \
   extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                                \
       const uint8_t* __restrict__ act, const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,        \
       float* __restrict__ C, uint32_t N, uint32_t K, uint32_t norm, float eps, const float* __restrict__ R,   \
       uint32_t epi, uint8_t* __restrict__ act_out, const float* __restrict__ gamma_out, float* __restrict__ ws, \
       uint32_t* __restrict__ counters) {                                                                     \
-    agemv_body<F, CT, S, WK, 0>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, counters,     \
-                                nullptr, 0, blockIdx.x);                                                     \
+    agemv_body<F, CT, S, WK, 0, ##__VA_ARGS__>(act, B, D, C, N, K, norm, eps, R, epi, act_out, gamma_out, ws, \
+                                               counters, nullptr, 0, blockIdx.x);                            \
   }
 
 // o-projection on attention split partials (SRC 1); parts in place of the act
@@ -1791,6 +1796,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   DEF_AGEMV(smith_agemv_##TAG##_k288, F, 1, 9, 8)             \
   DEF_AGEMV(smith_agemv_##TAG##_k96_c2, F, 2, 3, 8)           \
   DEF_AGEMV(smith_agemv_##TAG##_k288_w12, F, 1, 6, 12)        \
+  DEF_AGEMV(smith_agemv_##TAG##_k288_w12_nn, F, 1, 6, 12, true) \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k64, F, 1, 4, 4)      \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k96, F, 1, 3, 8)      \
   DEF_AGEMV_ATT(smith_agemv_att_##TAG##_k128, F, 1, 4, 8)     \
