@@ -1420,9 +1420,9 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   const u32x4* frag = (const u32x4*)act;
   const float* c1p = (const float*)(act + (size_t)K * 4);
   constexpr int NT = 64 * WK;
-  constexpr int SPL = (4 * GMAX + 63) / 64;       // part sums of squares per lane
+  constexpr int SPL = (GMAX + 63) / 64;           // float4s of part sums of squares per lane
   float c1[S], c1b[S], sg[S], sgb[S];  // (C1, S) of the group, or of its halves (HALVES)
-  float ssv[SPL];
+  float4 ssv[SPL];
   // SRC 1: split partials of this block's parts (part = 8 elements)
   constexpr int PPT = SRC == 1 ? (4 * GMAX + NT - 1) / NT : 1;
   float4 oa[PPT][ATTP_MAXSPLIT], ob[PPT][ATTP_MAXSPLIT];
@@ -1465,9 +1465,9 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     // finishing block reads them at the end)
     if (!NONORM)
 #pragma unroll
-      for (int q = 0; q < SPL; q++) {
+      for (int q = 0; q < SPL; q++) {  // T % 4 == 0 (K % 32 == 0): 16-byte loads
         const uint32_t t = lane + 64 * q;
-        ssv[q] = c1p[2 * T + (t < T ? t : T - 1)];
+        ssv[q] = ((const float4*)(c1p + 2 * T))[t < T / 4 ? t : T / 4 - 1];
       }
   } else {
     const uint32_t T1 = (uint32_t)pos_ptr[0] + 1;
@@ -1549,7 +1549,8 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (!NONORM && ksplit == 1)
 #pragma unroll
-      for (int q = 0; q < SPL; q++) ssum += lane + 64 * q < T ? ssv[q] : 0.f;
+      for (int q = 0; q < SPL; q++)
+        ssum += lane + 64 * q < T / 4 ? (ssv[q].x + ssv[q].y) + (ssv[q].z + ssv[q].w) : 0.f;
   } else {
     // softmax weights of each head's splits: e^(m_z - M) / sum_z e^(m_z - M) l_z
     if (threadIdx.x < GMAX) {
