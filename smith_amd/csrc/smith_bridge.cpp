@@ -403,8 +403,11 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
     if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
     if (ensure_counters(c, gx)) return -1;
   }
+  // plain single-row matmuls (no norm, plain store, one block per column
+  // tile): the variants without the code of the other paths
+  const bool plain = M == 1 && ksplit == 1 && !ep.gamma && !ep.resid && ep.mode == 0;
   char name[64];
-  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s", tag, M, kb, c2 ? "_c2" : "");
+  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s%s", tag, M, kb, c2 ? "_c2" : "", plain ? "_pl" : "");
   const float* pa = a;
   const void* pB = B;
   const void* pD = D;

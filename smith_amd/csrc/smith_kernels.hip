@@ -569,7 +569,9 @@ __device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
   return __builtin_bit_cast(half8, u);
 }
 
-template <int FMT, int MR, int CT, int WK, int WN, int S>
+// PLAIN: the variant for plain matmuls (no RMSNorm prologue, plain store,
+// no K split across blocks), without the code of those paths
+template <int FMT, int MR, int CT, int WK, int WN, int S, bool PLAIN = false>
 __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
                                             const uint16_t* __restrict__ D, float* __restrict__ C,
                                             float* __restrict__ ws, uint32_t* __restrict__ counters,
@@ -598,7 +600,12 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   const uint32_t n0 = blockIdx.x * BC + wn * 16 * CT;
   const uint32_t gb = blockIdx.y * KB;
   const uint32_t gw = gb + wk * GPW;
-  const uint32_t ksplit = gridDim.y;
+  const uint32_t ksplit = PLAIN ? 1u : gridDim.y;
+  if (PLAIN) {
+    gamma = nullptr;
+    R = nullptr;
+    epi = EPI_STORE;
+  }
 
   // 1. activation loads (small, cache resident) and the RMSNorm gammas go out
   //    BEFORE the weights: vector loads complete in order, so the prep below
@@ -838,12 +845,13 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
 }
 
-#define DEF_QGEMV1(NAME, FMT, MR, CT, WK, WN, S)                                                        \
+#define DEF_QGEMV1(NAME, FMT, MR, CT, WK, WN, S, ...)                                                   \
   extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                       \
       const float* A, const uint8_t* B, const uint16_t* D, float* C, float* ws, uint32_t* counters,      \
       uint32_t M, uint32_t N, uint32_t K, uint32_t G, const float* gamma, float eps, const float* R,     \
       uint32_t epi) {                                                                                    \
-    qgemv1_body<FMT, MR, CT, WK, WN, S>(A, B, D, C, ws, counters, M, N, K, G, gamma, eps, R, epi);      \
+    qgemv1_body<FMT, MR, CT, WK, WN, S, ##__VA_ARGS__>(A, B, D, C, ws, counters, M, N, K, G, gamma, eps, R, \
+                                                       epi);                                             \
   }
 
 // ---------------------------------------------------------------------------
@@ -1050,6 +1058,12 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 // 9216 in one block); _c2: two 16-column tiles per wave (wide N).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_pl, FMT, 1, 1, 8, 1, 4, true)   \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64_pl, FMT, 1, 1, 4, 1, 4, true)    \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_pl, FMT, 1, 1, 8, 1, 3, true)    \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288_pl, FMT, 1, 1, 8, 1, 9, true)   \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2_pl, FMT, 1, 2, 8, 1, 3, true) \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2_pl, FMT, 1, 2, 8, 1, 4, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96, FMT, 1, 1, 8, 1, 3)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288, FMT, 1, 1, 8, 1, 9)            \
