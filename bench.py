@@ -37,8 +37,8 @@ ROTATE_BYTES = 400 << 20
 # this kernel (FETCH_SIZE, then WRITE_SIZE, per dispatch), FETCH_SIZE scaled
 # by the factor a plain device copy of known size gives; the profile named in
 # TRAFFIC_SOURCE holds the commands and the figures.
-TRAFFIC_CFG1 = 12805588
-TRAFFIC_CFG1_Q40 = 9670308
+TRAFFIC_CFG1 = 12767542
+TRAFFIC_CFG1_Q40 = 9631308
 TRAFFIC_SOURCE = "profiles/qgemv1_q4s_m1_cfg1_hbm_traffic.md"
 
 
@@ -504,7 +504,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1,
                      "traffic_source": TRAFFIC_SOURCE,
-                     "kernel": "smith_qgemv1_q4s_m1_k128", "step_us": round(ms * 1e3, 3)},
+                     "kernel": "smith_qgemv1_q4s_m1_k128_pl", "step_us": round(ms * 1e3, 3)},
         "headline_q4_0": {
             "workload": "config 1 on GGUF Q4_0 blocks (18 B/32 weights, tile-major nibble/scale planes as the "
                         "GGUF loader holds them), smith_linear_q4_0_t M=1, K=N=4096",
@@ -513,7 +513,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(v40, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(v40 / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1_Q40,
                          "traffic_source": TRAFFIC_SOURCE,
-                         "kernel": "smith_qgemv1_q40t_m1_k128", "step_us": round(ms40 * 1e3, 3)}},
+                         "kernel": "smith_qgemv1_q40t_m1_k128_pl", "step_us": round(ms40 * 1e3, 3)}},
         "cpu_baseline": cpu,
         "configs": configs,
     }
