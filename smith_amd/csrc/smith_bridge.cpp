@@ -382,6 +382,55 @@ int qgemv4_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   return launch(c, name, dim3(gx, ksplit), dim3(512), args);
 }
 
+// 2 < M <= 16 in one launch (smith_qgemv5_*): each wave converts the
+// activations of its own groups (K % 32 == 0).  Whole K (<= 128 groups) per
+// block when 16-column blocks give 128..320 workgroups; narrower outputs
+// split K into 32-group ranges; wider ones (or longer K) use 64-column
+// blocks over 32-group ranges.
+int qgemv5_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
+                 uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
+  const char* tag = fmt_tag(fmt);
+  const uint32_t bucket = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
+  if (ep.gamma) {
+    if (ensure(c, &c->normbuf, &c->normbuf_bytes, (size_t)M * K * sizeof(float))) return -1;
+    const float* pa = a;
+    const float* pg = ep.gamma;
+    void* py = c->normbuf;
+    uint32_t pr = M, pc = K;
+    float pe = ep.eps;
+    void* nargs[] = {&pa, &pg, &py, &pr, &pc, &pe};
+    if (launch(c, "smith_rmsnorm_rows", dim3(M), dim3(256), nargs)) return -1;
+    a = (const float*)c->normbuf;
+  }
+  const uint32_t nb16 = (N + 15) / 16;
+  const char* var;
+  uint32_t gx, ksplit, threads;
+  if (G <= 128 && nb16 >= 128 && nb16 <= 320) {
+    var = "w16", gx = nb16, ksplit = 1, threads = 1024;
+  } else if (nb16 < 128) {
+    var = "k32", gx = nb16, ksplit = (G + 31) / 32, threads = 512;
+  } else {
+    var = "k32c4", gx = (N + 63) / 64, ksplit = (G + 31) / 32, threads = 512;
+  }
+  if (ksplit > 1) {
+    if (ensure(c, (void**)&c->ws, &c->ws_bytes, (size_t)ksplit * M * N * sizeof(float))) return -1;
+    if (ensure_counters(c, gx)) return -1;
+  }
+  char name[64];
+  snprintf(name, sizeof name, "smith_qgemv5_%s_m%u_%s", tag, bucket, var);
+  const float* pa = a;
+  const void* pB = B;
+  const void* pD = D;
+  float* pC = out;
+  float* pws = c->ws;
+  uint32_t* pcnt = c->counters;
+  uint32_t pM = M, pN = N, pK = K, pG = G;
+  const float* pR = ep.resid;
+  uint32_t pepi = ep.mode;
+  void* args[] = {&pa, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pK, &pG, &pR, &pepi};
+  return launch(c, name, dim3(gx, ksplit), dim3(threads), args);
+}
+
 // M <= 2: the fused kernel (activation prep in LDS, whole records per lane,
 // K split across the waves of a block; a cross-block split only when one
 // block's 64/128 groups do not cover K).
@@ -516,15 +565,18 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
     float* om = out + (size_t)m0 * nout;
     Epi e = ep;
     if (e.resid) e.resid += (size_t)m0 * N;
-    // SMITH_QGEMV=3 / 4 forces one of the two M > 2 paths (comparisons)
+    // SMITH_QGEMV=3 / 4 / 5 forces one of the M > 2 paths (comparisons)
     static const int vq = [] {
       const char* e = getenv("SMITH_QGEMV");
       return e ? atoi(e) : 0;
     }();
-    const bool v3 = vq == 3 || (vq != 4 && mc > 8);
+    // the one-launch kernels read the activations in 32-element groups
+    const bool v3 = K % 32 != 0 || vq == 3 || (vq == 0 && mc > 16);
+    const bool v5 = !v3 && vq != 4 && mc <= 16;
     int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
                      : (v3 ? qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
-                           : qgemv4_chunk(c, fmt, am, B, D, om, mc, N, K, G, e));
+                           : (v5 ? qgemv5_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
+                                 : qgemv4_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)));
     if (rc) return -1;
   }
   return 0;

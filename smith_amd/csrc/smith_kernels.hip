@@ -1086,6 +1086,54 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   DEF_QGEMV3(smith_qgemv3_##TAG##_m16_c1, FMT, 1, false, 4, 1, 1, 8, 1)   \
   DEF_QGEMV3(smith_qgemv3_##TAG##_m32_c1, FMT, 2, false, 4, 1, 1, 8, 1)
 
+// The four records a lane group holds (groups g..g+3 of one column per
+// lane) transposed into MFMA K slices: bf[t] is the B operand of group g+t,
+// sv[t] / zv[t] its scale / zero for this lane's column.
+template <int FMT>
+__device__ __forceinline__ void rec_kslices(const Rec<FMT>& rr, half8 bf[4], uint32_t sv[4], uint32_t zv[4]) {
+  if (FMT == FMT_Q8) {
+    uint32_t d[9] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w, rr.q8b.x, rr.q8b.y, rr.q8b.z, rr.q8b.w, rr.q8c};
+    uint32_t e[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) e[q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], rr.sh);
+    xpose4(e[0], e[2], e[4], e[6]);
+    xpose4(e[1], e[3], e[5], e[7]);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      uint32_t x0 = e[2 * t] ^ 0x80808080u, x1 = e[2 * t + 1] ^ 0x80808080u;
+      u32x4 u;
+      u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);
+      u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);
+      u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);
+      u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);
+      bf[t] = __builtin_bit_cast(half8, u);
+    }
+  } else {
+    uint32_t x[4] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w};
+    xpose4(x[0], x[1], x[2], x[3]);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint32_t y = x[t] >> 8;
+      u32x4 u;
+      u.x = bfi(0x000F000Fu, x[t], 0x64006400u);
+      u.y = bfi(0x00F000F0u, x[t], 0x54005400u);
+      u.z = bfi(0x000F000Fu, y, 0x64006400u);
+      u.w = bfi(0x00F000F0u, y, 0x54005400u);
+      bf[t] = __builtin_bit_cast(half8, u);
+    }
+  }
+  // scale (and zero) of group t for this lane's column: register t after
+  // the same transpose of four copies
+  const float rs = rec_scale(rr);
+  sv[0] = sv[1] = sv[2] = sv[3] = __float_as_uint(rs);
+  xpose4(sv[0], sv[1], sv[2], sv[3]);
+  zv[0] = zv[1] = zv[2] = zv[3] = 0u;
+  if (FMT == FMT_Q4S) {
+    zv[0] = zv[1] = zv[2] = zv[3] = __float_as_uint(rr.z);
+    xpose4(zv[0], zv[1], zv[2], zv[3]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Batched decode GEMV for 2 < M <= 32 in ONE launch (activation prep fused).
 //
@@ -1135,8 +1183,11 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
   const uint32_t gw = gb + wk * GPW;
   const uint32_t ksplit = gridDim.y;
 
-  // 1. activation loads of this block's K range
+  // 1. activation loads of this block's K range (K % 32 == 0 on this
+  //    path): unconditional 16-byte loads from a clamped address, dead
+  //    items zeroed where they are converted
   float av[IPT][8];
+  bool alive[IPT];
 #pragma unroll
   for (int it = 0; it < IPT; it++) {
     const uint32_t item = threadIdx.x + it * NT;
@@ -1144,24 +1195,25 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
     const uint32_t r = rest % RPB, rb = (rest / RPB) % RB, gl = rest / (RPB * RB);
     const uint32_t m = rb * RPB + r;
     const uint32_t k0 = (gb + gl) * 32 + 8 * kq;
-    const bool live = item < (uint32_t)NITEM && m < M;
-    if (live && k0 + 8 <= K) {
-      const float4* ap = (const float4*)(A + (size_t)m * K + k0);
-      float4 x0 = ap[0], x1 = ap[1];
-      av[it][0] = x0.x; av[it][1] = x0.y; av[it][2] = x0.z; av[it][3] = x0.w;
-      av[it][4] = x1.x; av[it][5] = x1.y; av[it][6] = x1.z; av[it][7] = x1.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; e++) av[it][e] = (live && k0 + e < K) ? A[(size_t)m * K + k0 + e] : 0.f;
-    }
+    alive[it] = item < (uint32_t)NITEM && m < M && k0 < K;
+    const float4* ap = (const float4*)(A + (alive[it] ? (size_t)m * K + k0 : 0));
+    float4 x0 = ap[0], x1 = ap[1];
+    av[it][0] = x0.x; av[it][1] = x0.y; av[it][2] = x0.z; av[it][3] = x0.w;
+    av[it][4] = x1.x; av[it][5] = x1.y; av[it][6] = x1.z; av[it][7] = x1.w;
   }
 
-  // 2. weight records of this wave, all loads in flight
+  // 2. weight records of this wave, all loads in flight.  The never-taken
+  //    branches on either side end basic blocks, which the instruction
+  //    scheduler does not reorder across: it would otherwise interleave the
+  //    conversion below (and its wait for the activation loads) with, or
+  //    ahead of, the weight loads
+  if (epi == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
   Rec<FMT> wr[S][CT];
 #pragma unroll
   for (int st = 0; st < S; st++)
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+  if (epi == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
 
   // 3. activations -> f16 fragments and (C1, S) in LDS
   {
@@ -1181,7 +1233,7 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
       for (int e = 0; e < 8; e++) {
         const int el = FMT == FMT_Q8 ? perm_q8[e] : perm_q4[e];
         const float off = FMT == FMT_Q8 ? 1152.f : off_q4[e];
-        const float a = av[it][el];
+        const float a = alive[it] ? av[it][el] : 0.f;
         const _Float16 h = (_Float16)a;
         const float hf = (float)h;
         hv[e] = h;
@@ -1248,47 +1300,8 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
     for (int ct = 0; ct < CT; ct++) {
       const Rec<FMT>& rr = wr[st][ct];
       half8 bf[4];
-      if (FMT == FMT_Q8) {
-        uint32_t d[9] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w, rr.q8b.x, rr.q8b.y, rr.q8b.z, rr.q8b.w, rr.q8c};
-        uint32_t e[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) e[q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], rr.sh);
-        xpose4(e[0], e[2], e[4], e[6]);
-        xpose4(e[1], e[3], e[5], e[7]);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          uint32_t x0 = e[2 * t] ^ 0x80808080u, x1 = e[2 * t + 1] ^ 0x80808080u;
-          u32x4 u;
-          u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);
-          u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);
-          u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);
-          u.w = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u);
-          bf[t] = __builtin_bit_cast(half8, u);
-        }
-      } else {
-        uint32_t x[4] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w};
-        xpose4(x[0], x[1], x[2], x[3]);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const uint32_t y = x[t] >> 8;
-          u32x4 u;
-          u.x = bfi(0x000F000Fu, x[t], 0x64006400u);
-          u.y = bfi(0x00F000F0u, x[t], 0x54005400u);
-          u.z = bfi(0x000F000Fu, y, 0x64006400u);
-          u.w = bfi(0x00F000F0u, y, 0x54005400u);
-          bf[t] = __builtin_bit_cast(half8, u);
-        }
-      }
-      // scale (and zero) of group t for this lane's column: register t after
-      // the same transpose of four copies
-      const float rs = rec_scale(rr);
-      uint32_t sv[4] = {__float_as_uint(rs), __float_as_uint(rs), __float_as_uint(rs), __float_as_uint(rs)};
-      xpose4(sv[0], sv[1], sv[2], sv[3]);
-      uint32_t zv[4] = {0u, 0u, 0u, 0u};
-      if (FMT == FMT_Q4S) {
-        zv[0] = zv[1] = zv[2] = zv[3] = __float_as_uint(rr.z);
-        xpose4(zv[0], zv[1], zv[2], zv[3]);
-      }
+      uint32_t sv[4], zv[4];
+      rec_kslices<FMT>(rr, bf, sv, zv);
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const float s = __uint_as_float(sv[t]), z = __uint_as_float(zv[t]);
@@ -1375,6 +1388,248 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
   DEF_QGEMV4(smith_qgemv4_##TAG##_p16_k16, FMT, 1, false, 1, 2, 2, 4)    \
   DEF_QGEMV4(smith_qgemv4_##TAG##_p32_k32, FMT, 2, false, 1, 4, 2, 4)    \
   DEF_QGEMV4(smith_qgemv4_##TAG##_p32_k16, FMT, 2, false, 1, 2, 2, 4)
+
+// ---------------------------------------------------------------------------
+// Batched decode GEMV for 2 < M <= 16 in ONE launch, each wave preparing
+// only the activations its own MFMAs read.
+//
+// The MFMA scheme is qgemv4's (records transposed into K slices, all 16 MFMA
+// rows carrying activation rows: hi rows 0-7 + lo rows 8-15 for M <= 8, or
+// 16 plain f16 rows), but the activation prep is qgemv1's: a wave loads the
+// MR rows of its own 4*S groups first (before its weight records: loads
+// complete in order), converts them into its private slice of LDS and needs
+// only a wave barrier before its MFMAs.  A block of WK waves covers 4*S*WK
+// groups -- all of K when that fits, so the usual shapes need no cross-block
+// reduction.  Lanes whose MFMA row is past the bucket's MR rows feed zeros
+// from registers; LDS holds only the MR live rows:
+//   fragL[group][kslice][vrow], vrow = m (hi or plain) or MR + m (lo).
+// The per-(group, row) sums C1 = sum(a * slot offset) and S = sum(a) come
+// from one more MFMA per group against a constant B operand (column 0 ones,
+// column 1 the slot offsets), so the conversion is only the f16 rounding
+// (v_cvt_pk_f16_f32, and one fused multiply-add per element for the lo
+// half); lanes read them with a row broadcast (DPP row_newbcast).
+// Grid: x = column blocks of 16*CT, y = K splits of 4*S*WK groups.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float row_bcast0(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_bcast1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x151, 0xF, 0xF, false));
+}
+
+template <int FMT, int MR, bool HILO, int CT, int S, int WK>
+__device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                            const uint16_t* __restrict__ D, float* __restrict__ C,
+                                            float* __restrict__ ws, uint32_t* __restrict__ counters,
+                                            uint32_t M, uint32_t N, uint32_t K, uint32_t G,
+                                            const float* __restrict__ R, uint32_t epi) {
+  constexpr int GPW = 4 * S;               // groups per wave
+  constexpr int KB = GPW * WK;             // groups per block
+  constexpr int BC = 16 * CT;              // block columns
+  constexpr int NT = 64 * WK;              // threads
+  constexpr int RPB = HILO ? 8 : 16;       // activation rows per MFMA row block
+  static_assert(MR <= RPB, "one row block");
+  constexpr int VR = HILO ? 2 * MR : MR;   // live virtual rows
+  constexpr int NITEM = GPW * MR * 4;      // prep items of a wave (group, row, kslice), kslice fastest
+  constexpr int IPT = (NITEM + 63) / 64;
+  __shared__ u32x4 fragL[KB][4][VR];
+  __shared__ float red[WK][16][BC];
+  __shared__ int s_last;
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t c = lane & 15, j = lane >> 4;
+  const uint32_t n0 = blockIdx.x * BC;
+  const uint32_t gb = blockIdx.y * KB;
+  const uint32_t gw = gb + wk * GPW;
+  const uint32_t ksplit = gridDim.y;
+
+  // 1. this wave's activations (K % 32 == 0 on this path): unconditional
+  //    16-byte loads from a clamped address, dead items zeroed where they
+  //    are converted
+  float av[IPT][8];
+  bool alive[IPT];
+#pragma unroll
+  for (int it = 0; it < IPT; it++) {
+    const uint32_t item = lane + it * 64;
+    const uint32_t kq = item & 3, m = (item >> 2) % MR, gl = (item >> 2) / MR;
+    const uint32_t k0 = (gw + gl) * 32 + 8 * kq;
+    alive[it] = item < (uint32_t)NITEM && m < M && k0 < K;
+    const float4* ap = (const float4*)(A + (alive[it] ? (size_t)m * K + k0 : 0));
+    float4 x0 = ap[0], x1 = ap[1];
+    av[it][0] = x0.x; av[it][1] = x0.y; av[it][2] = x0.z; av[it][3] = x0.w;
+    av[it][4] = x1.x; av[it][5] = x1.y; av[it][6] = x1.z; av[it][7] = x1.w;
+  }
+
+  // 2. weight records of this wave, all loads in flight.  The never-taken
+  //    branches on either side end basic blocks, which the instruction
+  //    scheduler does not reorder across: it would otherwise interleave the
+  //    conversion below (and its wait for the activation loads) with, or
+  //    ahead of, the weight loads
+  if (epi == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
+  Rec<FMT> wr[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
+  if (epi == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
+
+  // 3. activations -> f16 fragments in this wave's LDS slice, in the slot
+  //    order of the record conversion; hi = f16(a), lo = f16((a - hi) * 2048)
+  {
+    const int perm_q4[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    const int perm_q8[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    typedef float float2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int it = 0; it < IPT; it++) {
+      const uint32_t item = lane + it * 64;
+      const uint32_t kq = item & 3, m = (item >> 2) % MR, gl = wk * GPW + (item >> 2) / MR;
+      u32x4 hp, lp;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int e0 = FMT == FMT_Q8 ? perm_q8[2 * q] : perm_q4[2 * q];
+        const int e1 = FMT == FMT_Q8 ? perm_q8[2 * q + 1] : perm_q4[2 * q + 1];
+        const float a0 = alive[it] ? av[it][e0] : 0.f, a1 = alive[it] ? av[it][e1] : 0.f;
+        const half2_t h = __builtin_convertvector((float2_t){a0, a1}, half2_t);
+        hp[q] = __builtin_bit_cast(uint32_t, h);
+        if (HILO) {
+          const float l0 = __builtin_fmaf((float)h[0], -2048.0f, a0 * 2048.0f);
+          const float l1 = __builtin_fmaf((float)h[1], -2048.0f, a1 * 2048.0f);
+          lp[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){l0, l1}, half2_t));
+        }
+      }
+      if (item < (uint32_t)NITEM) {
+        fragL[gl][kq][m] = hp;
+        if (HILO) fragL[gl][kq][MR + m] = lp;
+      }
+    }
+  }
+  // LDS operations of one wave complete in order
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // 4. MFMAs.  A operand: lane (r = lane%16, kslice j); MFMA row r is
+  //    activation row r (hi or plain) or r-8 (lo), live when below MR.
+  const uint32_t r = lane & 15;
+  const uint32_t rm = HILO ? (r & 7) : r;
+  const bool a_live = rm < (uint32_t)MR;
+  const uint32_t avr = HILO && r >= 8 ? MR + rm : rm;
+  // B operand of the sums MFMA: column 0 ones (-> S), column 1 the offset of
+  // every slot (+8 for Q4_0, whose -8 then folds into C1), other columns 0
+  half8 bx;
+  {
+    const _Float16 off_q4[8] = {1024, 1024, 64, 64, 1024, 1024, 64, 64};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const _Float16 off = FMT == FMT_Q8 ? (_Float16)1152 : (_Float16)(off_q4[e] + (is_q40(FMT) ? 8 : 0));
+      bx[e] = c == 0 ? (_Float16)1 : (c == 1 ? off : (_Float16)0);
+    }
+  }
+  f32x4 acc[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++) acc[ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < S; st++) {
+    const uint32_t gl0 = wk * GPW + 4 * st;
+    half8 af[4];
+    float c1v[4][4], sv4[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      u32x4 f = (u32x4){0u, 0u, 0u, 0u};
+      if (a_live) f = fragL[gl0 + t][j][avr];
+      af[t] = __builtin_bit_cast(half8, f);
+      const f32x4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bx, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        c1v[t][i] = row_bcast1(pe[i]);
+        if (FMT == FMT_Q4S) sv4[t][i] = row_bcast0(pe[i]);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      half8 bf[4];
+      uint32_t sv[4], zv[4];
+      rec_kslices<FMT>(wr[st][ct], bf, sv, zv);
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const float s = __uint_as_float(sv[t]), z = __uint_as_float(zv[t]);
+        const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf[t], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float tt = p[i] - c1v[t][i];
+          if (FMT == FMT_Q4S) tt = __builtin_fmaf(-z, sv4[t][i], tt);
+          acc[ct][i] = __builtin_fmaf(s, tt, acc[ct][i]);
+        }
+      }
+    }
+  }
+
+  // 5. the WK waves of the block in fixed order, then the epilogue or the
+  //    cross-block split
+#pragma unroll
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wk][j * 4 + i][ct * 16 + c] = acc[ct][i];
+  __syncthreads();
+  const uint32_t mrows = M < (uint32_t)MR ? M : MR;
+  const uint32_t nb = blockIdx.x * BC;
+  auto colsum = [&](uint32_t m, uint32_t cc) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WK; w++) {
+      if (HILO) v += red[w][m][cc] + red[w][m + 8][cc] * (1.0f / 2048.0f);
+      else v += red[w][m][cc];
+    }
+    return v;
+  };
+  if (ksplit == 1) {
+    if (epi == EPI_SWIGLU) {
+      for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
+        const uint32_t m = e / (BC / 2), cc = 2 * (e % (BC / 2)), n = nb + cc;
+        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(colsum(m, cc), colsum(m, cc + 1));
+      }
+    } else {
+      for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+        const uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+        if (n >= N) continue;
+        const float v = colsum(m, cc);
+        C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+      }
+    }
+    return;
+  }
+  for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
+    const uint32_t m = e / BC, cc = e % BC, n = nb + cc;
+    if (n >= N) continue;
+    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(colsum(m, cc)),
+                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
+}
+
+#define DEF_QGEMV5(NAME, FMT, MR, HILO, CT, S, WK)                                                      \
+  extern "C" __global__ __launch_bounds__(WK * 64) void NAME(                                            \
+      const float* A, const uint8_t* B, const uint16_t* D, float* C, float* ws, uint32_t* counters,      \
+      uint32_t M, uint32_t N, uint32_t K, uint32_t G, const float* R, uint32_t epi) {                    \
+    qgemv5_body<FMT, MR, HILO, CT, S, WK>(A, B, D, C, ws, counters, M, N, K, G, R, epi);                 \
+  }
+
+// Row buckets m4 / m8 (hi/lo) and m16 (plain f16).  w16: 16 waves x 2
+// steps = 128 groups (all of K <= 4096 in one block), 16 columns; k32: 8
+// waves x 1 step, 16 columns (narrow N: K splits fill the chip); k32c4: the
+// same K range with 4 column tiles per wave (64 columns: wide N, long K)
+#define DEF_QGEMV5_FMT(TAG, FMT)                                       \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m4_w16, FMT, 4, true, 1, 2, 16)      \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m8_w16, FMT, 8, true, 1, 2, 16)      \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m16_w16, FMT, 16, false, 1, 2, 16)   \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m4_k32, FMT, 4, true, 1, 1, 8)       \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m8_k32, FMT, 8, true, 1, 1, 8)       \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32, FMT, 16, false, 1, 1, 8)    \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m4_k32c4, FMT, 4, true, 4, 1, 8)     \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m8_k32c4, FMT, 8, true, 4, 1, 8)     \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32c4, FMT, 16, false, 4, 1, 8)
 
 
 // ---------------------------------------------------------------------------
@@ -1870,6 +2125,10 @@ DEF_QGEMV4_FMT(q4s, FMT_Q4S)
 DEF_QGEMV4_FMT(q8, FMT_Q8)
 DEF_QGEMV4_FMT(q40, FMT_Q40)
 DEF_QGEMV4_FMT(q40t, FMT_Q40T)
+DEF_QGEMV5_FMT(q4s, FMT_Q4S)
+DEF_QGEMV5_FMT(q8, FMT_Q8)
+DEF_QGEMV5_FMT(q40, FMT_Q40)
+DEF_QGEMV5_FMT(q40t, FMT_Q40T)
 DEF_QGEMV1_FMT(q4s, FMT_Q4S)
 DEF_QGEMV1_FMT(q8, FMT_Q8)
 DEF_QGEMV1_FMT(q40, FMT_Q40)
