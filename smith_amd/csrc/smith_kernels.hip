@@ -648,7 +648,11 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     }
   }
 
-  // 2. weights: every record of this wave, all loads in flight
+  // 2. weights: every record of this wave, all loads in flight.  The
+  //    never-taken branches end basic blocks, which the instruction scheduler
+  //    does not reorder across (it would otherwise wait for the activation
+  //    loads before issuing the last records)
+  if (K == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
   Rec<FMT> wr[S][CT];
   {
 #pragma unroll
@@ -656,6 +660,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 #pragma unroll
       for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
   }
+  if (K == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
 
   // 3. optional RMSNorm prologue (gguf_cache.js:121 fused into the projection
   //    that consumes it): every workgroup sums x^2 over its rows' full K
@@ -1207,13 +1212,13 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
   //    scheduler does not reorder across: it would otherwise interleave the
   //    conversion below (and its wait for the activation loads) with, or
   //    ahead of, the weight loads
-  if (epi == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
+  if (K == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
   Rec<FMT> wr[S][CT];
 #pragma unroll
   for (int st = 0; st < S; st++)
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
-  if (epi == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
+  if (K == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
 
   // 3. activations -> f16 fragments and (C1, S) in LDS
   {
@@ -1466,13 +1471,13 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   //    scheduler does not reorder across: it would otherwise interleave the
   //    conversion below (and its wait for the activation loads) with, or
   //    ahead of, the weight loads
-  if (epi == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
+  if (K == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
   Rec<FMT> wr[S][CT];
 #pragma unroll
   for (int st = 0; st < S; st++)
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) wr[st][ct] = load_rec<FMT>(B, D, N, G, gw + 4 * st + j, n0 + ct * 16 + c);
-  if (epi == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
+  if (K == 0xFFFFFFFEu) __builtin_amdgcn_s_sleep(1);
 
   // 3. activations -> f16 fragments in this wave's LDS slice, in the slot
   //    order of the record conversion; hi = f16(a), lo = f16((a - hi) * 2048)
