@@ -382,15 +382,15 @@ int qgemv4_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   return launch(c, name, dim3(gx, ksplit), dim3(512), args);
 }
 
-// 2 < M <= 16 in one launch (smith_qgemv5_*): each wave converts the
+// 2 < M <= 32 in one launch (smith_qgemv5_*): each wave converts the
 // activations of its own groups (K % 32 == 0).  Whole K (<= 128 groups) per
-// block when 16-column blocks give 128..320 workgroups; narrower outputs
-// split K into 32-group ranges; wider ones (or longer K) use 64-column
-// blocks over 32-group ranges.
+// block when 16-column blocks give 128..320 workgroups (M <= 16); narrower
+// outputs split K into 32-group ranges; wider ones (or longer K) use
+// 64-column blocks over 32-group ranges.
 int qgemv5_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
                  uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
   const char* tag = fmt_tag(fmt);
-  const uint32_t bucket = M <= 4 ? 4 : (M <= 8 ? 8 : 16);
+  const uint32_t bucket = M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
   if (ep.gamma) {
     if (ensure(c, &c->normbuf, &c->normbuf_bytes, (size_t)M * K * sizeof(float))) return -1;
     const float* pa = a;
@@ -405,7 +405,7 @@ int qgemv5_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   const uint32_t nb16 = (N + 15) / 16;
   const char* var;
   uint32_t gx, ksplit, threads;
-  if (G <= 128 && nb16 >= 128 && nb16 <= 320) {
+  if (bucket <= 16 && G <= 128 && nb16 >= 128 && nb16 <= 320) {
     var = "w16", gx = nb16, ksplit = 1, threads = 1024;
   } else if (nb16 < 128) {
     var = "k32", gx = nb16, ksplit = (G + 31) / 32, threads = 512;
@@ -570,9 +570,14 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
       const char* e = getenv("SMITH_QGEMV");
       return e ? atoi(e) : 0;
     }();
-    // the one-launch kernels read the activations in 32-element groups
-    const bool v3 = K % 32 != 0 || vq == 3 || (vq == 0 && mc > 16);
-    const bool v5 = !v3 && vq != 4 && mc <= 16;
+    // the one-launch kernels read the activations in 32-element groups.
+    // Past 16 rows every workgroup of the one-launch kernel converts 32
+    // activation rows of its K range: worth it while one round of
+    // workgroups covers the matrix, else the activations are prepared once
+    // (smith_qprep_*) for smith_qgemv3_*
+    const uint64_t rounds32 = (uint64_t)((N + 15) / 16 < 128 ? (N + 15) / 16 : (N + 63) / 64) * ((G + 31) / 32);
+    const bool v3 = K % 32 != 0 || vq == 3 || (vq == 0 && mc > 16 && rounds32 > 256);
+    const bool v5 = !v3 && vq != 4;
     int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
                      : (v3 ? qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
                            : (v5 ? qgemv5_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)

@@ -1433,12 +1433,14 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   constexpr int BC = 16 * CT;              // block columns
   constexpr int NT = 64 * WK;              // threads
   constexpr int RPB = HILO ? 8 : 16;       // activation rows per MFMA row block
-  static_assert(MR <= RPB, "one row block");
+  constexpr int RB = (MR + RPB - 1) / RPB; // MFMA row blocks
+  static_assert(!HILO || RB == 1, "hi/lo rows fit one row block");
+  static_assert(RB <= 2, "at most two row blocks");
   constexpr int VR = HILO ? 2 * MR : MR;   // live virtual rows
   constexpr int NITEM = GPW * MR * 4;      // prep items of a wave (group, row, kslice), kslice fastest
   constexpr int IPT = (NITEM + 63) / 64;
   __shared__ u32x4 fragL[KB][4][VR];
-  __shared__ float red[WK][16][BC];
+  __shared__ float red[WK][16 * RB][BC];
   __shared__ int s_last;
 
   const uint32_t lane = threadIdx.x & 63;
@@ -1515,12 +1517,18 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // 4. MFMAs.  A operand: lane (r = lane%16, kslice j); MFMA row r is
-  //    activation row r (hi or plain) or r-8 (lo), live when below MR.
+  // 4. MFMAs.  A operand: lane (r = lane%16, kslice j); MFMA row r of row
+  //    block rb is activation row 16 rb + r (plain) or r / r-8 (hi / lo),
+  //    live when below MR.
   const uint32_t r = lane & 15;
   const uint32_t rm = HILO ? (r & 7) : r;
-  const bool a_live = rm < (uint32_t)MR;
-  const uint32_t avr = HILO && r >= 8 ? MR + rm : rm;
+  bool a_live[RB];
+  uint32_t avr[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    a_live[rb] = 16 * rb + rm < (uint32_t)MR;
+    avr[rb] = HILO && r >= 8 ? MR + rm : 16 * rb + rm;
+  }
   // B operand of the sums MFMA: column 0 ones (-> S), column 1 the offset of
   // every slot (+8 for Q4_0, whose -8 then folds into C1), other columns 0
   half8 bx;
@@ -1532,26 +1540,30 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
       bx[e] = c == 0 ? (_Float16)1 : (c == 1 ? off : (_Float16)0);
     }
   }
-  f32x4 acc[CT];
+  f32x4 acc[CT][RB];
 #pragma unroll
-  for (int ct = 0; ct < CT; ct++) acc[ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < S; st++) {
     const uint32_t gl0 = wk * GPW + 4 * st;
-    half8 af[4];
-    float c1v[4][4], sv4[4][4];
+    half8 af[4][RB];
+    float c1v[4][RB][4], sv4[4][RB][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      u32x4 f = (u32x4){0u, 0u, 0u, 0u};
-      if (a_live) f = fragL[gl0 + t][j][avr];
-      af[t] = __builtin_bit_cast(half8, f);
-      const f32x4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bx, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    for (int t = 0; t < 4; t++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        c1v[t][i] = row_bcast1(pe[i]);
-        if (FMT == FMT_Q4S) sv4[t][i] = row_bcast0(pe[i]);
+      for (int rb = 0; rb < RB; rb++) {
+        u32x4 f = (u32x4){0u, 0u, 0u, 0u};
+        if (a_live[rb]) f = fragL[gl0 + t][j][avr[rb]];
+        af[t][rb] = __builtin_bit_cast(half8, f);
+        const f32x4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bx, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          c1v[t][rb][i] = row_bcast1(pe[i]);
+          if (FMT == FMT_Q4S) sv4[t][rb][i] = row_bcast0(pe[i]);
+        }
       }
-    }
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
       half8 bf[4];
@@ -1560,12 +1572,15 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const float s = __uint_as_float(sv[t]), z = __uint_as_float(zv[t]);
-        const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf[t], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          float tt = p[i] - c1v[t][i];
-          if (FMT == FMT_Q4S) tt = __builtin_fmaf(-z, sv4[t][i], tt);
-          acc[ct][i] = __builtin_fmaf(s, tt, acc[ct][i]);
+        for (int rb = 0; rb < RB; rb++) {
+          const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bf[t], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float tt = p[i] - c1v[t][rb][i];
+            if (FMT == FMT_Q4S) tt = __builtin_fmaf(-z, sv4[t][rb][i], tt);
+            acc[ct][rb][i] = __builtin_fmaf(s, tt, acc[ct][rb][i]);
+          }
         }
       }
     }
@@ -1576,7 +1591,9 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) red[wk][j * 4 + i][ct * 16 + c] = acc[ct][i];
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) red[wk][16 * rb + j * 4 + i][ct * 16 + c] = acc[ct][rb][i];
   __syncthreads();
   const uint32_t mrows = M < (uint32_t)MR ? M : MR;
   const uint32_t nb = blockIdx.x * BC;
@@ -1634,7 +1651,10 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32, FMT, 16, false, 1, 1, 8)    \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m4_k32c4, FMT, 4, true, 4, 1, 8)     \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m8_k32c4, FMT, 8, true, 4, 1, 8)     \
-  DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32c4, FMT, 16, false, 4, 1, 8)
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32c4, FMT, 16, false, 4, 1, 8)   \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32, FMT, 32, false, 1, 1, 8)      \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c4, FMT, 32, false, 4, 1, 8)    \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c2, FMT, 32, false, 2, 1, 8)
 
 
 // ---------------------------------------------------------------------------
