@@ -97,7 +97,7 @@ __device__ __forceinline__ WRec load_wrec(const uint8_t* __restrict__ B, const u
     const uint8_t* p = B + ((size_t)gc * N + nc) * 34;
     r.s = (float)__builtin_bit_cast(_Float16, *(const uint16_t*)p);
     const size_t a = (size_t)(p + 2);
-    const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
+    const uint32_t* w = (const uint32_t*)(p + 2 - (a & 3));  // stays a global pointer (no flat loads)
     r.sh = (uint32_t)(a & 3);
     r.q = (u32x4){w[0], w[1], w[2], w[3]};
     r.q8b = (u32x4){w[4], w[5], w[6], w[7]};

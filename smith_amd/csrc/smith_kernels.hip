@@ -523,7 +523,10 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
     // otherwise the scale is bytes 2-3 and the int8 are dwords 1..8.
     const uint8_t* p = B + rec * 34;
     const size_t a = (size_t)p;
-    const uint32_t* w = (const uint32_t*)(a & ~(size_t)3);
+    // aligned down by pointer arithmetic on p (an integer-to-pointer cast
+    // would lose the global address space: flat loads, which also count
+    // against every LDS wait)
+    const uint32_t* w = (const uint32_t*)(p - (a & 3));
     u32x4 w0 = *(const u32x4*)w, w1 = *(const u32x4*)(w + 4);
     uint32_t w8 = w[8];
     const bool odd = (a & 3) != 0;
