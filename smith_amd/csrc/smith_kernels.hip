@@ -1411,18 +1411,17 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
 // reduction.  Lanes whose MFMA row is past the bucket's MR rows feed zeros
 // from registers; LDS holds only the MR live rows:
 //   fragL[group][kslice][vrow], vrow = m (hi or plain) or MR + m (lo).
-// The per-(group, row) sums C1 = sum(a * slot offset) and S = sum(a) come
-// from one more MFMA per group against a constant B operand (column 0 ones,
-// column 1 the slot offsets), so the conversion is only the f16 rounding
+// The record operands have their exponent-bias offsets subtracted in f16
+// (exact), so the MFMA yields sum(a * q); the per-(group, row) sums S =
+// sum(a) for the zero term come from one more MFMA per group against a
+// constant B operand (column 0 ones), read by every lane with a row
+// broadcast (DPP row_newbcast).  The conversion is only the f16 rounding
 // (v_cvt_pk_f16_f32, and one fused multiply-add per element for the lo
-// half); lanes read them with a row broadcast (DPP row_newbcast).
+// half).
 // Grid: x = column blocks of 16*CT, y = K splits of 4*S*WK groups.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float row_bcast0(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float row_bcast1(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x151, 0xF, 0xF, false));
 }
 
 template <int FMT, int MR, bool HILO, int CT, int S, int WK>
@@ -1532,17 +1531,22 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
     a_live[rb] = 16 * rb + rm < (uint32_t)MR;
     avr[rb] = HILO && r >= 8 ? MR + rm : 16 * rb + rm;
   }
-  // B operand of the sums MFMA: column 0 ones (-> S), column 1 the offset of
-  // every slot (+8 for Q4_0, whose -8 then folds into C1), other columns 0
-  half8 bx;
+  // B operand of the sums MFMA: column 0 ones (-> S per group and row), the
+  // other columns zero.  The record operands get their exponent-bias offset
+  // (1024 / 64 per nibble slot, 1152 per int8) subtracted in f16 -- exact --
+  // so the MFMA sums a * q itself instead of a * (offset + q) with the
+  // offset part taken off afterwards in f32, which cancelled ~1e-5 of the
+  // result at K = 512
+  half8 bx, boff;
   {
     const _Float16 off_q4[8] = {1024, 1024, 64, 64, 1024, 1024, 64, 64};
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      const _Float16 off = FMT == FMT_Q8 ? (_Float16)1152 : (_Float16)(off_q4[e] + (is_q40(FMT) ? 8 : 0));
-      bx[e] = c == 0 ? (_Float16)1 : (c == 1 ? off : (_Float16)0);
+      bx[e] = c == 0 ? (_Float16)1 : (_Float16)0;
+      boff[e] = FMT == FMT_Q8 ? (_Float16)1152 : off_q4[e];
     }
   }
+  constexpr bool NEED_S = FMT != FMT_Q8;  // Q4S: - zero * S, Q4_0: - 8 * S
   f32x4 acc[CT][RB];
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
@@ -1552,7 +1556,7 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   for (int st = 0; st < S; st++) {
     const uint32_t gl0 = wk * GPW + 4 * st;
     half8 af[4][RB];
-    float c1v[4][RB][4], sv4[4][RB][4];
+    float sv4[4][RB][4];
 #pragma unroll
     for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -1560,11 +1564,10 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
         u32x4 f = (u32x4){0u, 0u, 0u, 0u};
         if (a_live[rb]) f = fragL[gl0 + t][j][avr[rb]];
         af[t][rb] = __builtin_bit_cast(half8, f);
-        const f32x4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bx, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        if (NEED_S) {
+          const f32x4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bx, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          c1v[t][rb][i] = row_bcast1(pe[i]);
-          if (FMT == FMT_Q4S) sv4[t][rb][i] = row_bcast0(pe[i]);
+          for (int i = 0; i < 4; i++) sv4[t][rb][i] = row_bcast0(pe[i]);
         }
       }
 #pragma unroll
@@ -1574,14 +1577,14 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
       rec_kslices<FMT>(wr[st][ct], bf, sv, zv);
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const float s = __uint_as_float(sv[t]), z = __uint_as_float(zv[t]);
+        const float s = __uint_as_float(sv[t]), z = is_q40(FMT) ? 8.0f : __uint_as_float(zv[t]);
+        const half8 bq = bf[t] - boff;  // the integers q themselves
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
-          const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bf[t], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bq, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            float tt = p[i] - c1v[t][rb][i];
-            if (FMT == FMT_Q4S) tt = __builtin_fmaf(-z, sv4[t][rb][i], tt);
+            const float tt = NEED_S ? __builtin_fmaf(-z, sv4[t][rb][i], p[i]) : p[i];
             acc[ct][rb][i] = __builtin_fmaf(s, tt, acc[ct][rb][i]);
           }
         }

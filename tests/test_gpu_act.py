@@ -125,6 +125,35 @@ def test_linear_t_all_epilogues(M):
         assert O.normwise_rel_err(got, y) <= tol, (M, epi)
 
 
+@pytest.mark.parametrize("N,K", [(2048, 1024), (6144, 512), (512, 1024), (2048, 8192)])
+def test_linear_t_batched_decode_variants(N, K):
+    """2 < M <= 32 on the one-launch kernel's variants (whole K in a
+    workgroup: 2048 x 1024; 32-group K ranges over 16-column tiles: 512 x
+    1024; over 64-column tiles: 6144 x 512 and the long K 2048 x 8192), every
+    row bucket (hi/lo M <= 8, plain f16 M <= 16, two row blocks M <= 32) and
+    every epilogue with the RMSNorm in front."""
+    _, nib, dsc, wd = _q4_0(N, K, 21)
+    ctx = device.ops_ctx()
+    for M in (3, 6, 8, 12, 16, 20, 32):
+        x = prng.randn((M, K), 22 + M)
+        g = 1 + prng.randn((K,), 23, std=0.1)
+        r = prng.randn((M, N), 24 + M)
+        xb, gb, rb, ob = _buf(x), _buf(g), _buf(r), device.alloc(M * N * 4)
+        xn = np.stack([_rms(x[m].astype(np.float64), g) for m in range(M)])
+        for epi in (0, 1, 2):
+            device.check(device.lib.smith_linear_q4_0_t(ctx, xb, nib, dsc, ob, M, N, K, gb, EPS, rb, epi))
+            y = xn @ wd.T
+            if epi == 1:
+                y = y + r
+            if epi == 2:
+                y = np.stack([_silu_mul(y[m]) for m in range(M)])
+            got = _get(ob, y.size).reshape(y.shape)
+            tol = (TOL_SWIGLU if epi == 2 else TOL) if M <= 8 else 1e-3
+            assert O.normwise_rel_err(got, y) <= tol, (M, N, K, epi)
+        for b in (xb, gb, rb, ob):
+            device.release_buffer(b)
+
+
 @pytest.mark.parametrize("N,K", [(64, 256), (5120, 3072), (96, 9600), (48, 32 * 7)])
 @pytest.mark.parametrize("norm", [0, 1])
 def test_act_gemv_matches_reference(N, K, norm):

@@ -223,6 +223,23 @@ def test_config3_batched_decode_sweep(N, K):
         assert e <= (TOL_HILO if M <= 8 else TOL), (M, N, K, e)
 
 
+@pytest.mark.parametrize("N,K", [(2048, 1024), (512, 1024), (6144, 512), (2048, 8192)])
+def test_batched_decode_variants_q4s_q8(N, K):
+    """2 < M <= 32 on matmulQ4 / matmulQ8 at shapes that select each variant
+    of the one-launch kernel (whole K per workgroup; 32-group K ranges over
+    16- or 64-column tiles), every row bucket including partial ones."""
+    w = prng.randn((K, N), 61, std=0.02)
+    q4, q8 = S.quantizeQ4(w), S.quantizeQ8(w)
+    dq4 = O.dequant_q4s(dev_bytes(q4), K, N).astype(np.float64)
+    dq8 = O.dequant_q8(dev_bytes(q8), K, N).astype(np.float64)
+    for M in (3, 6, 8, 12, 16, 20, 32):
+        a = prng.randn((M, K), 62 + M)
+        at = S.tensor(a)
+        for name, y, dq in (("q4", S.matmulQ4(at, q4).data, dq4), ("q8", S.matmulQ8(at, q8).data, dq8)):
+            e = err(y, a.astype(np.float64) @ dq)
+            assert e <= (TOL_HILO if M <= 8 else TOL), (name, M, N, K, e)
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 def test_config4_prefill_gemm(N, K):
     """Config 4 on the MFMA GEMM: M=512 checked in full, M=2048 on 512
