@@ -24,8 +24,13 @@
 // 32-K group and activation row the MFMA result P becomes the exact group
 // contribution scale * (P - C1 - zero * S), with C1 = sum(a * offset) and
 // S = sum(a), accumulated in f32; scale and zero never touch the f16 path.
+// (smith_qgemv5 subtracts the offsets from the f16 operands instead -- exact
+// -- and needs no C1.)
 //   smith_qgemv1_*  M <= 2: activation prep fused (LDS), one kernel per call
-//   smith_qgemv3_*  M >  2: activations prepared once by smith_qprep_*
+//   smith_qgemv5_*  2 < M <= 32: per-wave activation prep, one launch
+//   smith_qgemv3_*  2 < M <= 32: activations prepared once by smith_qprep_*
+//                   (M > 16 on the widest shapes, K % 32 != 0)
+//   smith_qgemv4_*  2 < M <= 32: workgroup-shared prep (comparison path)
 //   smith_agemv_*   M == 1 on an act (act_frag.h) its producer wrote
 // Q4_0 weights for the decode path use tile-major planes (FMT_Q40T): the 16
 // columns of a tile are contiguous over all of K, so a wave's records sit at
