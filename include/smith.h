@@ -282,6 +282,15 @@ uint64_t smith_lmhead_q6_k_bytes(uint32_t K, uint32_t N);
 int smith_repack_lmhead_q6_k(void* ctx, const void* blocks, void* planes, uint32_t K, uint32_t N);
 int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes, float* y,
                          uint32_t K, uint32_t N);
+/* smith_lmhead_q6_k_nb followed by the greedy step in the same launch, as
+ * smith_lmhead_q4_0_greedy does for the Q4_0 head (gguf_cache.js:174-184,
+ * generate.js:70-76, gguf_cache.js:335-341).  Calls on one context must not
+ * overlap (one device-side argmax slot). */
+int smith_lmhead_q6_k_greedy(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes,
+                             float* logits, uint32_t K, uint32_t N, const float* E, float* x_out, int32_t* tokens,
+                             int32_t* count, int32_t* pos, void* act_out, const float* gamma_out,
+                             const float* rope_cos, const float* rope_sin, uint32_t rope_len, uint32_t wq,
+                             uint32_t wk, float* rope_row);
 /* dequantizeTensor (src/gguf.js:343-394) on the device: numel elements of a
  * flat GGUF tensor of type F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q8_0, Q4_K or
  * Q6_K to f32, bit-identical to the reference's Float32Array. */

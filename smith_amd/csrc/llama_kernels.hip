@@ -878,6 +878,46 @@ __device__ __forceinline__ void embed_row(const float* __restrict__ E, int32_t t
 #define LMH_OCT 4
 #define LMH_ROWS (8 * 8 * LMH_OCT)
 
+// The greedy step after an LM head's column tile (one workgroup of 512
+// threads, thread tid holds logit v of column n): the tile's best key goes
+// into gt.amx with an atomic max, and the last tile to arrive runs the step
+// (token append, count / position advance, x = E[token] and its act).  The
+// max is a returning atomic, complete (performed at agent scope) before the
+// tile counter moves, so no fence is needed.  c0 / p0: count and position
+// read at the kernel's start (only this last tile writes them).
+__device__ __forceinline__ void greedy_finish(float v, uint32_t n, uint32_t N, const GreedyTail& gt, int32_t c0,
+                                              int32_t p0) {
+  __shared__ uint64_t kred[8];
+  __shared__ int g_last;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t key = wave_max64(n < N ? argmax_key(v, n) : 0ull);
+  if (lane == 0) kred[wave] = key;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t b = kred[0];
+    for (int w = 1; w < 8; w++) b = umax64(b, kred[w]);
+    kred[0] = __hip_atomic_fetch_max(gt.amx, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint32_t prev =
+        __hip_atomic_fetch_add((uint32_t*)(gt.amx + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    g_last = prev == gridDim.x - 1;
+    if (g_last) {
+      kred[1] = __hip_atomic_exchange(gt.amx, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store((uint32_t*)(gt.amx + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (!g_last) return;
+  const uint64_t best = kred[1];
+  const int32_t t = best == 0 ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)best);
+  if (tid == 0) {
+    gt.tokens[c0] = t;
+    gt.count[0] = c0 + 1;
+    gt.pos[0] = p0 + 1;
+  }
+  embed_row<512, 6>(gt.E, t, gt.dim, gt.x, gt.act_out, gt.gamma_out, tid);
+}
+
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) void smith_lmhead_q4_0_nb(
     const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ nib,
     const uint16_t* __restrict__ dsc, float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws,
@@ -885,7 +925,6 @@ extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(
   __shared__ float xs[LMH_ROWS];
   __shared__ float part[8][512];
   __shared__ float red[8];
-  __shared__ uint64_t kred[8];
   __shared__ int s_last;
   const uint32_t NB = N / 32;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -999,35 +1038,7 @@ extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(
   if (n < N) y[n] = v;
   if (!gt.E) return;
 
-  // 4. greedy: this tile's best key, then the last tile runs the step.  The
-  //    max is a returning atomic, complete (performed at agent scope) before
-  //    the tile counter moves, so no fence is needed.
-  const uint64_t key = wave_max64(n < N ? argmax_key(v, n) : 0ull);
-  if (lane == 0) kred[wave] = key;
-  __syncthreads();
-  if (tid == 0) {
-    uint64_t b = kred[0];
-    for (int w = 1; w < 8; w++) b = umax64(b, kred[w]);
-    kred[0] = __hip_atomic_fetch_max(gt.amx, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    const uint32_t prev =
-        __hip_atomic_fetch_add((uint32_t*)(gt.amx + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == gridDim.x - 1;
-    if (s_last) {
-      kred[1] = __hip_atomic_exchange(gt.amx, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store((uint32_t*)(gt.amx + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-  if (!s_last) return;
-  const uint64_t best = kred[1];
-  const int32_t t = best == 0 ? 0 : (int32_t)(0xFFFFFFFFu - (uint32_t)best);
-  if (tid == 0) {
-    gt.tokens[c0] = t;
-    gt.count[0] = c0 + 1;
-    gt.pos[0] = p0 + 1;
-  }
-  embed_row<512, 6>(gt.E, t, gt.dim, gt.x, gt.act_out, gt.gamma_out, tid);
+  greedy_finish(v, n, N, gt, c0, p0);
 }
 
 // f32 GEMV on a [K][N] row-major weight (an F32 output.weight read as
@@ -1253,7 +1264,8 @@ extern "C" __global__ void smith_repack_lmhead_q6_k(const uint8_t* __restrict__ 
 
 extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
     const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ planes,
-    float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws, uint32_t* __restrict__ counters) {
+    float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws, uint32_t* __restrict__ counters,
+    GreedyTail gt) {
   __shared__ float xs[8192];
   __shared__ float part[8][512];
   __shared__ float red[8];
@@ -1299,6 +1311,16 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
     wd[1] = *(const uint4*)(dp + (size_t)v256 * K + kc + 8);
   };
   if (k0 < k1) load_batch(k0);
+
+  // the greedy step's count and position (written only by this launch's last
+  // workgroup) and the next position's rope row (workgroup (0, 0))
+  int32_t c0 = 0, p0 = 0;
+  if (gt.E) {
+    c0 = gt.count[0];
+    p0 = gt.pos[0];
+    if (blockIdx.x == 0 && blockIdx.y == 0)
+      rope_row_write(gt.rrow, gt.cosT, gt.sinT, gt.rope_len, gt.wq, gt.wk, (uint32_t)p0 + 1, threadIdx.x, 512);
+  }
 
   float ss = 0.f;
 #pragma unroll
@@ -1357,26 +1379,24 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
   float v = 0.f;
 #pragma unroll
   for (int w = 0; w < 8; w++) v += part[w][o];
-  if (ksplit == 1) {
-    if (n < N) y[n] = v;
-    return;
+  if (ksplit > 1) {
+    if (n < N)
+      __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == ksplit - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (n < N) v = splitk_sum(ws + n, N, ksplit);
+    if (threadIdx.x == 0)
+      __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (n < N)
-    __hip_atomic_exchange((uint32_t*)ws + (size_t)blockIdx.y * N + n, __float_as_uint(v), __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t prev = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == ksplit - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  if (n < N) {
-    y[n] = splitk_sum(ws + n, N, ksplit);
-  }
-  if (threadIdx.x == 0)
-    __hip_atomic_exchange(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (n < N) y[n] = v;
+  if (gt.E) greedy_finish(v, n, N, gt, c0, p0);
 }
 
 // ---------------------------------------------------------------------------

@@ -1770,12 +1770,10 @@ int smith_repack_lmhead_q6_k(void* ctx, const void* blocks, void* planes, uint32
                 dim3(256), args);
 }
 
-int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes, float* y,
-                         uint32_t K, uint32_t N) {
-  Ctx* c = (Ctx*)ctx;
-  if (!c) return -1;
-  if (N % 256 || !N) return fail(c, "smith_lmhead_q6_k_nb: vocab %u is not a multiple of 256", N);
-  if (K > 8192 || K % 16 || !K) return fail(c, "smith_lmhead_q6_k_nb: dim %u unsupported (16..8192, %% 16)", K);
+static int lmhead_q6_k(Ctx* c, const char* who, const float* x, const float* norm_gamma, float eps,
+                       const void* planes, float* y, uint32_t K, uint32_t N, GreedyTail gt) {
+  if (N % 256 || !N) return fail(c, "%s: vocab %u is not a multiple of 256", who, N);
+  if (K > 8192 || K % 16 || !K) return fail(c, "%s: dim %u unsupported (16..8192, %% 16)", who, K);
   if (set_device(c)) return -1;
   uint32_t gx = (N / 32 + 15) / 16;
   uint32_t ksplit = std::max<uint32_t>(1, std::min<uint32_t>((K + 255) / 256, 64));
@@ -1785,8 +1783,34 @@ int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, flo
   }
   float* pws = c->ws;
   uint32_t* pcnt = c->counters;
-  void* args[] = {&x, &norm_gamma, &eps, &planes, &y, &K, &N, &pws, &pcnt};
+  void* args[] = {&x, &norm_gamma, &eps, &planes, &y, &K, &N, &pws, &pcnt, &gt};
   return launch(c, "smith_lmhead_q6_k_nb", dim3(gx, ksplit), dim3(512), args);
+}
+
+int smith_lmhead_q6_k_nb(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes, float* y,
+                         uint32_t K, uint32_t N) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  GreedyTail gt{};
+  return lmhead_q6_k(c, "smith_lmhead_q6_k_nb", x, norm_gamma, eps, planes, y, K, N, gt);
+}
+
+int smith_lmhead_q6_k_greedy(void* ctx, const float* x, const float* norm_gamma, float eps, const void* planes,
+                             float* logits, uint32_t K, uint32_t N, const float* E, float* x_out, int32_t* tokens,
+                             int32_t* count, int32_t* pos, void* act_out, const float* gamma_out,
+                             const float* rope_cos, const float* rope_sin, uint32_t rope_len, uint32_t wq,
+                             uint32_t wk, float* rope_row) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  if (!E || !x_out || !tokens || !count || !pos)
+    return fail(c, "smith_lmhead_q6_k_greedy: embedding, x, tokens, count and position are required");
+  if (act_out && K % 32) return fail(c, "smith_lmhead_q6_k_greedy: an act output needs dim %% 32 == 0 (dim %u)", K);
+  if (rope_row && (!rope_cos || !rope_sin || wq % 2 || wk % 2))
+    return fail(c, "smith_lmhead_q6_k_greedy: a rope row needs both tables and even row widths");
+  if (set_device(c) || ensure_amx(c)) return -1;
+  GreedyTail gt{E, x_out, tokens, count, pos, act_out, gamma_out, rope_cos, rope_sin, rope_row, c->amx,
+                rope_len, wq, wk, K};
+  return lmhead_q6_k(c, "smith_lmhead_q6_k_greedy", x, norm_gamma, eps, planes, logits, K, N, gt);
 }
 
 int smith_gemv_f32(void* ctx, const float* x, const float* norm_gamma, float eps, const float* W, float* y,

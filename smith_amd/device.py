@@ -90,6 +90,8 @@ SYMBOLS = {
     "smith_lmhead_q6_k_bytes": (_U64, [_U32, _U32]),
     "smith_repack_lmhead_q6_k": (_INT, [_P, _P, _P, _U32, _U32]),
     "smith_lmhead_q6_k_nb": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _U32, _U32]),
+    "smith_lmhead_q6_k_greedy": (_INT, [_P, _P, _P, ctypes.c_float, _P, _P, _U32, _U32, _P, _P, _P, _P, _P, _P, _P,
+                                        _P, _P, _U32, _U32, _U32, _P]),
     "smith_copy_2d": (_INT, [_P, _P, _U64, _P, _U64, _U64, _U64]),
     "smith_repack_gguf_tiles_into": (_INT, [_P, _U32, _P, _P, _U32, _U32, _U32, _U32, _U32]),
     "smith_linear_gguf_tiles": (_INT, [_P, _U32, _P, _P, _P, _U32, _U32, _U32, _P, ctypes.c_float, _P, _U32]),

@@ -32,7 +32,7 @@ from . import device
 # SMITH_DECODE_GRAPH=0 runs every decode step eagerly (kernel-level profilers
 # that cannot trace graph replays); results are identical.
 USE_GRAPH = os.environ.get("SMITH_DECODE_GRAPH", "1") != "0"
-# Q4_0 LM head and the greedy step in one launch (smith_lmhead_q4_0_greedy)
+# Q4_0 / Q6_K LM head and the greedy step in one launch (smith_lmhead_*_greedy)
 FUSED_GREEDY = os.environ.get("SMITH_FUSED_GREEDY", "1") != "0"
 
 PREFILL_CHUNK = 256
@@ -184,9 +184,10 @@ class _Engine:
                                                    cfg["numKVHeads"] * hd, rr), "argmax")
 
     def head_greedy(self, model):
-        """LM head on x, then the greedy step: one launch for a Q4_0 head."""
+        """LM head on x, then the greedy step: one launch for a Q4_0 or Q6_K
+        head."""
         head = model["lmHead"]
-        if not (FUSED_GREEDY and head["kind"] == "q4_0_nb"):
+        if not (FUSED_GREEDY and head["kind"] in ("q4_0_nb", "q6_k_nb")):
             self.lm_head(model, self.x.ptr)
             self.greedy_step(model)
             return
@@ -194,11 +195,15 @@ class _Engine:
         a0, g0 = self._act0(model)
         rope, hd = model["rope"], cfg["headDim"]
         rr = self.rope_row.ptr if self.use_parts else None
-        device.check(device.lib.smith_lmhead_q4_0_greedy(
-            device.ops_ctx(), self.x.ptr, model["lnFGamma"].ptr, model["normEps"], head["nib"].ptr, head["d"].ptr,
-            self.logits.ptr, cfg["dim"], cfg["vocabSize"], self.model_embedding, self.x.ptr, self.tokens.ptr,
-            self.count.ptr, self.pos.ptr, a0, g0, rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0],
-            cfg["numHeads"] * hd, cfg["numKVHeads"] * hd, rr), "lm head + greedy step")
+        tail = (self.logits.ptr, cfg["dim"], cfg["vocabSize"], self.model_embedding, self.x.ptr, self.tokens.ptr,
+                self.count.ptr, self.pos.ptr, a0, g0, rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0],
+                cfg["numHeads"] * hd, cfg["numKVHeads"] * hd, rr)
+        ctx, g, eps = device.ops_ctx(), model["lnFGamma"].ptr, model["normEps"]
+        if head["kind"] == "q4_0_nb":
+            rc = device.lib.smith_lmhead_q4_0_greedy(ctx, self.x.ptr, g, eps, head["nib"].ptr, head["d"].ptr, *tail)
+        else:
+            rc = device.lib.smith_lmhead_q6_k_greedy(ctx, self.x.ptr, g, eps, head["planes"].ptr, *tail)
+        device.check(rc, "lm head + greedy step")
 
     def embed(self, model, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.int32)

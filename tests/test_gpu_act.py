@@ -317,3 +317,56 @@ def test_lmhead_greedy_matches_two_step(K, N, case):
         assert rb["cnt"][0] == 4 + call and rb["pos"][0] == 21 + call
         Eh = device.download(E, K * 4, np.float32, offset=tok * K * 4)
         assert np.array_equal(rb["x"], Eh)
+
+
+@pytest.mark.parametrize("K,N,case", [(1024, 32000, "ties"), (3072, 4096, "plain"), (256, 512, "ties")])
+def test_lmhead_q6_k_greedy_matches_two_step(K, N, case):
+    """smith_lmhead_q6_k_greedy == smith_lmhead_q6_k_nb then
+    smith_argmax_embed, bit for bit (logits, token, count, position, x, its
+    act, rope row), on two calls in a row.  "ties": 256-column Q6_K blocks
+    copied into the same 512-column tile and into the last tile, with a
+    dominant column, so equal maxima sit in two tiles and the first wins."""
+    nh, hd = 4, 8
+    wq, wk = nh * hd, 2 * hd
+    w = prng.randn((K, N), 81, std=0.02)
+    xs = [prng.randn((K,), 82), prng.randn((K,), 83)]
+    if case == "ties":
+        w[:, 5] = 0.06 * np.sign(xs[0])
+        nb = N // 256
+        for b in (1, nb - 1):
+            w[:, 256 * b:256 * b + 256] = w[:, 0:256]
+    blocks = O.quantize_rows(O.GGML_Q6_K, w)
+    ctx = device.ops_ctx()
+    src = device.alloc(blocks.size)
+    device.upload(src, blocks)
+    planes = device.alloc(int(device.lib.smith_lmhead_q6_k_bytes(K, N)))
+    device.check(device.lib.smith_repack_lmhead_q6_k(ctx, src, planes, K, N))
+    E = device.alloc(N * K * 4)
+    device.check(device.lib.smith_randn(ctx, E, N * K, 84, 0, 1.0, 0.0))
+    g = _buf(1 + prng.randn((K,), 85, std=0.1))
+    gout = _buf(1 + prng.randn((K,), 86, std=0.1))
+    rope_len = 64 * hd // 2 * nh
+    cos, sin = _buf(prng.randn((rope_len,), 87)), _buf(prng.randn((rope_len,), 88))
+    xin = device.alloc(K * 4)
+    la, lb = device.alloc(N * 4), device.alloc(N * 4)
+    sa = _greedy_state(ctx, K, wq, wk, 3, 20)
+    sb = _greedy_state(ctx, K, wq, wk, 3, 20)
+    for call, xv in enumerate(xs):
+        device.upload(xin, xv.astype(np.float32))
+        device.check(device.lib.smith_lmhead_q6_k_nb(ctx, xin, g, EPS, planes, la, K, N))
+        device.check(device.lib.smith_argmax_embed(ctx, la, N, E, K, sa["x"], sa["toks"], sa["cnt"], sa["pos"],
+                                                   sa["act"], gout, cos, sin, rope_len, wq, wk, sa["rr"]))
+        device.check(device.lib.smith_lmhead_q6_k_greedy(ctx, xin, g, EPS, planes, lb, K, N, E, sb["x"], sb["toks"],
+                                                         sb["cnt"], sb["pos"], sb["act"], gout, cos, sin, rope_len,
+                                                         wq, wk, sb["rr"]))
+        ra, rb = _greedy_read(sa, K, wq, wk, N, la), _greedy_read(sb, K, wq, wk, N, lb)
+        for k in ra:
+            assert np.array_equal(ra[k].view(np.uint8), rb[k].view(np.uint8)), (call, k)
+        lg = ra["logits"].astype(np.float64)
+        tok = int(rb["toks"][3 + call])
+        assert tok == int(np.argmax(lg)), (call, tok)
+        if case == "ties" and call == 0:
+            assert tok == 5 and lg[5] == lg[256 + 5] == lg[N - 256 + 5]
+        assert rb["cnt"][0] == 4 + call and rb["pos"][0] == 21 + call
+    assert device.lib.smith_lmhead_q6_k_greedy(ctx, xin, g, EPS, planes, lb, K, N, None, sb["x"], sb["toks"],
+                                               sb["cnt"], sb["pos"], None, None, None, None, 0, 0, 0, None) != 0
