@@ -441,11 +441,14 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   // block, else 128 with a cross-block split
   uint32_t kb = G <= 64 ? 64 : (G <= 96 ? 96 : (G <= 128 ? 128 : (G <= 288 ? 288 : 128)));
   uint32_t threads = kb == 64 ? 256 : 512;
-  // wide outputs: two column tiles per wave halve the workgroup count
-  // (4-bit records from N = 8192: 11.3 -> 10.5 us at N = 14336; the Q8 records,
-  // 34 B and more registers per record, lose below 16384: 16.2 -> 17.3 us)
-  const uint32_t c2min = fmt == FQ8 ? 16384u : 8192u;
-  bool c2 = M == 1 && (kb == 96 || kb == 128) && N >= c2min;
+  // wide outputs (N >= 8192): two column tiles per wave halve the workgroup
+  // count, and both the c2 and the _pls variants read each step's A operands
+  // just before its MFMAs, which frees 48 VGPRs for more resident workgroups
+  // (N = 14336: Q4S 10.3 -> 9.5 us, Q8 14.6 -> 13.7 us; Q4_0 tiles keep one
+  // tile per wave: 8.7 -> 8.3 us)
+  const bool wide = M == 1 && (kb == 96 || kb == 128) && N >= 8192;
+  const bool q40 = fmt == FQ40 || fmt == FQ40T;
+  bool c2 = wide && !q40;
   uint32_t gx = c2 ? (N + 31) / 32 : (N + 15) / 16;
   uint32_t ksplit = (G + kb - 1) / kb;
   if (ksplit > 1) {
@@ -455,8 +458,10 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   // plain single-row matmuls (no norm, plain store, one block per column
   // tile): the variants without the code of the other paths
   const bool plain = M == 1 && ksplit == 1 && !ep.gamma && !ep.resid && ep.mode == 0;
+  const bool pls = plain && wide && q40 && kb == 128;
   char name[64];
-  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s%s", tag, M, kb, c2 ? "_c2" : "", plain ? "_pl" : "");
+  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s%s", tag, M, kb, c2 ? "_c2" : "",
+           pls ? "_pls" : (plain ? "_pl" : ""));
   const float* pa = a;
   const void* pB = B;
   const void* pD = D;

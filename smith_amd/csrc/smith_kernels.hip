@@ -579,7 +579,7 @@ __device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
 
 // PLAIN: the variant for plain matmuls (no RMSNorm prologue, plain store,
 // no K split across blocks), without the code of those paths
-template <int FMT, int MR, int CT, int WK, int WN, int S, bool PLAIN = false>
+template <int FMT, int MR, int CT, int WK, int WN, int S, bool PLAIN = false, bool PS = false>
 __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
                                             const uint16_t* __restrict__ D, float* __restrict__ C,
                                             float* __restrict__ ws, uint32_t* __restrict__ counters,
@@ -769,27 +769,37 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   for (int ct = 0; ct < CT; ct++)
 #pragma unroll
     for (int m = 0; m < MR; m++) acc[ct][m] = 0.f;
-  // A fragments of every step into registers first.  Only the 2*MR lanes
-  // per lane group whose MFMA row carries an activation row read LDS (the
-  // exec-masked reads move 1/8 of the bytes a read by all 64 lanes would);
-  // the rest hold zeros.
-  u32x4 afr[S][4];
-#pragma unroll
-  for (int st = 0; st < S; st++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) afr[st][i] = (u32x4){0u, 0u, 0u, 0u};
-  if (a_active) {
+  // A fragments of every step into registers first (PS: each step's right
+  // before its MFMAs -- 48 fewer VGPRs, more workgroups resident per CU on
+  // the wide matrices).  Only the 2*MR lanes per lane group whose MFMA row
+  // carries an activation row read LDS (the exec-masked reads move 1/8 of
+  // the bytes a read by all 64 lanes would); the rest hold zeros.
+  u32x4 afr[PS ? 1 : S][4];
+  if (!PS) {
 #pragma unroll
     for (int st = 0; st < S; st++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) afr[st][i] = fragL[wk * GPW + 4 * st + j][ru][i];
+      for (int i = 0; i < 4; i++) afr[PS ? 0 : st][i] = (u32x4){0u, 0u, 0u, 0u};
+    if (a_active) {
+#pragma unroll
+      for (int st = 0; st < S; st++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) afr[PS ? 0 : st][i] = fragL[wk * GPW + 4 * st + j][ru][i];
+    }
   }
 #pragma unroll
   for (int st = 0; st < S; st++) {
     const uint32_t gl = wk * GPW + 4 * st + j;
     half8 af[4];
+    if (PS) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) af[i] = __builtin_bit_cast(half8, afr[st][i]);
+      for (int i = 0; i < 4; i++) afr[0][i] = (u32x4){0u, 0u, 0u, 0u};
+      if (a_active)
+#pragma unroll
+        for (int i = 0; i < 4; i++) afr[0][i] = fragL[gl][ru][i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) af[i] = __builtin_bit_cast(half8, afr[PS ? 0 : st][i]);
     float2 cv[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) cv[m] = cL[gl][m];
@@ -1068,20 +1078,23 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 
 // Fused M <= 2 variants, named by the groups one block covers: k64 = 4 waves
 // x 4 steps, k96 / k128 / k288 = 8 waves x 3 / 4 / 9 steps (K = 3072, 4096,
-// 9216 in one block); _c2: two 16-column tiles per wave (wide N).
+// 9216 in one block); _c2: two 16-column tiles per wave (wide N); _pl:
+// plain matmuls; the _c2 and _pls variants read each step's A operands
+// right before its MFMAs (fewer VGPRs: more workgroups per CU, for wide N).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128, FMT, 1, 1, 8, 1, 4)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_pl, FMT, 1, 1, 8, 1, 4, true)   \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_pls, FMT, 1, 1, 8, 1, 4, true, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64_pl, FMT, 1, 1, 4, 1, 4, true)    \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_pl, FMT, 1, 1, 8, 1, 3, true)    \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288_pl, FMT, 1, 1, 8, 1, 9, true)   \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2_pl, FMT, 1, 2, 8, 1, 3, true) \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2_pl, FMT, 1, 2, 8, 1, 4, true) \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2_pl, FMT, 1, 2, 8, 1, 3, true, true) \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2_pl, FMT, 1, 2, 8, 1, 4, true, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96, FMT, 1, 1, 8, 1, 3)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288, FMT, 1, 1, 8, 1, 9)            \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2, FMT, 1, 2, 8, 1, 3)          \
-  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2, FMT, 1, 2, 8, 1, 4)         \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2, FMT, 1, 2, 8, 1, 3, false, true) \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2, FMT, 1, 2, 8, 1, 4, false, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k128, FMT, 2, 1, 8, 1, 4)            \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k96, FMT, 2, 1, 8, 1, 3)             \
