@@ -301,3 +301,22 @@ def test_gemm_big_tiles_epilogues(epi, K):
     device.check(device.lib.smith_linear_q8(ctx, xb.buffer, q8["buffer"], out.buffer, M, N, K, gb.buffer, eps,
                                             rb.buffer, epi))
     assert err(out.data, y) <= TOL_GEMM
+
+
+def test_decode_shapes_random_sweep():
+    """matmulQ4 / matmulQ8 against the float64 reference on seeded random
+    shapes: M in 1..40 (every GEMV path and row bucket), K with and without
+    K % 32 == 0, N not a multiple of 16."""
+    rng = np.random.default_rng(91)
+    for case in range(16):
+        M = int(rng.integers(1, 41))
+        K = int(rng.choice([32, 96, 100, 256, 320, 736, 1024, 1056]))
+        N = int(rng.integers(1, 700))
+        w = prng.randn((K, N), 900 + case, std=0.02)
+        a = prng.randn((M, K), 950 + case)
+        q4, q8 = S.quantizeQ4(w), S.quantizeQ8(w)
+        for name, q, dq in (("q4", q4, O.dequant_q4s(dev_bytes(q4), K, N)),
+                            ("q8", q8, O.dequant_q8(dev_bytes(q8), K, N))):
+            y = (S.matmulQ4 if name == "q4" else S.matmulQ8)(S.tensor(a), q).data
+            e = err(y, a.astype(np.float64) @ dq.astype(np.float64))
+            assert e <= tol_for(M, K), (case, name, M, K, N, e)
