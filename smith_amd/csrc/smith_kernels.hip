@@ -474,33 +474,46 @@ __device__ __forceinline__ void splitk_finish(float* __restrict__ ws, uint32_t* 
 // ---------------------------------------------------------------------------
 template <int FMT>
 struct Rec {
-  u32x4 q;        // 32 nibbles (Q4) or int8 0..15 (Q8)
-  u32x4 q8b;      // Q8: int8 16..31 (+ one spare dword for the 2-byte shift)
-  uint32_t q8c;
-  uint32_t sh;
-  float s, z;     // Q4S: scale, zero (0 for a record outside the weight)
-  uint32_t sb;    // Q4_0: the f16 scale's raw bits, converted where used
-  bool ok;        // Q4_0: record inside the weight
+  u32x4 q;        // Q4: 32 nibbles; Q8: raw dwords 0-3 of the record's 36 bytes
+  u32x4 q8b;      // Q8: raw dwords 4-7
+  uint32_t q8c;   // Q8: raw dword 8
+  float s, z;     // Q4S: scale, zero as loaded
+  uint32_t sb;    // Q4_0: the f16 scale's raw bits
+  bool odd;       // Q8: the record starts at byte 2 of its first dword
+  bool ok;        // record inside the weight (else its scale reads as 0)
 };
 
-// The record's scale.  Q4_0 scales stay raw 16-bit load results until the
-// post-step: converting them where they are loaded made every wave wait for
-// its scale loads before issuing the nibble loads behind them.
+// Every load result stays raw until its use: a select or conversion right
+// where a record is loaded makes the wave wait for that load before it can
+// issue the loads behind it (vector loads complete in order), and with
+// everything converted at the point of use the waits fall where the data
+// is needed.
 template <int FMT>
 __device__ __forceinline__ float rec_scale(const Rec<FMT>& r) {
   if (FMT == FMT_Q40 || FMT == FMT_Q40T)
     return r.ok ? (float)__builtin_bit_cast(_Float16, (uint16_t)r.sb) : 0.f;
-  return r.s;
+  if (FMT == FMT_Q8)
+    return r.ok ? (float)__builtin_bit_cast(_Float16, (uint16_t)(r.odd ? (r.q.x >> 16) : (r.q.x & 0xFFFFu))) : 0.f;
+  return r.ok ? r.s : 0.f;
+}
+
+// Q8: the 8 dwords of int8 0..31.  At an aligned record the f16 scale is
+// bytes 0-1 and the int8 start at byte 2; otherwise the scale is bytes 2-3
+// and the int8 are raw dwords 1..8.
+template <int FMT>
+__device__ __forceinline__ void q8_dwords(const Rec<FMT>& r, uint32_t e[8]) {
+  const uint32_t w[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
+#pragma unroll
+  for (int q = 0; q < 8; q++) e[q] = r.odd ? w[q + 1] : __builtin_amdgcn_alignbyte(w[q + 1], w[q], 2);
 }
 
 template <int FMT>
 __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
                                              uint32_t N, uint32_t G, uint32_t g, uint32_t n) {
   Rec<FMT> r;
-  bool ok = g < G && n < N;
+  r.ok = g < G && n < N;
   size_t rec = (size_t)(g < G ? g : G - 1) * N + (n < N ? n : N - 1);
   r.z = 0.f;
-  r.sh = 0;
   if (FMT == FMT_Q4S) {
     const uint8_t* p = B + rec * 24;
     r.q = *(const u32x4*)p;
@@ -513,36 +526,24 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
     rec = ((size_t)(nn >> 4) * G + gg) * 16 + (nn & 15);
     r.q = *(const u32x4*)(B + rec * 16);
     r.sb = D[rec];
-    r.ok = ok;
-    return r;
   } else if (FMT == FMT_Q40) {
     r.q = *(const u32x4*)(B + rec * 16);
     r.sb = D[rec];
-    r.ok = ok;
-    return r;
   } else {
     // the 36 bytes from the dword holding the record's first byte, in two
     // 128-bit loads + one dword (global loads need dword alignment only):
-    // 3 load instructions per record.  Records are 2-byte aligned: at an
-    // aligned record the f16 scale is bytes 0-1 and the int8 start at byte 2;
-    // otherwise the scale is bytes 2-3 and the int8 are dwords 1..8.
+    // 3 load instructions per record (records are 2-byte aligned)
     const uint8_t* p = B + rec * 34;
     const size_t a = (size_t)p;
     // aligned down by pointer arithmetic on p (an integer-to-pointer cast
     // would lose the global address space: flat loads, which also count
     // against every LDS wait)
     const uint32_t* w = (const uint32_t*)(p - (a & 3));
-    u32x4 w0 = *(const u32x4*)w, w1 = *(const u32x4*)(w + 4);
-    uint32_t w8 = w[8];
-    const bool odd = (a & 3) != 0;
-    r.s = (float)__builtin_bit_cast(_Float16, (uint16_t)(odd ? (w0.x >> 16) : (w0.x & 0xFFFFu)));
-    r.sh = odd ? 0u : 2u;
-    r.q = odd ? (u32x4){w0.y, w0.z, w0.w, w1.x} : w0;
-    r.q8b = odd ? (u32x4){w1.y, w1.z, w1.w, w8} : w1;
-    r.q8c = w8;
+    r.q = *(const u32x4*)w;
+    r.q8b = *(const u32x4*)(w + 4);
+    r.q8c = w[8];
+    r.odd = (a & 3) != 0;
   }
-  r.s = ok ? r.s : 0.f;
-  r.z = ok ? r.z : 0.f;
   return r;
 }
 
@@ -559,9 +560,9 @@ template <int FMT>
 __device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
   u32x4 u;
   if (FMT == FMT_Q8) {
-    uint32_t d[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
-    uint32_t x0 = __builtin_amdgcn_alignbyte(d[2 * i + 1], d[2 * i], r.sh) ^ 0x80808080u;
-    uint32_t x1 = __builtin_amdgcn_alignbyte(d[2 * i + 2], d[2 * i + 1], r.sh) ^ 0x80808080u;
+    const uint32_t w[9] = {r.q.x, r.q.y, r.q.z, r.q.w, r.q8b.x, r.q8b.y, r.q8b.z, r.q8b.w, r.q8c};
+    uint32_t x0 = (r.odd ? w[2 * i + 1] : __builtin_amdgcn_alignbyte(w[2 * i + 1], w[2 * i], 2)) ^ 0x80808080u;
+    uint32_t x1 = (r.odd ? w[2 * i + 2] : __builtin_amdgcn_alignbyte(w[2 * i + 2], w[2 * i + 1], 2)) ^ 0x80808080u;
     u.x = __builtin_amdgcn_perm(0x64646464u, x0, 0x04020400u);
     u.y = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u);
     u.z = __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u);
@@ -963,10 +964,8 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
       // K-slice operands of the four records after the transpose
       half8 bf[4];
       if (FMT == FMT_Q8) {
-        uint32_t d[9] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w, rr.q8b.x, rr.q8b.y, rr.q8b.z, rr.q8b.w, rr.q8c};
         uint32_t e[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) e[q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], rr.sh);
+        q8_dwords(rr, e);
         xpose4(e[0], e[2], e[4], e[6]);
         xpose4(e[1], e[3], e[5], e[7]);
 #pragma unroll
@@ -1118,10 +1117,8 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 template <int FMT>
 __device__ __forceinline__ void rec_kslices(const Rec<FMT>& rr, half8 bf[4], uint32_t sv[4], uint32_t zv[4]) {
   if (FMT == FMT_Q8) {
-    uint32_t d[9] = {rr.q.x, rr.q.y, rr.q.z, rr.q.w, rr.q8b.x, rr.q8b.y, rr.q8b.z, rr.q8b.w, rr.q8c};
     uint32_t e[8];
-#pragma unroll
-    for (int q = 0; q < 8; q++) e[q] = __builtin_amdgcn_alignbyte(d[q + 1], d[q], rr.sh);
+    q8_dwords(rr, e);
     xpose4(e[0], e[2], e[4], e[6]);
     xpose4(e[1], e[3], e[5], e[7]);
 #pragma unroll
