@@ -225,6 +225,46 @@ def bench_cfg4(D, S, prng, steps=5):
     return pre
 
 
+def bench_cfg4_library_f16():
+    """Reference point for config 4: the vendor library's plain f16 GEMM
+    (torch.matmul -> hipBLASLt) on already-dequantized f16 weights of the same
+    shapes -- no quantized weights, no dequantization, f16 activations.  Not
+    part of the product path; it shows the MFMA utilisation a tuned library
+    reaches on these shapes.  Run in a child process: torch's wheel carries
+    its own HIP runtime, which does not initialise in a process where this
+    build's library already holds the GPU."""
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cfg4-library-child"], capture_output=True,
+                       text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": r.stderr.strip().splitlines()[-1] if r.stderr.strip() else "rc %d" % r.returncode}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def _cfg4_library_child(steps=50):
+    import torch
+    out = {}
+    for (Nn, Kk) in [(14336, 4096), (4096, 14336)]:
+        for M in (512, 2048):
+            a = torch.randn(M, Kk, device="cuda", dtype=torch.float16)
+            ws = [torch.randn(Kk, Nn, device="cuda", dtype=torch.float16) for _ in range(4)]
+            for i in range(10):
+                torch.matmul(a, ws[i % 4])
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(steps):
+                torch.matmul(a, ws[i % 4])
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            fl = 2.0 * M * Nn * Kk
+            out["M%d_N%d_K%d" % (M, Nn, Kk)] = {"us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 1),
+                                                "mfma_util_vs_f16_dense": round(fl / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)}
+            del a, ws
+    return out
+
+
 def cpu_baseline(K, N, budget_s):
     """Oracle dequantize + f32 matmul (the reference's CPU semantics), 1 thread."""
     from oracle import oracle as O
@@ -415,7 +455,11 @@ def main():
     ap.add_argument("--cfg3-only", action="store_true", help="only the config-2/3 GEMV sweep")
     ap.add_argument("--gguf", default="/tmp/smith_config5.gguf", help="synthetic config-5 GGUF path (written if absent)")
     ap.add_argument("--mix", default="q4_0", choices=["q4_0", "q4_k_m"], help="config-5 weight types for --e2e-only")
+    ap.add_argument("--cfg4-library-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cfg4_library_child:
+        print(json.dumps(_cfg4_library_child()), flush=True)
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (--gpus %d requested); multi-GPU "
               "sharding is not implemented" % args.gpus, file=sys.stderr)
@@ -435,7 +479,8 @@ def main():
         print(json.dumps({"cfg5_e2e": bench_e2e(D, path, mix=args.mix)}), flush=True)
         return
     if args.cfg4_only:
-        print(json.dumps({"cfg4_q4s_prefill": bench_cfg4(D, S, prng)}), flush=True)
+        print(json.dumps({"cfg4_q4s_prefill": bench_cfg4(D, S, prng),
+                          "cfg4_library_f16_gemm_reference": bench_cfg4_library_f16()}), flush=True)
         return
     if args.cfg3_only:
         print(json.dumps(bench_sweeps(D, S, prng)), flush=True)
@@ -465,6 +510,8 @@ def main():
         pre = bench_cfg4(D, S, prng)
         configs["cfg4_q4s_prefill"] = pre
         log("cfg4:", json.dumps(pre))
+        configs["cfg4_library_f16_gemm_reference"] = bench_cfg4_library_f16()
+        log("cfg4 library f16 reference:", json.dumps(configs["cfg4_library_f16_gemm_reference"]))
 
     cpu = None
     if not args.quick:
