@@ -358,6 +358,27 @@ def calibrate(D, steps):
     return res
 
 
+def read_floor(D, S, prng, K, N, steps, warmup):
+    """The config-1 step's floor on this GPU, timed like the headline
+    (graph-replayed steps over the same rotated weight copies): an empty
+    launch, a plain 16-byte streaming read of the weight bytes, and the
+    GEMV's own record loads with its grid and nothing else
+    (smith_calib_read kinds 0 / 1 / 2)."""
+    W = q4s_weights(D, S, prng, K, N)
+    bufs = W.bufs
+    out = D.alloc(256)
+    ctx = D.ops_ctx()
+    nbytes = q4s_bytes(K, N)
+    res = {}
+    for kind, name in ((0, "empty_launch_us"), (1, "stream_read_us"), (2, "q4s_record_read_us")):
+        def step(i, kind=kind):
+            D.check(D.lib.smith_calib_read(ctx, kind, bufs[i % len(bufs)], nbytes, N, out), "calib")
+        ms, _ = time_steps(D, step, steps, warmup, rotation=len(bufs), graph=True)
+        res[name] = round(ms * 1e3, 3)
+    D.release_buffer(out)
+    return res
+
+
 def bench_sweeps(D, S, prng):
     """Config 2 and the config-3 sweeps (Q4S records and GGUF Q4_0 blocks),
     each point graph-replayed."""
@@ -501,6 +522,10 @@ def main():
     ms40_stream, kt40, b40 = bench_q40(D, S, prng, 1, K, N, args.steps, args.warmup)
     ms40, _, _ = bench_q40(D, S, prng, 1, K, N, args.steps, args.warmup, graph=True)
     v40 = b40 / (ms40 * 1e-3) / 1e9
+    floor = read_floor(D, S, prng, K, N, args.steps, args.warmup)
+    floor["kernel_over_record_read"] = round(ms * 1e3 / floor["q4s_record_read_us"], 3)
+    floor["frac_of_stream_read"] = round(floor["stream_read_us"] / (ms * 1e3), 3)
+    log("cfg1 floor:", json.dumps(floor))
     log("cfg1 q4s M=1: %.2f us/step graph = %.0f GB/s, %.2f us/step stream; q4_0: %.2f us graph = %.0f GB/s, %.2f stream"
         % (ms * 1e3, value, ms_stream * 1e3, ms40 * 1e3, v40, ms40_stream * 1e3))
 
@@ -552,6 +577,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_CFG1,
                      "traffic_source": TRAFFIC_SOURCE,
                      "kernel": "smith_qgemv1_q4s_m1_k128_pl", "step_us": round(ms * 1e3, 3)},
+        "read_floor": dict(floor, note="same weight bytes and rotation, graph-replayed: empty launch, plain "
+                                       "streaming read, the GEMV's record loads alone (its grid, no math)"),
         "headline_q4_0": {
             "workload": "config 1 on GGUF Q4_0 blocks (18 B/32 weights, tile-major nibble/scale planes as the "
                         "GGUF loader holds them), smith_linear_q4_0_t M=1, K=N=4096",
