@@ -1738,6 +1738,9 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
   constexpr int SPL = (GMAX + 63) / 64;           // float4s of part sums of squares per lane
   float c1[S], c1b[S], sg[S], sgb[S];  // (C1, S) of the group, or of its halves (HALVES)
   float4 ssv[SPL];
+  float4 ccv = make_float4(0.f, 0.f, 0.f, 0.f), svv = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int q = 0; q < SPL; q++) ssv[q] = make_float4(0.f, 0.f, 0.f, 0.f);
   // SRC 1: split partials of this block's parts (part = 8 elements)
   constexpr int PPT = SRC == 1 ? (4 * GMAX + NT - 1) / NT : 1;
   float4 oa[PPT][ATTP_MAXSPLIT], ob[PPT][ATTP_MAXSPLIT];
@@ -1755,30 +1758,23 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       const uint32_t e = 8 * gw + lane + 64 * q;
       fv[q] = frag[e < 8 * G ? e : 8 * G - 1];  // clamped: branch-free issue
     }
-#pragma unroll
-    for (int st = 0; st < S; st++) {
-      const uint32_t g = gw + 4 * st + j;
+    // the tile sums of the wave's GPW groups: lane l < GPW loads group gw + l
+    // once (a per-step load by every lane returned 64 copies of 4 groups'
+    // sums: the wave's load data, which the CU returns at 64 B per clock,
+    // was then mostly duplicates); handed to the lanes after the weight loads
+    // (buffer loads: the other lanes' offsets are out of range, so they
+    // fetch nothing and read zeros, with no branch around the load)
+    {
+      const uint32_t g = gw + lane;
       const uint32_t gc = g < G ? g : G - 1;
-      const float4 cc = *(const float4*)(c1p + 4 * gc);
-      if (HALVES) {
-        c1[st] = cc.x + cc.y;
-        c1b[st] = cc.z + cc.w;
-      } else {
-        c1[st] = (cc.x + cc.y) + (cc.z + cc.w);
-      }
-      if (NEED_S) {
-        const float4 sv = *(const float4*)(c1p + T + 4 * gc);
-        if (HALVES) {
-          sg[st] = sv.x + sv.y;
-          sgb[st] = sv.z + sv.w;
-        } else {
-          sg[st] = (sv.x + sv.y) + (sv.z + sv.w);
-        }
-      }
+      const uint32_t off = lane < (uint32_t)GPW ? 16 * gc : 0x80000000u;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)c1p, 0, (int)(8 * T), 0x00020000);
+      ccv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+      if (NEED_S) svv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4 * T, 0, 0));
     }
     // sums of squares for the RMSNorm (one block covers K; with a K split the
-    // finishing block reads them at the end)
-    if (!NONORM)
+    // finishing block reads them at the end): only wave 0 forms the norm
+    if (!NONORM && wk == 0)
 #pragma unroll
       for (int q = 0; q < SPL; q++) {  // T % 4 == 0 (K % 32 == 0): 16-byte loads
         const uint32_t t = lane + 64 * q;
@@ -1862,7 +1858,25 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (!NONORM && ksplit == 1)
+    {  // (C1, S) of group gw + 4 st + j from lane 4 st + j; the empty asm
+       // keeps the sums here (hoisted into the load's branch they made the
+       // wave wait for the load before issuing its weight loads)
+      asm volatile("" : "+v"(ccv.x), "+v"(ccv.y), "+v"(ccv.z), "+v"(ccv.w));
+      if (NEED_S) asm volatile("" : "+v"(svv.x), "+v"(svv.y), "+v"(svv.z), "+v"(svv.w));
+      const float c1v = HALVES ? ccv.x + ccv.y : (ccv.x + ccv.y) + (ccv.z + ccv.w), c1bv = ccv.z + ccv.w;
+      const float sgv = HALVES ? svv.x + svv.y : (svv.x + svv.y) + (svv.z + svv.w), sgbv = svv.z + svv.w;
+#pragma unroll
+      for (int st = 0; st < S; st++) {
+        const int src = 4 * st + (int)j;
+        c1[st] = __shfl(c1v, src);
+        if (HALVES) c1b[st] = __shfl(c1bv, src);
+        if (NEED_S) {
+          sg[st] = __shfl(sgv, src);
+          if (HALVES) sgb[st] = __shfl(sgbv, src);
+        }
+      }
+    }
+    if (!NONORM && ksplit == 1 && wk == 0)
 #pragma unroll
       for (int q = 0; q < SPL; q++)
         ssum += lane + 64 * q < T / 4 ? (ssv[q].x + ssv[q].y) + (ssv[q].z + ssv[q].w) : 0.f;
