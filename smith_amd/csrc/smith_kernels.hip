@@ -1787,25 +1787,32 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     const float* parts = (const float*)act;
     h0 = gb * 32 / hd;
     const uint32_t hend = ((gb + GMAX < G ? gb + GMAX : G) * 32 + hd - 1) / hd;
+    // buffer loads: threads past the block's heads / parts get out-of-range
+    // offsets and fetch nothing (clamped duplicates of the last head's
+    // partials made up 40 % of the block's load data: the workgroup's loads
+    // return at ~155 GB/s, which bounds this kernel)
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void*)parts, 0, 0x7FFFFFFF, 0x00020000);
     {  // (m, l) of head h0 + threadIdx.x
-      const uint32_t hh = h0 + threadIdx.x < hend ? h0 + threadIdx.x : hend - 1;
+      const bool live = h0 + threadIdx.x < hend;
 #pragma unroll
       for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
-        const float2 ml = *(const float2*)(parts + ((size_t)hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE);
+        const uint32_t off =
+            live ? (uint32_t)((((h0 + threadIdx.x) * ATTP_MAXSPLIT + zz) * ATTP_STRIDE) * 4) : 0x80000000u;
+        const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(prs, off, 0, 0));
         mlv[2 * zz] = ml.x;
         mlv[2 * zz + 1] = ml.y;
       }
     }
 #pragma unroll
     for (int q = 0; q < PPT; q++) {
-      uint32_t pi = 4 * gb + threadIdx.x + q * NT;
-      pi = pi < 4 * G ? pi : 4 * G - 1;
+      const uint32_t pl = threadIdx.x + q * NT, pi = 4 * gb + pl;
+      const bool live = pl < 4 * GMAX && pi < 4 * G;
       const uint32_t e0 = 8 * pi, hh = e0 / hd, d0 = e0 % hd;
 #pragma unroll
       for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
-        const float4* op = (const float4*)(parts + ((size_t)hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE + 4 + d0);
-        oa[q][zz] = op[0];
-        ob[q][zz] = op[1];
+        const uint32_t off = live ? (uint32_t)(((hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE + 4 + d0) * 4) : 0x80000000u;
+        oa[q][zz] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 0));
+        ob[q][zz] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, 0));
       }
     }
   }
