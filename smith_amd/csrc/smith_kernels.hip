@@ -1696,6 +1696,10 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
 // split, ATTP_STRIDE floats each); the block combines the splits of the
 // heads in its K range (softmax weights e^(m_z - M) / L) and converts them
 // to the MFMA operand in LDS itself.  No RMSNorm in front (norm == 0).
+// Word 3 of a raw buffer resource on gfx9 (CDNA): DATA_FORMAT = 32 bits, no
+// swizzle; with stride 0 a lane whose byte offset is >= num_records reads
+// zeros without a memory access
+#define RSRC_WORD3 0x00020000
 #define ATTP_MAXSPLIT 8  // as llama_kernels.hip
 #define ATTP_ROWS 32
 #define ATTP_STRIDE 132
@@ -1768,7 +1772,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       const uint32_t g = gw + lane;
       const uint32_t gc = g < G ? g : G - 1;
       const uint32_t off = lane < (uint32_t)GPW ? 16 * gc : 0x80000000u;
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)c1p, 0, (int)(8 * T), 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)c1p, 0, (int)(8 * T), RSRC_WORD3);
       ccv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
       if (NEED_S) svv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4 * T, 0, 0));
     }
@@ -1791,7 +1795,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     // offsets and fetch nothing (clamped duplicates of the last head's
     // partials made up 40 % of the block's load data: the workgroup's loads
     // return at ~155 GB/s, which bounds this kernel)
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void*)parts, 0, 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void*)parts, 0, 0x7FFFFFFF, RSRC_WORD3);
     {  // (m, l) of head h0 + threadIdx.x
       const bool live = h0 + threadIdx.x < hend;
 #pragma unroll
