@@ -459,8 +459,11 @@ int qgemv1_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   // tile): the variants without the code of the other paths
   const bool plain = M == 1 && ksplit == 1 && !ep.gamma && !ep.resid && ep.mode == 0;
   const bool pls = plain && wide && q40 && kb == 128;
+  // plain Q8 matmuls whose 16-column record runs are whole and 16-byte
+  // aligned read them as contiguous chunks (config 2: 13.7 -> ~12 us)
+  const bool q8c = plain && fmt == FQ8 && M == 1 && N % (c2 ? 32 : 16) == 0 && ((uintptr_t)B & 15) == 0;
   char name[64];
-  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s%s", tag, M, kb, c2 ? "_c2" : "",
+  snprintf(name, sizeof name, "smith_qgemv1_%s_m%u_k%u%s%s", q8c ? "q8c" : tag, M, kb, c2 ? "_c2" : "",
            pls ? "_pls" : (plain ? "_pl" : ""));
   const float* pa = a;
   const void* pB = B;

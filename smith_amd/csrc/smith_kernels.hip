@@ -580,7 +580,12 @@ __device__ __forceinline__ half8 rec_to_f16(const Rec<FMT>& r, int i) {
 
 // PLAIN: the variant for plain matmuls (no RMSNorm prologue, plain store,
 // no K split across blocks), without the code of those paths
-template <int FMT, int MR, int CT, int WK, int WN, int S, bool PLAIN = false, bool PS = false>
+// Q8C (Q8 records, N % 16 == 0, 16-byte aligned weight): each lane group
+// reads the 544 contiguous bytes of its 16 records as 16-byte chunks (the
+// records' own 36-byte windows at a 34-byte stride cost ~15 % of HBM rate
+// at config 2) and the wave regroups them into records through a private
+// LDS slice, which needs no barrier: one wave's LDS accesses run in order.
+template <int FMT, int MR, int CT, int WK, int WN, int S, bool PLAIN = false, bool PS = false, bool Q8C = false>
 __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
                                             const uint16_t* __restrict__ D, float* __restrict__ C,
                                             float* __restrict__ ws, uint32_t* __restrict__ counters,
@@ -601,6 +606,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   __shared__ float red[WK][MR][BC];
   __shared__ float nred[MR][WK * WN];
   __shared__ int s_last;
+  __shared__ u32x4 q8L[Q8C ? WK * WN : 1][Q8C ? 4 * CT : 1][Q8C ? 34 : 1];  // [wave][run][chunk]
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -663,7 +669,23 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   //    loads before issuing the last records)
   if (K == 0xFFFFFFFFu) __builtin_amdgcn_s_sleep(1);
   Rec<FMT> wr[S][CT];
-  {
+  u32x4 q8ch[Q8C ? S : 1][Q8C ? CT : 1][3];
+  if constexpr (Q8C) {
+    // run (group g, tile ct) = records n0 + 16 ct .. +15 of group g: 34
+    // chunks; lane c takes chunks c, c + 16 and (c < 2) c + 32 -- the other
+    // lanes repeat chunk c + 16 (the same line, so no extra HBM bytes)
+#pragma unroll
+    for (int st = 0; st < S; st++)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const uint32_t g = gw + 4 * st + j, gc = g < G ? g : G - 1;
+        const uint32_t nt = n0 + ct * 16 < N ? n0 + ct * 16 : N - 16;  // a tile past N: read in range, scale 0
+        const u32x4* run = (const u32x4*)(B + ((size_t)gc * N + nt) * 34);
+        q8ch[st][ct][0] = run[c];
+        q8ch[st][ct][1] = run[c + 16];
+        q8ch[st][ct][2] = run[c < 2 ? c + 32 : c + 16];
+      }
+  } else {
 #pragma unroll
     for (int st = 0; st < S; st++)
 #pragma unroll
@@ -804,6 +826,29 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     float2 cv[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) cv[m] = cL[gl][m];
+    if constexpr (Q8C) {
+      // this step's chunks into the wave's slice, then each lane's record:
+      // the 9 dwords from the one holding its first byte (byte 34 c of the run)
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        u32x4* sl = q8L[wave][j * CT + ct];
+        sl[c] = q8ch[st][ct][0];
+        sl[c + 16] = q8ch[st][ct][1];
+        if (c < 2) sl[c + 32] = q8ch[st][ct][2];
+      }
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++) {
+        const uint32_t* w = (const uint32_t*)q8L[wave][j * CT + ct] + ((34 * c) >> 2);
+        Rec<FMT>& rr = wr[st][ct];
+        rr.q = (u32x4){w[0], w[1], w[2], w[3]};
+        rr.q8b = (u32x4){w[4], w[5], w[6], w[7]};
+        rr.q8c = w[8];
+        rr.odd = (c & 1) != 0;
+        const uint32_t g = gw + 4 * st + j, n = n0 + ct * 16 + c;
+        rr.ok = g < G && n < N;
+        rr.z = 0.f;
+      }
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) {
       f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1098,6 +1143,16 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k64, FMT, 2, 1, 4, 1, 4)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k96, FMT, 2, 1, 8, 1, 3)             \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m2_k288, FMT, 2, 1, 8, 1, 9)
+
+// Q8 records read as contiguous 16-byte chunks (plain single-row matmuls
+// with N % 16 == 0 on a 16-byte aligned weight)
+#define DEF_QGEMV1_Q8C                                                                 \
+  DEF_QGEMV1(smith_qgemv1_q8c_m1_k128_pl, FMT_Q8, 1, 1, 8, 1, 4, true, false, true)    \
+  DEF_QGEMV1(smith_qgemv1_q8c_m1_k64_pl, FMT_Q8, 1, 1, 4, 1, 4, true, false, true)     \
+  DEF_QGEMV1(smith_qgemv1_q8c_m1_k96_pl, FMT_Q8, 1, 1, 8, 1, 3, true, false, true)     \
+  DEF_QGEMV1(smith_qgemv1_q8c_m1_k288_pl, FMT_Q8, 1, 1, 8, 1, 9, true, false, true)    \
+  DEF_QGEMV1(smith_qgemv1_q8c_m1_k96_c2_pl, FMT_Q8, 1, 2, 8, 1, 3, true, true, true)   \
+  DEF_QGEMV1(smith_qgemv1_q8c_m1_k128_c2_pl, FMT_Q8, 1, 2, 8, 1, 4, true, true, true)
 
 // M > 2 row buckets (RB, HILO, VPL): m4 / m8 hi/lo, m16 / m32 plain f16;
 // 2 column tiles x 1 step per wave, 8 waves split the block's 32 groups.
@@ -2202,6 +2257,7 @@ DEF_QGEMV5_FMT(q40, FMT_Q40)
 DEF_QGEMV5_FMT(q40t, FMT_Q40T)
 DEF_QGEMV1_FMT(q4s, FMT_Q4S)
 DEF_QGEMV1_FMT(q8, FMT_Q8)
+DEF_QGEMV1_Q8C
 DEF_QGEMV1_FMT(q40, FMT_Q40)
 DEF_QGEMV1_FMT(q40t, FMT_Q40T)
 #endif
