@@ -200,6 +200,34 @@ def test_config1_q4_gemv_4096():
     assert err(y, ref) <= TOL_HILO
 
 
+@pytest.mark.parametrize("N", [1024, 1040])
+def test_q8_chunked_and_window_reads_agree(N):
+    """Single-row Q8 matmuls read whole 16-column record runs as 16-byte
+    chunks when N % 16 == 0 (two-tile blocks: N % 32 == 0) and the weight is
+    16-byte aligned, else each record's own 36-byte window: the same records
+    through both readers give bit-identical outputs (the weight copied to a
+    2-byte offset forces the window reader), within the GEMV bar of the
+    oracle."""
+    K = 512
+    w = prng.randn((K, N), 73, std=0.02)
+    a = prng.randn((1, K), 74)
+    q = S.quantizeQ8(w)
+    raw = dev_bytes(q)
+    ctx = device.ops_ctx()
+    at = S.tensor(a)
+    out0 = S.create([1, N])
+    device.check(device.lib.smith_matmul_q8(ctx, at.buffer, q["buffer"], out0.buffer, 1, N, K, K // 32))
+    buf = device.alloc(raw.size + 64)
+    device.upload(buf, raw, 2)
+    out1 = S.create([1, N])
+    device.check(device.lib.smith_matmul_q8(ctx, at.buffer, buf + 2, out1.buffer, 1, N, K, K // 32))
+    y0, y1 = out0.data, out1.data
+    device.release_buffer(buf)
+    assert np.array_equal(y0, y1)
+    ref = a.astype(np.float64) @ O.dequant_q8(raw, K, N).astype(np.float64)
+    assert err(y0, ref) <= TOL_HILO
+
+
 def test_config2_q8_gemv_14336():
     K, N = 4096, 14336
     w = prng.randn((K, N), 1, std=0.02)
