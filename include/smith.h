@@ -72,6 +72,17 @@ int smith_copy_2d(void* ctx, void* dst, uint64_t dpitch, const void* src, uint64
                   uint64_t rows);
 int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes); /* enqueued fill kernel */
 
+/* Fusion hint, no counterpart in the reference (for host loops that run
+ * GEMM after GEMM on the same rows, such as a prompt's layers): the next
+ * matmul / linear call that takes the MFMA GEMM path and ends in a K-split
+ * reduce with a residual or SwiGLU epilogue also writes its output rows as
+ * the f16 A operand of the GEMM after it (RMS-normalised with gamma when
+ * gamma is non-null, with eps), and that GEMM skips its own activation prep
+ * if it reads exactly those rows with the same gamma and eps.  Any other op
+ * between the two must not modify those rows.  The hint is dropped by the
+ * next matmul / linear call whatever path it takes. */
+int smith_prep_next(void* ctx, const float* gamma, float eps);
+
 /* Platform calibration, no counterpart in the reference (for benchmarks that
  * put a kernel beside the floor of its bytes): kind 0 = an empty launch,
  * 1 = a plain 16-byte streaming read of `bytes` (contiguous 12 KB per

@@ -880,6 +880,136 @@ __device__ __forceinline__ void prep_a_row(const float* __restrict__ A, const fl
   }
 }
 
+// smith_gemm_reduce fused with the next GEMM's activation prep: the K-split
+// partials summed in split order with the epilogue (1: + residual, 2:
+// SwiGLU of the (gate, up) column pairs) -- the same sums and epilogue as
+// smith_gemm_reduce -- stored to C, and the output rows also written as the
+// next GEMM's A operand: f16, each 8-element chunk in the slot order
+// {0,4,1,5,2,6,3,7} (as smith_gemm_prep_a_perm).  Row length Kn = N (N / 2
+// for SwiGLU), Kn % 8 == 0.  reduce_chunk8: one 8-output chunk of row m.
+__device__ __forceinline__ void reduce_chunk8(const float* __restrict__ ws, uint32_t ks, size_t MN, uint32_t m,
+                                              uint32_t N, const float* __restrict__ R, uint32_t epi, uint32_t k0,
+                                              float v[8]) {
+  const float* wr = ws + (size_t)m * N;
+  if (epi == 2) {
+    float4 a[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) a[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t z0 = 0; z0 < ks; z0 += RED_BATCH) {
+      float4 t[RED_BATCH][4];
+#pragma unroll
+      for (uint32_t b = 0; b < RED_BATCH; b++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          t[b][q] = z0 + b < ks ? *(const float4*)(wr + (z0 + b) * MN + 2 * k0 + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (uint32_t b = 0; b < RED_BATCH; b++)
+        if (z0 + b < ks)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            a[q].x += t[b][q].x;
+            a[q].y += t[b][q].y;
+            a[q].z += t[b][q].z;
+            a[q].w += t[b][q].w;
+          }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      v[2 * q] = silu_mul_g(a[q].x, a[q].y);
+      v[2 * q + 1] = silu_mul_g(a[q].z, a[q].w);
+    }
+  } else {
+    float4 a[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    for (uint32_t z0 = 0; z0 < ks; z0 += RED_BATCH) {
+      float4 t[RED_BATCH][2];
+#pragma unroll
+      for (uint32_t b = 0; b < RED_BATCH; b++)
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+          t[b][q] = z0 + b < ks ? *(const float4*)(wr + (z0 + b) * MN + k0 + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (uint32_t b = 0; b < RED_BATCH; b++)
+        if (z0 + b < ks)
+#pragma unroll
+          for (int q = 0; q < 2; q++) {
+            a[q].x += t[b][q].x;
+            a[q].y += t[b][q].y;
+            a[q].z += t[b][q].z;
+            a[q].w += t[b][q].w;
+          }
+    }
+    if (epi == 1) {
+      const float4 r0 = *(const float4*)(R + (size_t)m * N + k0), r1 = *(const float4*)(R + (size_t)m * N + k0 + 4);
+      a[0] = make_float4(r0.x + a[0].x, r0.y + a[0].y, r0.z + a[0].z, r0.w + a[0].w);
+      a[1] = make_float4(r1.x + a[1].x, r1.y + a[1].y, r1.z + a[1].z, r1.w + a[1].w);
+    }
+    v[0] = a[0].x; v[1] = a[0].y; v[2] = a[0].z; v[3] = a[0].w;
+    v[4] = a[1].x; v[5] = a[1].y; v[6] = a[1].z; v[7] = a[1].w;
+  }
+}
+
+__device__ __forceinline__ uint4 perm_chunk8(const float v[8]) {
+  uint4 o;
+  o.x = pack_h2(v[0], v[4]);
+  o.y = pack_h2(v[1], v[5]);
+  o.z = pack_h2(v[2], v[6]);
+  o.w = pack_h2(v[3], v[7]);
+  return o;
+}
+
+// no norm: one 8-output chunk per thread over the whole M x Kn output
+extern "C" __global__ __launch_bounds__(256) void smith_gemm_reduce_perm(
+    const float* __restrict__ ws, uint32_t ks, float* __restrict__ C, uint32_t M, uint32_t N,
+    const float* __restrict__ R, uint32_t epi, _Float16* __restrict__ A16) {
+  const uint32_t Kn = epi == 2 ? N / 2 : N, cpr = Kn / 8;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)M * cpr) return;
+  const uint32_t m = (uint32_t)(idx / cpr), k0 = 8 * (uint32_t)(idx % cpr);
+  float v[8];
+  reduce_chunk8(ws, ks, (size_t)M * N, m, N, R, epi, k0, v);
+  float* cr = C + (size_t)m * Kn + k0;
+  *(float4*)cr = make_float4(v[0], v[1], v[2], v[3]);
+  *(float4*)(cr + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  *(uint4*)(A16 + (size_t)m * Kn + k0) = perm_chunk8(v);
+}
+
+// with the next GEMM's RMSNorm (gamma): one row per 1024-thread workgroup;
+// the row's sum of squares, rsqrt(mean + eps), x * rms * gamma as
+// smith_gemm_prep_a_perm.  A thread re-reads only the C elements it stored.
+extern "C" __global__ __launch_bounds__(1024) void smith_gemm_reduce_prep(
+    const float* __restrict__ ws, uint32_t ks, float* __restrict__ C, uint32_t M, uint32_t N,
+    const float* __restrict__ R, uint32_t epi, const float* __restrict__ gamma, float eps,
+    _Float16* __restrict__ A16) {
+  __shared__ float red[16];
+  const uint32_t m = blockIdx.x, tid = threadIdx.x;
+  const uint32_t Kn = epi == 2 ? N / 2 : N;
+  float* cr = C + (size_t)m * Kn;
+  _Float16* ar = A16 + (size_t)m * Kn;
+  float ss = 0.f;
+  for (uint32_t k0 = 8 * tid; k0 < Kn; k0 += 8 * 1024) {
+    float v[8];
+    reduce_chunk8(ws, ks, (size_t)M * N, m, N, R, epi, k0, v);
+    *(float4*)(cr + k0) = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)(cr + k0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[e], v[e], ss);
+  }
+  for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < 16; w++) tot += red[w];
+  const float rms = 1.0f / __builtin_sqrtf(tot / (float)Kn + eps);
+  for (uint32_t k0 = 8 * tid; k0 < Kn; k0 += 8 * 1024) {
+    const float4 c0 = *(const float4*)(cr + k0), c1 = *(const float4*)(cr + k0 + 4);
+    const float4 g0 = *(const float4*)(gamma + k0), g1 = *(const float4*)(gamma + k0 + 4);
+    const float v[8] = {c0.x * rms * g0.x, c0.y * rms * g0.y, c0.z * rms * g0.z, c0.w * rms * g0.w,
+                        c1.x * rms * g1.x, c1.y * rms * g1.y, c1.z * rms * g1.z, c1.w * rms * g1.w};
+    *(uint4*)(ar + k0) = perm_chunk8(v);
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256) void smith_gemm_prep_a(const float* __restrict__ A,
                                                                    const float* __restrict__ gamma, float eps,
                                                                    _Float16* __restrict__ A16, uint32_t K) {

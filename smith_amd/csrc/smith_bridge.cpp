@@ -60,6 +60,15 @@ struct Ctx {
   size_t normbuf_bytes = 0;
   void* a16 = nullptr;  // f16 activations of the GEMM path
   size_t a16_bytes = 0;
+  // smith_prep_next: the next GEMM's K-split reduce also writes its output
+  // as the A operand of the GEMM after it (a16_* say which one it fits)
+  bool next_pending = false;
+  const float* next_gamma = nullptr;
+  float next_eps = 0.f;
+  const float* a16_src = nullptr;
+  const float* a16_gamma = nullptr;
+  float a16_eps = 0.f;
+  uint32_t a16_M = 0, a16_K = 0;
   void* att_ws = nullptr;
   size_t att_ws_bytes = 0;
   uint32_t* att_cnt = nullptr;
@@ -486,6 +495,14 @@ const uint32_t GEMM_MIN_M = 64;
 
 int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M, uint32_t N,
          uint32_t K, const Epi& ep) {
+  // A operand already written by the previous GEMM's fused reduce (same
+  // source rows, norm and shape; only the permuted layout is written)
+  const bool want_next = c->next_pending;
+  c->next_pending = false;
+  const bool pre = c->a16_src && c->a16_src == a && c->a16_gamma == ep.gamma &&
+                   (!ep.gamma || c->a16_eps == ep.eps) && c->a16_M == M && c->a16_K == K &&
+                   c->a16_bytes >= (size_t)M * K * 2;
+  c->a16_src = nullptr;
   if (ensure(c, &c->a16, &c->a16_bytes, (size_t)M * K * 2)) return -1;
   // tile-plane formats (Q4_0 tiles, Q4_1, Q5_0, Q4_K, Q6_K) with K % 64 == 0:
   // the DMA-staged kernels (smith_gemm2_*),
@@ -507,7 +524,8 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
     // the DMA-staged kernels and the register-staged Q4S / Q4_0 ones take A
     // in the permuted slot order of their packed-f16 weight conversion
     const bool perm = g2 || fmt == FQ4S || fmt == FQ40 || fmt == FQ40T;
-    if (launch(c, perm ? "smith_gemm_prep_a_perm" : "smith_gemm_prep_a", dim3(M), dim3(256), args)) return -1;
+    if (!(pre && perm) && launch(c, perm ? "smith_gemm_prep_a_perm" : "smith_gemm_prep_a", dim3(M), dim3(256), args))
+      return -1;
   }
   // tile choice: the biggest tile that still gives about one tile per CU
   // (bigger tiles carry more MFMA work per K stage to cover load latency);
@@ -555,6 +573,30 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
   if (ks == 1) return 0;
   const float* cws = c->ws;
   uint32_t pks = ks;
+  const uint32_t Kn = ep.mode == 2 ? N / 2 : N;
+  if (want_next && (ep.mode == 1 || ep.mode == 2) && Kn % 8 == 0 && ((uintptr_t)out & 15) == 0 &&
+      (ep.mode != 1 || ((uintptr_t)ep.resid & 15) == 0) && (!c->next_gamma || ((uintptr_t)c->next_gamma & 15) == 0)) {
+    // the reduce also writes the rows as the next GEMM's (permuted) A operand
+    // into the f16 scratch, whose GEMM has finished reading it by then
+    if (ensure(c, &c->a16, &c->a16_bytes, (size_t)M * Kn * 2)) return -1;
+    const float* pg = c->next_gamma;
+    float pe = c->next_eps;
+    void* pa = c->a16;
+    if (pg) {
+      void* fargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi, &pg, &pe, &pa};
+      if (launch(c, "smith_gemm_reduce_prep", dim3(M), dim3(1024), fargs)) return -1;
+    } else {
+      void* fargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi, &pa};
+      const uint64_t chunks = (uint64_t)M * (Kn / 8);
+      if (launch(c, "smith_gemm_reduce_perm", dim3((unsigned)((chunks + 255) / 256)), dim3(256), fargs)) return -1;
+    }
+    c->a16_src = out;
+    c->a16_gamma = c->next_gamma;
+    c->a16_eps = c->next_eps;
+    c->a16_M = M;
+    c->a16_K = Kn;
+    return 0;
+  }
   void* rargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi};
   const size_t per = (size_t)M * N % 4 == 0 ? (size_t)M * N / 4 : (size_t)M * N / (ep.mode == 2 ? 2 : 1);
   return launch(c, "smith_gemm_reduce", dim3((unsigned)std::min<size_t>((per + 255) / 256, 65536)), dim3(256), rargs);
@@ -566,6 +608,8 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
   if (M == 0 || N == 0) return 0;
   if (ep.mode == 2 && N % 2) return fail(c, "smith: SwiGLU epilogue needs an even column count (got %u)", N);
   if (M >= GEMM_MIN_M && K % 32 == 0) return gemm(c, fmt, a, B, D, out, M, N, K, ep);
+  c->next_pending = false;  // the GEMV path has no K-split reduce to fuse
+  c->a16_src = nullptr;
   const uint32_t nout = ep.mode == 2 ? N / 2 : N;
   for (uint32_t m0 = 0; m0 < M; m0 += 32) {
     uint32_t mc = std::min<uint32_t>(32, M - m0);
@@ -881,6 +925,15 @@ int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes) {
   void* args[] = {&p, &n};
   uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 65536);
   return launch(c, "smith_zero_u32", dim3((unsigned)blocks), dim3(256), args);
+}
+
+int smith_prep_next(void* ctx, const float* gamma, float eps) {
+  Ctx* c = (Ctx*)ctx;
+  if (!c) return -1;
+  c->next_pending = true;
+  c->next_gamma = gamma;
+  c->next_eps = eps;
+  return 0;
 }
 
 int smith_calib_read(void* ctx, uint32_t kind, const void* buffer, uint64_t bytes, uint32_t N, void* out) {

@@ -34,6 +34,7 @@ from . import device
 USE_GRAPH = os.environ.get("SMITH_DECODE_GRAPH", "1") != "0"
 # Q4_0 / Q6_K LM head and the greedy step in one launch (smith_lmhead_*_greedy)
 FUSED_GREEDY = os.environ.get("SMITH_FUSED_GREEDY", "1") != "0"
+PREP_NEXT = os.environ.get("SMITH_PREP_NEXT", "1") != "0"
 
 PREFILL_CHUNK = 256
 
@@ -107,14 +108,24 @@ class _Engine:
         dim = cfg["dim"]
         x, x2, qkv, attn, h = self.x.ptr, self.x2.ptr, self.qkv.ptr, self.attn.ptr, self.h.ptr
         rope = model["rope"]
-        for blk, cache in zip(model["blocks"], caches):
+        blocks = model["blocks"]
+        # each residual / SwiGLU GEMM's K-split reduce also writes the next
+        # GEMM's f16 operand (with its RMSNorm), which then skips its prep
+        hint = PREP_NEXT and M > 1
+        for li, (blk, cache) in enumerate(zip(blocks, caches)):
             blk["qkv"](x, qkv, M, gamma=blk["ln1Gamma"].ptr, eps=eps)
             device.check(device.lib.smith_attention(
                 ctx, qkv, self.qkv_ld, self.pos.ptr, M, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
                 rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0], cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, None),
                 "attention")
+            if hint:
+                device.check(device.lib.smith_prep_next(ctx, blk["ln2Gamma"].ptr, eps), "prep hint")
             blk["outProj"](attn, x2, M, resid=x, epilogue=1)
+            if hint:
+                device.check(device.lib.smith_prep_next(ctx, None, 0.0), "prep hint")
             blk["gateUp"](x2, h, M, gamma=blk["ln2Gamma"].ptr, eps=eps, epilogue=2)
+            if hint and li + 1 < len(blocks):
+                device.check(device.lib.smith_prep_next(ctx, blocks[li + 1]["ln1Gamma"].ptr, eps), "prep hint")
             blk["ffnDown"](h, x, M, resid=x2, epilogue=1)
         del dim
 

@@ -236,6 +236,9 @@ def _greedy_state(ctx, dim, wq, wk, count, pos):
     st = {"x": device.alloc(dim * 4), "toks": device.alloc(64 * 4), "cnt": device.alloc(4), "pos": device.alloc(4),
           "act": device.alloc(_act_bytes(dim)), "rr": device.alloc((4 + wq + wk) * 4)}
     device.upload(st["toks"], np.full(64, -7, np.int32))
+    # the act is written only when dim % 32 == 0; zeroed so both states
+    # compare equal when it is not
+    device.upload(st["act"], np.zeros(_act_bytes(dim), np.uint8))
     device.upload(st["cnt"], np.array([count], np.int32))
     device.upload(st["pos"], np.array([pos], np.int32))
     row = np.zeros(4 + wq + wk, np.float32)
