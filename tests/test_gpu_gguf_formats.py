@@ -353,3 +353,57 @@ def test_lmhead_q6_k_matches_reference(K, N):
     device.check(device.lib.smith_lmhead_q6_k_nb(ctx, xb, None, 0.0, planes, yb, K, N))
     assert normwise_rel_err(_get(yb, N), x @ wd) <= 2e-6
     assert device.lib.smith_lmhead_q6_k_nb(ctx, xb, None, 0.0, planes, yb, 40, N) != 0  # K % 16
+
+
+@pytest.mark.parametrize("t", [O.GGML_Q4_0, O.GGML_Q4_K])
+def test_prep_next_chain_matches_unhinted(t):
+    """smith_prep_next on a prompt-shaped chain (M = 128 rows on the MFMA
+    GEMM, every GEMM split over K): o-proj (+ residual) -> gate|up (RMSNorm,
+    SwiGLU) -> down (+ residual) -> next q|k|v (RMSNorm), hinted so each
+    reduce also writes the next GEMM's operand.  Same outputs as the chain
+    without hints (the first GEMM bit for bit, the others within 2e-4
+    normwise: the fused RMSNorm sums its squares in another order, which can
+    move an f16 operand by one unit in the last place), one prep
+    launch instead of four, and the oracle's chain within the GEMM bar."""
+    M, D, F = 128, 1024, 1536
+    ctx = device.ops_ctx()
+    x0 = prng.randn((M, D), 81)
+    res = prng.randn((M, D), 82)
+    g2 = 1 + prng.randn((D,), 83, std=0.1)
+    g1 = 1 + prng.randn((D,), 84, std=0.1)
+    ws = [_weights(t, n, k, s) for (n, k, s) in ((D, D, 85), (2 * F, D, 86), (D, F, 87), (D, D, 88))]
+    pls = [_planes(t, b, n, k)[0] for (b, _), (n, k) in zip(ws, ((D, D), (2 * F, D), (D, F), (D, D)))]
+    xb, rb, g2b, g1b = _buf(x0), _buf(res), _buf(g2), _buf(g1)
+
+    def chain(hint):
+        y1, y2, y3, y4 = device.alloc(M * D * 4), device.alloc(M * F * 4), device.alloc(M * D * 4), device.alloc(M * D * 4)
+        steps = [(pls[0], xb, y1, D, D, None, 0.0, rb, 1, (g2b, EPS)),
+                 (pls[1], y1, y2, 2 * F, D, g2b, EPS, None, 2, (None, 0.0)),
+                 (pls[2], y2, y3, D, F, None, 0.0, y1, 1, (g1b, EPS)),
+                 (pls[3], y3, y4, D, D, g1b, EPS, None, 0, None)]
+        device.profile_kernels(True)
+        for pl, a, o, n, k, g, e, r, epi, nxt in steps:
+            if hint and nxt is not None:
+                device.check(device.lib.smith_prep_next(ctx, nxt[0], nxt[1]))
+            device.check(device.lib.smith_linear_gguf_tiles(ctx, t, a, pl, o, M, n, k, g, e, r, epi))
+        _, preps = device.profile_read("smith_gemm_prep_a")
+        device.profile_read("")
+        device.profile_kernels(False)
+        outs = [_get(b, M * d).reshape(M, d) for b, d in ((y1, D), (y2, F), (y3, D), (y4, D))]
+        for b in (y1, y2, y3, y4):
+            device.release_buffer(b)
+        return outs, preps
+
+    plain, p0 = chain(False)
+    fused, p1 = chain(True)
+    assert (p0, p1) == (4, 1)
+    assert np.array_equal(plain[0], fused[0])
+    for a, b in zip(plain[1:], fused[1:]):
+        assert normwise_rel_err(b, a) <= 2e-4
+    wd = [w for _, w in ws]
+    r1 = x0.astype(np.float64) @ wd[0].T.astype(np.float64) + res
+    h = np.stack([_silu_mul(row) for row in (np.stack([_rms(r, g2) for r in r1]) @ wd[1].T)])
+    r3 = h @ wd[2].T + r1
+    r4 = np.stack([_rms(r, g1) for r in r3]) @ wd[3].T
+    for got, ref in zip(fused, (r1, h, r3, r4)):
+        assert normwise_rel_err(got, ref) <= 1e-2
