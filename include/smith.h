@@ -75,12 +75,13 @@ int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes); /* enqueued fill k
 /* Fusion hint, no counterpart in the reference (for host loops that run
  * GEMM after GEMM on the same rows, such as a prompt's layers): the next
  * matmul / linear call that takes the MFMA GEMM path and ends in a K-split
- * reduce with a residual or SwiGLU epilogue also writes its output rows as
+ * reduce with a residual or SwiGLU epilogue -- or the next prompt-row
+ * smith_attention call, with gamma null -- also writes its output rows as
  * the f16 A operand of the GEMM after it (RMS-normalised with gamma when
  * gamma is non-null, with eps), and that GEMM skips its own activation prep
  * if it reads exactly those rows with the same gamma and eps.  Any other op
  * between the two must not modify those rows.  The hint is dropped by the
- * next matmul / linear call whatever path it takes. */
+ * next matmul / linear / attention call whatever path it takes. */
 int smith_prep_next(void* ctx, const float* gamma, float eps);
 
 /* Platform calibration, no counterpart in the reference (for benchmarks that

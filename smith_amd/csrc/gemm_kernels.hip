@@ -973,40 +973,53 @@ extern "C" __global__ __launch_bounds__(256) void smith_gemm_reduce_perm(
   *(uint4*)(A16 + (size_t)m * Kn + k0) = perm_chunk8(v);
 }
 
-// with the next GEMM's RMSNorm (gamma): one row per 1024-thread workgroup;
-// the row's sum of squares, rsqrt(mean + eps), x * rms * gamma as
-// smith_gemm_prep_a_perm.  A thread re-reads only the C elements it stored.
-extern "C" __global__ __launch_bounds__(1024) void smith_gemm_reduce_prep(
+// with the next GEMM's RMSNorm (gamma): one row per 512-thread workgroup,
+// at most 4 chunks of 8 per thread (Kn <= 16384), kept in registers across
+// the row's sum of squares (gamma loaded before it); rsqrt(mean + eps) and
+// x * rms * gamma as smith_gemm_prep_a_perm.
+#define RP_MAXC 4
+#define RP_NT 512
+extern "C" __global__ __launch_bounds__(RP_NT) void smith_gemm_reduce_prep(
     const float* __restrict__ ws, uint32_t ks, float* __restrict__ C, uint32_t M, uint32_t N,
     const float* __restrict__ R, uint32_t epi, const float* __restrict__ gamma, float eps,
     _Float16* __restrict__ A16) {
-  __shared__ float red[16];
+  __shared__ float red[RP_NT / 64];
   const uint32_t m = blockIdx.x, tid = threadIdx.x;
   const uint32_t Kn = epi == 2 ? N / 2 : N;
   float* cr = C + (size_t)m * Kn;
   _Float16* ar = A16 + (size_t)m * Kn;
+  float v[RP_MAXC][8], g[RP_MAXC][8];
   float ss = 0.f;
-  for (uint32_t k0 = 8 * tid; k0 < Kn; k0 += 8 * 1024) {
-    float v[8];
-    reduce_chunk8(ws, ks, (size_t)M * N, m, N, R, epi, k0, v);
-    *(float4*)(cr + k0) = make_float4(v[0], v[1], v[2], v[3]);
-    *(float4*)(cr + k0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
 #pragma unroll
-    for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[e], v[e], ss);
+  for (int q = 0; q < RP_MAXC; q++) {
+    const uint32_t k0 = 8 * (tid + RP_NT * q);
+    if (k0 < Kn) {
+      const float4 g0 = *(const float4*)(gamma + k0), g1 = *(const float4*)(gamma + k0 + 4);
+      g[q][0] = g0.x; g[q][1] = g0.y; g[q][2] = g0.z; g[q][3] = g0.w;
+      g[q][4] = g1.x; g[q][5] = g1.y; g[q][6] = g1.z; g[q][7] = g1.w;
+      reduce_chunk8(ws, ks, (size_t)M * N, m, N, R, epi, k0, v[q]);
+      *(float4*)(cr + k0) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+      *(float4*)(cr + k0 + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+#pragma unroll
+      for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[q][e], v[q][e], ss);
+    }
   }
   for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
-  for (int w = 0; w < 16; w++) tot += red[w];
+  for (int w = 0; w < RP_NT / 64; w++) tot += red[w];
   const float rms = 1.0f / __builtin_sqrtf(tot / (float)Kn + eps);
-  for (uint32_t k0 = 8 * tid; k0 < Kn; k0 += 8 * 1024) {
-    const float4 c0 = *(const float4*)(cr + k0), c1 = *(const float4*)(cr + k0 + 4);
-    const float4 g0 = *(const float4*)(gamma + k0), g1 = *(const float4*)(gamma + k0 + 4);
-    const float v[8] = {c0.x * rms * g0.x, c0.y * rms * g0.y, c0.z * rms * g0.z, c0.w * rms * g0.w,
-                        c1.x * rms * g1.x, c1.y * rms * g1.y, c1.z * rms * g1.z, c1.w * rms * g1.w};
-    *(uint4*)(ar + k0) = perm_chunk8(v);
+#pragma unroll
+  for (int q = 0; q < RP_MAXC; q++) {
+    const uint32_t k0 = 8 * (tid + RP_NT * q);
+    if (k0 < Kn) {
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) y[e] = v[q][e] * rms * g[q][e];
+      *(uint4*)(ar + k0) = perm_chunk8(y);
+    }
   }
 }
 

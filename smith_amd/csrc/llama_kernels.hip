@@ -409,7 +409,7 @@ __device__ __forceinline__ void attention_prefill_body(
     const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,
     uint32_t nKV, const float* __restrict__ cosT, const float* __restrict__ sinT, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out, uint32_t rope_len,
-    uint32_t* __restrict__ err) {
+    uint32_t* __restrict__ err, _Float16* __restrict__ a16) {
   constexpr uint32_t hd = 16 * NT;
   __shared__ __attribute__((aligned(16))) float Qs[FA_BQ * FA_QS];
   __shared__ __attribute__((aligned(16))) float KV[FA_BK * FA_QS + FA_BK * FA_VS];  // then the waves' O
@@ -529,6 +529,37 @@ __device__ __forceinline__ void attention_prefill_body(
     }
     out[(size_t)(s0 + r) * Wq + h * hd + e] = num / den;
   }
+  if (!a16) return;
+  // the rows also as the output projection's f16 GEMM operand: each
+  // 8-element chunk in the slot order {0,4,1,5,2,6,3,7} (the order of
+  // smith_gemm_prep_a_perm), the same values as above
+  for (uint32_t ci = tid; ci < nrow * (hd / 8); ci += 256) {
+    const uint32_t r = ci / (hd / 8), e0 = 8 * (ci % (hd / 8));
+    float M = MLs[0][0][r];
+#pragma unroll
+    for (int ww = 1; ww < 4; ww++) M = MLs[ww][0][r] > M ? MLs[ww][0][r] : M;
+    float f[4], den = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ww++) {
+      const float mw = MLs[ww][0][r];
+      f[ww] = mw == -__builtin_inff() ? 0.f : __expf(mw - M);
+      den = __builtin_fmaf(f[ww], MLs[ww][1][r], den);
+    }
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      float num = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 4; ww++) num = __builtin_fmaf(f[ww], Os[(ww * 16 + r) * hd + e0 + e], num);
+      v[e] = num / den;
+    }
+    uint32_t w4[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      w4[q] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[q]) |
+              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[q + 4]) << 16);
+    *(uint4*)(a16 + (size_t)(s0 + r) * Wq + h * hd + e0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  }
 }
 
 #define DEF_ATT_PREFILL(NT)                                                                                      \
@@ -536,8 +567,9 @@ __device__ __forceinline__ void attention_prefill_body(
       const float* __restrict__ qkv, uint32_t ld, const int32_t* __restrict__ pos_ptr, uint32_t S, uint32_t nH,   \
       uint32_t nKV, const float* __restrict__ cosT, const float* __restrict__ sinT,                              \
       const float* __restrict__ kcache, const float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ out, \
-      uint32_t rope_len, uint32_t* __restrict__ err) {                                                            \
-    attention_prefill_body<NT>(qkv, ld, pos_ptr, S, nH, nKV, cosT, sinT, kcache, vcache, maxSeq, out, rope_len, err); \
+      uint32_t rope_len, uint32_t* __restrict__ err, _Float16* __restrict__ a16) {                                \
+    attention_prefill_body<NT>(qkv, ld, pos_ptr, S, nH, nKV, cosT, sinT, kcache, vcache, maxSeq, out, rope_len, err, \
+                               a16);                                                                             \
   }
 // named by head_dim / 16
 DEF_ATT_PREFILL(1)

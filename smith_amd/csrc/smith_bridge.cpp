@@ -574,7 +574,8 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
   const float* cws = c->ws;
   uint32_t pks = ks;
   const uint32_t Kn = ep.mode == 2 ? N / 2 : N;
-  if (want_next && (ep.mode == 1 || ep.mode == 2) && Kn % 8 == 0 && ((uintptr_t)out & 15) == 0 &&
+  if (want_next && (ep.mode == 1 || ep.mode == 2) && Kn % 8 == 0 && (!c->next_gamma || Kn <= 16384) &&
+      ((uintptr_t)out & 15) == 0 &&
       (ep.mode != 1 || ((uintptr_t)ep.resid & 15) == 0) && (!c->next_gamma || ((uintptr_t)c->next_gamma & 15) == 0)) {
     // the reduce also writes the rows as the next GEMM's (permuted) A operand
     // into the f16 scratch, whose GEMM has finished reading it by then
@@ -584,7 +585,7 @@ int gemm(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* o
     void* pa = c->a16;
     if (pg) {
       void* fargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi, &pg, &pe, &pa};
-      if (launch(c, "smith_gemm_reduce_prep", dim3(M), dim3(1024), fargs)) return -1;
+      if (launch(c, "smith_gemm_reduce_prep", dim3(M), dim3(512), fargs)) return -1;
     } else {
       void* fargs[] = {&cws, &pks, &pC, &pM, &pN, &pR, &pepi, &pa};
       const uint64_t chunks = (uint64_t)M * (Kn / 8);
@@ -1552,6 +1553,9 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
   if (!rope_cos || !rope_sin || !kcache || !vcache || !qkv || !pos_ptr || !out)
     return fail(c, "smith_attention: null buffer");
   if (set_device(c)) return -1;
+  const bool want_next = c->next_pending && !c->next_gamma;  // smith_prep_next: no norm before the output projection
+  c->next_pending = false;
+  c->a16_src = nullptr;
   if (!S) return 0;
   uint32_t* perr = c->pos_err_dev;
   if (S > 1 && head_dim % 16 == 0) {
@@ -1562,11 +1566,26 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
     void* aargs[] = {&qkv, &ld, &pos_ptr, &Wq, &n_kv_heads, &head_dim, &rope_cos, &rope_sin, &kcache, &vcache,
                      &max_seq, &rope_len, &perr};
     if (launch(c, "smith_kv_append", dim3(S), dim3(256), aargs)) return -1;
+    // with the hint the rows are also written as the output projection's f16
+    // operand (its GEMM then skips the activation prep)
+    void* pa = nullptr;
+    if (want_next && S >= GEMM_MIN_M && Wq % 32 == 0) {
+      if (ensure(c, &c->a16, &c->a16_bytes, (size_t)S * Wq * 2)) return -1;
+      pa = c->a16;
+    }
     void* fargs[] = {&qkv, &ld, &pos_ptr, &S, &n_heads, &n_kv_heads, &rope_cos, &rope_sin,
-                     &kcache, &vcache, &max_seq, &out, &rope_len, &perr};
+                     &kcache, &vcache, &max_seq, &out, &rope_len, &perr, &pa};
     char name[48];
     snprintf(name, sizeof name, "smith_attention_prefill_hd%u", head_dim / 16);
-    return launch(c, name, dim3(n_heads, (S + 15) / 16), dim3(256), fargs);
+    if (launch(c, name, dim3(n_heads, (S + 15) / 16), dim3(256), fargs)) return -1;
+    if (pa) {
+      c->a16_src = out;
+      c->a16_gamma = nullptr;
+      c->a16_eps = 0.f;
+      c->a16_M = S;
+      c->a16_K = Wq;
+    }
+    return 0;
   }
   const uint32_t nsplit = 8;  // ATT_SPLIT in llama_kernels.hip
   size_t slots = (size_t)S * n_heads;

@@ -114,6 +114,8 @@ class _Engine:
         hint = PREP_NEXT and M > 1
         for li, (blk, cache) in enumerate(zip(blocks, caches)):
             blk["qkv"](x, qkv, M, gamma=blk["ln1Gamma"].ptr, eps=eps)
+            if hint:
+                device.check(device.lib.smith_prep_next(ctx, None, 0.0), "prep hint")
             device.check(device.lib.smith_attention(
                 ctx, qkv, self.qkv_ld, self.pos.ptr, M, cfg["numHeads"], cfg["numKVHeads"], cfg["headDim"],
                 rope["cos"].ptr, rope["sin"].ptr, rope["cos"].shape[0], cache["k"].ptr, cache["v"].ptr, cfg["maxSeqLen"], attn, None),
