@@ -427,6 +427,26 @@ __device__ __forceinline__ void attention_prefill_body(
   const uint32_t Wq = nH * hd;
   const float scale = 1.0f / __builtin_sqrtf((float)hd);
   const uint32_t nrow = S - s0 < FA_BQ ? S - s0 : FA_BQ;
+  const uint32_t Tend = p0 + s0 + nrow;  // keys of the block: 0 .. Tend-1
+  const float* kb = kcache + (size_t)kvh * maxSeq * hd;
+  const float* vb = vcache + (size_t)kvh * maxSeq * hd;
+  constexpr uint32_t c4n = hd / 4;
+  constexpr uint32_t TPT = (FA_BK * c4n + 255) / 256;  // float4s of a K (and V) tile per thread
+  // K / V tiles staged through registers: tile t+1's loads are in flight
+  // while tile t is multiplied (and tile 0's while the queries are roped)
+  float4 kr[TPT], vr[TPT];
+  auto load_tile = [&](uint32_t t0) {
+#pragma unroll
+    for (uint32_t q = 0; q < TPT; q++) {
+      const uint32_t i = tid + 256 * q, r = i / c4n, c4 = i % c4n, t = t0 + r;
+      kr[q] = vr[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < FA_BK * c4n && t < Tend) {
+        kr[q] = *(const float4*)(kb + (size_t)t * hd + 4 * c4);
+        vr[q] = *(const float4*)(vb + (size_t)t * hd + 4 * c4);
+      }
+    }
+  };
+  load_tile(0);
   // 1. roped queries (whole-row RoPE of the q part of each qkv row); rows past S zero
   for (uint32_t i = tid; i < FA_BQ * hd; i += 256) {
     const uint32_t r = i / hd, e = i % hd;
@@ -434,7 +454,6 @@ __device__ __forceinline__ void attention_prefill_body(
     if (r < nrow) v = rope_elem(qkv + (size_t)(s0 + r) * ld, Wq, h * hd + e, p0 + s0 + r, cosT, sinT);
     Qs[r * FA_QS + e] = v;
   }
-  const uint32_t Tend = p0 + s0 + nrow;  // keys of the block: 0 .. Tend-1
   f32x4_t o[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) o[t] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
@@ -444,32 +463,34 @@ __device__ __forceinline__ void attention_prefill_body(
     m[r] = -__builtin_inff();
     l[r] = 0.f;
   }
-  const float* kb = kcache + (size_t)kvh * maxSeq * hd;
-  const float* vb = vcache + (size_t)kvh * maxSeq * hd;
-  const uint32_t c4n = hd / 4;
   float* P = Ps[w];
   for (uint32_t t0 = 0; t0 < Tend; t0 += FA_BK) {
     __syncthreads();  // previous tile's K/V reads done (and, first time, Qs written)
-    // 2. K and V tile (rows past Tend zero: their P is 0 and V must be finite)
-    for (uint32_t i = tid; i < FA_BK * c4n; i += 256) {
-      const uint32_t r = i / c4n, c4 = i % c4n, t = t0 + r;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (t < Tend) {
-        kv = *(const float4*)(kb + (size_t)t * hd + 4 * c4);
-        vv = *(const float4*)(vb + (size_t)t * hd + 4 * c4);
+    // 2. K and V tile from the registers (rows past Tend zero: their P is 0
+    //    and V must be finite), then the next tile's loads
+#pragma unroll
+    for (uint32_t q = 0; q < TPT; q++) {
+      const uint32_t i = tid + 256 * q, r = i / c4n, c4 = i % c4n;
+      if (i < FA_BK * c4n) {
+        *(float4*)&Ks[r * FA_QS + 4 * c4] = kr[q];
+        *(float4*)&Vs[r * FA_VS + 4 * c4] = vr[q];
       }
-      *(float4*)&Ks[r * FA_QS + 4 * c4] = kv;
-      *(float4*)&Vs[r * FA_VS + 4 * c4] = vv;
     }
+    if (t0 + FA_BK < Tend) load_tile(t0 + FA_BK);
     __syncthreads();
     const uint32_t k0 = t0 + 16 * w;  // this wave's 16 keys
     if (k0 >= Tend) continue;         // after every row of the block
-    // 3. scores of the 16 rows against the wave's 16 keys
-    f32x4_t sc = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    // 3. scores of the 16 rows against the wave's 16 keys (two independent
+    //    accumulator chains over alternate k steps, summed at the end)
+    f32x4_t sc = (f32x4_t){0.f, 0.f, 0.f, 0.f}, sc2 = sc;
 #pragma unroll 8
-    for (uint32_t kk = 0; kk < hd; kk += 4)
+    for (uint32_t kk = 0; kk < hd; kk += 8) {
       sc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[c * FA_QS + kk + j], Ks[(16 * w + c) * FA_QS + kk + j], sc, 0, 0,
                                                 0);
+      sc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[c * FA_QS + kk + 4 + j], Ks[(16 * w + c) * FA_QS + kk + 4 + j],
+                                                 sc2, 0, 0, 0);
+    }
+    sc += sc2;
     // 4. online softmax per row (row 4j + r: the 16 lanes of group j)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
