@@ -393,9 +393,11 @@ int qgemv4_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
 
 // 2 < M <= 32 in one launch (smith_qgemv5_*): each wave converts the
 // activations of its own groups (K % 32 == 0).  Whole K (<= 128 groups) per
-// block when 16-column blocks give 128..320 workgroups (M <= 16); narrower
-// outputs split K into 32-group ranges; wider ones (or longer K) use
-// 64-column blocks over 32-group ranges.
+// block when 16-column blocks give 128..320 workgroups (M <= 16); M = 32
+// runs 16 waves over 64-group K ranges and 32 columns when that gives
+// 192..320 workgroups (a 2-way K split at 4096 x 4096); narrower outputs
+// split K into 32-group ranges; wider ones (or longer K) use 64-column
+// blocks over 32-group ranges.
 int qgemv5_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float* out, uint32_t M,
                  uint32_t N, uint32_t K, uint32_t G, const Epi& ep) {
   const char* tag = fmt_tag(fmt);
@@ -416,6 +418,9 @@ int qgemv5_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   uint32_t gx, ksplit, threads;
   if (bucket <= 16 && G <= 128 && nb16 >= 128 && nb16 <= 320) {
     var = "w16", gx = nb16, ksplit = 1, threads = 1024;
+  } else if (bucket == 32 && (N + 31) / 32 * ((G + 63) / 64) >= 192 &&
+             (uint64_t)((N + 31) / 32) * ((G + 63) / 64) <= 320) {
+    var = "k64c2", gx = (N + 31) / 32, ksplit = (G + 63) / 64, threads = 1024;
   } else if (nb16 < 128) {
     var = "k32", gx = nb16, ksplit = (G + 31) / 32, threads = 512;
   } else {

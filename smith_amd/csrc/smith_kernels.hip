@@ -1512,7 +1512,13 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   constexpr int NITEM = GPW * MR * 4;      // prep items of a wave (group, row, kslice), kslice fastest
   constexpr int IPT = (NITEM + 63) / 64;
   __shared__ u32x4 fragL[KB][4][VR];
-  __shared__ float red[WK][16 * RB][BC];
+  // when the fragments and a separate reduction array would not fit the
+  // LDS (16 waves x 32 rows), the reduction reuses the fragments after a
+  // block barrier
+  constexpr bool ALIAS = sizeof(fragL) + sizeof(float) * WK * 16 * RB * BC > 150 * 1024;
+  static_assert(!ALIAS || sizeof(fragL) >= sizeof(float) * WK * 16 * RB * BC, "reduction fits the fragments");
+  __shared__ float red_own[ALIAS ? 1 : WK][ALIAS ? 1 : 16 * RB][BC];
+  float(*red)[16 * RB][BC] = ALIAS ? (float(*)[16 * RB][BC])(void*)fragL : (float(*)[16 * RB][BC])red_own;
   __shared__ int s_last;
 
   const uint32_t lane = threadIdx.x & 63;
@@ -1664,6 +1670,7 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
 
   // 5. the WK waves of the block in fixed order, then the epilogue or the
   //    cross-block split
+  if (ALIAS) __syncthreads();  // every wave is done with the fragments
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
 #pragma unroll
@@ -1717,7 +1724,8 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
 // Row buckets m4 / m8 (hi/lo) and m16 (plain f16).  w16: 16 waves x 2
 // steps = 128 groups (all of K <= 4096 in one block), 16 columns; k32: 8
 // waves x 1 step, 16 columns (narrow N: K splits fill the chip); k32c4: the
-// same K range with 4 column tiles per wave (64 columns: wide N, long K)
+// same K range with 4 column tiles per wave (64 columns: wide N, long K);
+// m32_k64c2: 16 waves x 1 step over 64 groups, 32 columns (M = 32)
 #define DEF_QGEMV5_FMT(TAG, FMT)                                       \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m4_w16, FMT, 4, true, 1, 2, 16)      \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m8_w16, FMT, 8, true, 1, 2, 16)      \
@@ -1730,7 +1738,8 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32c4, FMT, 16, false, 4, 1, 8)   \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32, FMT, 32, false, 1, 1, 8)      \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c4, FMT, 32, false, 4, 1, 8)    \
-  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c2, FMT, 32, false, 2, 1, 8)
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c2, FMT, 32, false, 2, 1, 8)    \
+  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k64c2, FMT, 32, false, 2, 1, 16)
 
 
 // ---------------------------------------------------------------------------
