@@ -87,7 +87,11 @@ def time_steps(D, step, steps, warmup, rotation=1, graph=False):
     step makes (counted in a separate, untimed pass).  graph=True: the
     `steps` calls (step i on weight copy i % rotation, each its own launches)
     are captured once as a HIP graph, replayed once untimed, then replayed
-    once timed (launch-bound loops go through graphs)."""
+    once timed (launch-bound loops go through graphs).  SMITH_BENCH_EAGER=1
+    runs every step eagerly instead (kernel traces: the tracer sees each
+    launch)."""
+    if os.environ.get("SMITH_BENCH_EAGER") == "1":
+        graph = False
     for i in range(warmup):
         step(i)
     D.sync()
