@@ -1738,7 +1738,6 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   DEF_QGEMV5(smith_qgemv5_##TAG##_m16_k32c4, FMT, 16, false, 4, 1, 8)   \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32, FMT, 32, false, 1, 1, 8)      \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c4, FMT, 32, false, 4, 1, 8)    \
-  DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k32c2, FMT, 32, false, 2, 1, 8)    \
   DEF_QGEMV5(smith_qgemv5_##TAG##_m32_k64c2, FMT, 32, false, 2, 1, 16)
 
 
