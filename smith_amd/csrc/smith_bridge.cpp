@@ -710,13 +710,13 @@ void* smith_init(void) {
       hipEventCreate(&c->t0) != hipSuccess || hipEventCreate(&c->t1) != hipSuccess ||
       hipHostMalloc((void**)&c->pos_err_host, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
       hipHostGetDevicePointer((void**)&c->pos_err_dev, c->pos_err_host, 0) != hipSuccess) {
-    if (c->pos_err_host) hipHostFree(c->pos_err_host);
+    if (c->pos_err_host) (void)hipHostFree(c->pos_err_host);
     delete c;
     return nullptr;
   }
   memset(c->pos_err_host, 0, 256);
   if (noalloc_setup(c)) {
-    hipHostFree(c->pos_err_host);
+    (void)hipHostFree(c->pos_err_host);
     delete c;
     return nullptr;
   }
@@ -726,42 +726,42 @@ void* smith_init(void) {
 void smith_destroy(void* ctx) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return;
-  hipSetDevice(c->device);
-  hipStreamSynchronize(c->stream);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
   {
     std::lock_guard<std::mutex> lk(g_mu);
     for (auto it = g_bufs.begin(); it != g_bufs.end();) {
       if (it->second.ctx == c) {
-        hipFree(it->first);
+        (void)hipFree(it->first);
         it = g_bufs.erase(it);
       } else {
         ++it;
       }
     }
   }
-  if (c->prep) hipFree(c->prep);
-  if (c->normbuf) hipFree(c->normbuf);
-  if (c->a16) hipFree(c->a16);
-  if (c->att_ws) hipFree(c->att_ws);
-  if (c->att_cnt) hipFree(c->att_cnt);
-  if (c->ws) hipFree(c->ws);
-  if (c->counters) hipFree(c->counters);
-  if (c->amx) hipFree(c->amx);
-  for (void* r : c->retired) hipFree(r);
+  if (c->prep) (void)hipFree(c->prep);
+  if (c->normbuf) (void)hipFree(c->normbuf);
+  if (c->a16) (void)hipFree(c->a16);
+  if (c->att_ws) (void)hipFree(c->att_ws);
+  if (c->att_cnt) (void)hipFree(c->att_cnt);
+  if (c->ws) (void)hipFree(c->ws);
+  if (c->counters) (void)hipFree(c->counters);
+  if (c->amx) (void)hipFree(c->amx);
+  for (void* r : c->retired) (void)hipFree(r);
   for (auto& r : c->recs) {
-    hipEventDestroy(r.a);
-    hipEventDestroy(r.b);
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
   }
-  for (hipEvent_t e : c->event_pool) hipEventDestroy(e);
+  for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
   for (Pipeline* p : c->pipelines) delete p;
   for (Library* l : c->libs) {
-    hipModuleUnload(l->mod);
+    (void)hipModuleUnload(l->mod);
     delete l;
   }
-  hipEventDestroy(c->t0);
-  hipEventDestroy(c->t1);
-  hipStreamDestroy(c->stream);
-  if (c->pos_err_host) hipHostFree(c->pos_err_host);
+  (void)hipEventDestroy(c->t0);
+  (void)hipEventDestroy(c->t1);
+  (void)hipStreamDestroy(c->stream);
+  if (c->pos_err_host) (void)hipHostFree(c->pos_err_host);
   delete c;
 }
 
@@ -844,9 +844,9 @@ void smith_release_buffer(void* buffer) {
     g_bufs.erase(it);
   }
   // work already enqueued may still read the buffer
-  hipSetDevice(c->device);
-  hipStreamSynchronize(c->stream);
-  hipFree(buffer);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(buffer);
 }
 
 uint64_t smith_allocated_size(void* ctx) {
@@ -1120,7 +1120,7 @@ void smith_dispatch(SmithEncoder* enc, uint64_t gx, uint64_t gy, uint64_t gz, ui
   if (!enc->timed_started) {
     enc->timed_started = true;
     enc->submit_s = now_s();
-    if (hipEventCreate(&enc->ev0) == hipSuccess) hipEventRecord(enc->ev0, c->stream);
+    if (hipEventCreate(&enc->ev0) == hipSuccess) (void)hipEventRecord(enc->ev0, c->stream);
   }
   hipError_t e = hipModuleLaunchKernel(enc->pipe->fn, (unsigned)((gx + bx - 1) / bx), (unsigned)((gy + by - 1) / by),
                                        (unsigned)((gz + bz - 1) / bz), (unsigned)bx, (unsigned)by, (unsigned)bz,
@@ -1133,9 +1133,12 @@ void smith_dispatch(SmithEncoder* enc, uint64_t gx, uint64_t gy, uint64_t gz, ui
 
 void smith_end_sync(SmithEncoder* enc) {
   if (!enc) return;
-  hipSetDevice(enc->ctx->device);
-  hipStreamSynchronize(enc->ctx->stream);
-  if (enc->ev0) hipEventDestroy(enc->ev0);
+  (void)hipSetDevice(enc->ctx->device);
+  // void in the reference too: a failure of the enqueued work is left in
+  // smith_last_error
+  const hipError_t e = hipStreamSynchronize(enc->ctx->stream);
+  if (e != hipSuccess) fail(enc->ctx, "smith_end_sync: %s", hipGetErrorString(e));
+  if (enc->ev0) (void)hipEventDestroy(enc->ev0);
   delete enc;
 }
 
@@ -1144,10 +1147,10 @@ void* smith_end_async(SmithEncoder* enc) {
   hipEvent_t ev;
   void* token = nullptr;
   if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
-    hipEventRecord(ev, enc->ctx->stream);
+    (void)hipEventRecord(ev, enc->ctx->stream);
     token = (void*)ev;
   }
-  if (enc->ev0) hipEventDestroy(enc->ev0);
+  if (enc->ev0) (void)hipEventDestroy(enc->ev0);
   delete enc;
   return token;
 }
@@ -1155,29 +1158,31 @@ void* smith_end_async(SmithEncoder* enc) {
 void smith_wait(void* token) {
   if (!token) return;
   hipEvent_t ev = (hipEvent_t)token;
-  hipEventSynchronize(ev);
-  hipEventDestroy(ev);
+  (void)hipEventSynchronize(ev);
+  (void)hipEventDestroy(ev);
 }
 
 SmithTiming* smith_end_timed(SmithEncoder* enc) {
   if (!enc) return nullptr;
   Ctx* c = enc->ctx;
   SmithTiming* t = (SmithTiming*)calloc(1, sizeof(SmithTiming));
-  hipSetDevice(c->device);
+  (void)hipSetDevice(c->device);
   hipEvent_t ev1 = nullptr;
   if (enc->ev0 && hipEventCreate(&ev1) == hipSuccess) {
-    hipEventRecord(ev1, c->stream);
-    hipEventSynchronize(ev1);
+    (void)hipEventRecord(ev1, c->stream);
+    const hipError_t e = hipEventSynchronize(ev1);
+    if (e != hipSuccess) fail(c, "smith_end_timed: %s", hipGetErrorString(e));
     float ms = 0.f;
-    hipEventElapsedTime(&ms, enc->ev0, ev1);
+    (void)hipEventElapsedTime(&ms, enc->ev0, ev1);
     t->gpu_ms = ms;
-    hipEventDestroy(ev1);
+    (void)hipEventDestroy(ev1);
   } else {
-    hipStreamSynchronize(c->stream);
+    const hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) fail(c, "smith_end_timed: %s", hipGetErrorString(e));
   }
   t->gpu_end = now_s();
   t->gpu_start = enc->timed_started ? enc->submit_s : t->gpu_end;
-  if (enc->ev0) hipEventDestroy(enc->ev0);
+  if (enc->ev0) (void)hipEventDestroy(enc->ev0);
   delete enc;
   return t;
 }
@@ -1994,7 +1999,7 @@ void* smith_graph_end(void* ctx) {
   }
   hipGraphExec_t ge = nullptr;
   e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  (void)hipGraphDestroy(g);
   if (e != hipSuccess) {
     fail(c, "smith_graph_end: instantiate: %s", hipGetErrorString(e));
     return nullptr;
@@ -2011,7 +2016,7 @@ int smith_graph_launch(void* ctx, void* graph) {
 }
 
 void smith_graph_destroy(void* graph) {
-  if (graph) hipGraphExecDestroy((hipGraphExec_t)graph);
+  if (graph) (void)hipGraphExecDestroy((hipGraphExec_t)graph);
 }
 
 // ---------------- timing ----------------
