@@ -251,11 +251,13 @@ def test_config3_batched_decode_sweep(N, K):
         assert e <= (TOL_HILO if M <= 8 else TOL), (M, N, K, e)
 
 
-@pytest.mark.parametrize("N,K", [(2048, 1024), (512, 1024), (6144, 512), (2048, 8192)])
+@pytest.mark.parametrize("N,K", [(2048, 1024), (512, 1024), (6144, 512), (2048, 8192), (4080, 4096)])
 def test_batched_decode_variants_q4s_q8(N, K):
     """2 < M <= 32 on matmulQ4 / matmulQ8 at shapes that select each variant
     of the one-launch kernel (whole K per workgroup; 32-group K ranges over
-    16- or 64-column tiles), every row bucket including partial ones."""
+    16- or 64-column tiles; 64-group ranges over 32 columns at M > 16,
+    N = 4080 ending in a half-empty column block), every row bucket
+    including partial ones."""
     w = prng.randn((K, N), 61, std=0.02)
     q4, q8 = S.quantizeQ4(w), S.quantizeQ8(w)
     dq4 = O.dequant_q4s(dev_bytes(q4), K, N).astype(np.float64)
