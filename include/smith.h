@@ -295,8 +295,9 @@ int smith_linear_gguf_tiles_pair_act(void* ctx, uint32_t type1, const void* plan
                                      float* out, uint32_t K);
 /* LM head on a Q6_K output.weight read as lmHead[K=dim][N=vocab] (256-element
  * blocks along vocab, dequantQ6_K src/gguf.js:309-339): the blocks are split
- * into one plane buffer of smith_lmhead_q6_k_bytes(K, N) bytes (nibbles,
- * high bits, int8 scales and f16 d; N % 256 == 0), then
+ * into one plane buffer of smith_lmhead_q6_k_bytes(K, N) bytes (nibbles and
+ * high bits in row octets, int8 scales and f16 d; N % 256 == 0, K % 8 == 0
+ * for the repack), then
  * y = rmsnorm(x, gamma) . lmHead as smith_lmhead_q4_0_nb (K % 16 == 0). */
 uint64_t smith_lmhead_q6_k_bytes(uint32_t K, uint32_t N);
 int smith_repack_lmhead_q6_k(void* ctx, const void* blocks, void* planes, uint32_t K, uint32_t N);

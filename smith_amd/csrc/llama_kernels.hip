@@ -1278,9 +1278,12 @@ extern "C" __global__ void smith_randn_f32(float* __restrict__ out, uint64_t n, 
 // ---------------------------------------------------------------------------
 // LM head on a Q6_K output.weight read as lmHead[K=dim][N=vocab] (256-element
 // blocks along vocab, dequantQ6_K, src/gguf.js:309-339).  Planes of one
-// buffer (offsets below): per (k, 32-column group vb) 16 B of low nibbles
-// (the block's ql bytes of that group) and 8 B of high bits (its qh bytes:
-// element e's 2 bits at bit 2e), the int8 scales transposed to [N/16][K] and
+// buffer (offsets below), in row octets (K % 8 == 0): per (octet k/8,
+// 32-column group vb, quarter sub) the 4 low-nibble bytes of the quarter's 8
+// outputs for the octet's 8 rows (32 B) and their 2 high-bit bytes (16 B:
+// element e's 2 bits at bit 2e) -- the block's ql / qh bytes of that group,
+// moved, so a lane reads 8 rows of its outputs in three 16-byte loads and a
+// wave 2 KB of contiguous nibbles; the int8 scales transposed to [N/16][K] and
 // the f16 d to [N/256][K] (16 / 8 rows per 16-byte load).  Same structure as
 // smith_lmhead_q4_0_nb: lane (vb, sub) owns outputs 32vb + 8sub .. +7; per
 // row c = x_k * d * scale, 8 fma(c, q) and one -32c correction.
@@ -1304,9 +1307,9 @@ extern "C" __global__ void smith_repack_lmhead_q6_k(const uint8_t* __restrict__ 
     const uint32_t k = (uint32_t)(idx / NB), vb = (uint32_t)(idx % NB);
     const uint8_t* b = src + idx * 210;
     for (int i8 = 0; i8 < 8; i8++) {
-      const size_t r = (size_t)k * NB32 + vb * 8 + i8;
-      for (int q = 0; q < 16; q++) planes[r * 16 + q] = b[16 * i8 + q];
-      for (int q = 0; q < 8; q++) planes[ohb + r * 8 + q] = b[128 + 8 * i8 + q];
+      const size_t g = ((size_t)(k / 8) * NB32 + vb * 8 + i8) * 4;  // (octet, group) quarter 0
+      for (int q = 0; q < 16; q++) planes[(g + q / 4) * 32 + (k % 8) * 4 + q % 4] = b[16 * i8 + q];
+      for (int q = 0; q < 8; q++) planes[ohb + (g + q / 2) * 16 + (k % 8) * 2 + q % 2] = b[128 + 8 * i8 + q];
     }
     for (int t = 0; t < 16; t++) planes[osc + ((size_t)vb * 16 + t) * K + k] = b[192 + t];
     ((uint16_t*)(planes + od))[(size_t)vb * K + k] = (uint16_t)(b[208] | (b[209] << 8));
@@ -1315,7 +1318,9 @@ extern "C" __global__ void smith_repack_lmhead_q6_k(const uint8_t* __restrict__ 
 
 #define LMH_BATCH 16  // rows per batch of loads
 
-extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
+// two workgroups per CU (<= 128 VGPRs): three rounds of one did not hide the
+// batch load latency
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void smith_lmhead_q6_k_nb(
     const float* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ planes,
     float* __restrict__ y, uint32_t K, uint32_t N, float* __restrict__ ws, uint32_t* __restrict__ counters,
     GreedyTail gt) {
@@ -1349,14 +1354,19 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
     xv[q] = i < K ? x[i] : 0.f;
     gvv[q] = gamma && i < K ? gamma[i] : 1.f;
   }
-  uint32_t wn[LMH_BATCH], wh[LMH_BATCH];
+  // a batch's raw loads (the 16-bit high-bit words stay packed until use:
+  // both batches' registers live at once)
+  uint4 wn[LMH_BATCH / 4], wh[LMH_BATCH / 8];
   uint4 ws8, wd[2];
+  // kbase is a multiple of 16 below k1, and k1 a multiple of 16: both octets
+  // of a batch lie inside the wave's rows
   auto load_batch = [&](uint32_t kbase) {
 #pragma unroll
-    for (int r = 0; r < LMH_BATCH; r++) {
-      const uint32_t k = kbase + r < k1 ? kbase + r : (k1 > 0 ? k1 - 1 : 0);
-      wn[r] = *(const uint32_t*)(nib + ((size_t)k * NB + vb) * 16 + 4 * sub);
-      wh[r] = hbp[((size_t)k * NB + vb) * 4 + sub];
+    for (int oc = 0; oc < LMH_BATCH / 8; oc++) {
+      const size_t g = ((size_t)(kbase / 8 + oc) * NB + vb) * 4 + sub;
+      wn[2 * oc] = *(const uint4*)(nib + g * 32);
+      wn[2 * oc + 1] = *(const uint4*)(nib + g * 32 + 16);
+      wh[oc] = *(const uint4*)((const uint8_t*)hbp + g * 16);
     }
     const uint32_t kc = kbase < K ? kbase : K - 16;  // K % 16 == 0
     ws8 = *(const uint4*)(scp + (size_t)v16 * K + kc);
@@ -1399,12 +1409,11 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
   for (int i = 0; i < 8; i++) acc[i] = 0.f;
   float corr = 0.f;
   for (uint32_t kb16 = k0; kb16 < k1; kb16 += LMH_BATCH) {
-    uint32_t cn[LMH_BATCH], ch[LMH_BATCH];
+    uint4 cn[LMH_BATCH / 4], ch[LMH_BATCH / 8];
 #pragma unroll
-    for (int r = 0; r < LMH_BATCH; r++) {
-      cn[r] = wn[r];
-      ch[r] = wh[r];
-    }
+    for (int q = 0; q < LMH_BATCH / 4; q++) cn[q] = wn[q];
+#pragma unroll
+    for (int q = 0; q < LMH_BATCH / 8; q++) ch[q] = wh[q];
     const uint4 cs = ws8, cd0 = wd[0], cd1 = wd[1];
     if (kb16 + LMH_BATCH < k1) load_batch(kb16 + LMH_BATCH);
 #pragma unroll
@@ -1415,7 +1424,9 @@ extern "C" __global__ __launch_bounds__(512) void smith_lmhead_q6_k_nb(
       const uint32_t dw = r < 8 ? (&cd0.x)[r / 2] : (&cd1.x)[(r - 8) / 2];
       const uint16_t dh = (uint16_t)((r & 1) ? dw >> 16 : dw & 0xFFFFu);
       const float c = k < k1 ? xs[k] * ((float)__builtin_bit_cast(_Float16, dh) * (float)sc) : 0.f;
-      const uint32_t w = cn[r], h = ch[r];
+      const uint32_t w = (&cn[r / 4].x)[r % 4];
+      const uint32_t hw = (&ch[r / 8].x)[(r % 8) / 2];
+      const uint32_t h = (r & 1) ? hw >> 16 : hw & 0xFFFFu;
       corr += c;
 #pragma unroll
       for (int e = 0; e < 8; e++) {

@@ -1879,6 +1879,7 @@ int smith_repack_lmhead_q6_k(void* ctx, const void* blocks, void* planes, uint32
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
   if (N % 256 || !N) return fail(c, "smith_repack_lmhead_q6_k: vocab %u is not a multiple of 256", N);
+  if (K % 8) return fail(c, "smith_repack_lmhead_q6_k: dim %u is not a multiple of 8 (row octets)", K);
   if (set_device(c)) return -1;
   uint64_t total = (uint64_t)K * (N / 256);
   if (!total) return 0;
