@@ -1429,13 +1429,15 @@ int act_gemv(Ctx* c, const char* fn, Fmt fmt, const void* act_in, int norm, floa
   // K = 9216 (down projection): 12 waves of 6 steps instead of 8 of 9;
   // 256 < N/16 <= 512 column tiles (the fused q|k|v at dim 3072): two tiles
   // per wave, so the blocks fit one round on the 256 CUs instead of leaving
-  // 1.25 per CU (config-5 decode 948 -> 973-980 tok/s with both)
+  // 1.25 per CU (config-5 decode 948 -> 973-980 tok/s with both).  Q4_K also
+  // on the wider gate|up (1152 column tiles: Q4_K_M decode 873 -> 882
+  // tok/s; Q4_0 there measured 1010 -> 998, so it keeps one tile per wave)
   uint32_t gxx = gx, thr = threads;
   if (kb == 288) {
     // without a norm (the down projection): the variant that has no norm code
     strncat(name, norm ? "_w12" : "_w12_nn", sizeof name - strlen(name) - 1);
     thr = 768;
-  } else if (kb == 96 && gx > 256 && gx <= 512 && gx % 2 == 0) {
+  } else if (kb == 96 && gx > 256 && gx % 2 == 0 && (gx <= 512 || fmt == FQ4KT)) {
     strncat(name, "_c2", sizeof name - strlen(name) - 1);
     gxx = gx / 2;
   }
