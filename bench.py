@@ -464,6 +464,15 @@ def bench_e2e(D, path, prompt_len=128, new_tokens=128, reps=3, mix="q4_0"):
                  "weight_stream_GBps": round(gb_per_token / (best["decode_ms_per_token"] * 1e-3) / 1e9, 1),
                  "tokens_generated": len(out) - prompt_len, "gguf_write_s": round(t_write, 1),
                  "load_s": round(t_load, 1), "first_tokens": out[prompt_len:prompt_len + 8]})
+    # a fast decode of wrong tokens is no measurement: the first tokens must be
+    # those of the oracle-checked run (tests/test_gpu_config5.py holds them to
+    # the same file)
+    with open(os.path.join(ROOT, "tests", "golden", "cfg5_first_tokens.json")) as f:
+        want = json.load(f)[mix]
+    if best["first_tokens"] != want:
+        raise RuntimeError("config 5 (%s): first tokens %s differ from the oracle-checked %s"
+                           % (mix, best["first_tokens"], want))
+    best["first_tokens_match_fixture"] = True
     return best
 
 

@@ -80,8 +80,10 @@ int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes); /* enqueued fill k
  * the f16 A operand of the GEMM after it (RMS-normalised with gamma when
  * gamma is non-null, with eps), and that GEMM skips its own activation prep
  * if it reads exactly those rows with the same gamma and eps.  Any other op
- * between the two must not modify those rows.  The hint is dropped by the
- * next matmul / linear / attention call whatever path it takes. */
+ * between the two must not modify those rows.  The hint, and the prepared
+ * operand it leads to, are dropped by every kernel launch of any other call
+ * (op entry points, smith_fill_zero, generic dispatches) and every copy into
+ * device memory. */
 int smith_prep_next(void* ctx, const float* gamma, float eps);
 
 /* Platform calibration, no counterpart in the reference (for benchmarks that
@@ -153,7 +155,11 @@ int smith_matmul_q4(void* ctx, const float* a, const void* wq, float* out, uint3
  * not fit returns -1 with the sizes in smith_last_error (e.g. the M >= 256
  * prefill GEMM at K = 14336); no hipMalloc / hipFree is ever called.  Calls
  * that overlap on one GPU (two contexts or streams at once) race on the
- * array. */
+ * array: a second host thread entering while one is enqueueing fails with an
+ * error, but work of two streams overlapping on the GPU is not detected.
+ * The split-K counters in the array return to zero at the end of every
+ * launch that completes; a launch that faults ends the process's device
+ * context anyway. */
 int smith_matmul_q4_noalloc(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
                             uint32_t K, uint32_t groups);
 

@@ -253,3 +253,15 @@ def normwise_rel_err(y, ref):
     ref = np.asarray(ref, dtype=np.float64)
     den = np.max(np.abs(ref))
     return float(np.max(np.abs(y - ref)) / (den if den > 0 else 1.0))
+
+
+def elementwise_rel_err(y, ref, atol_frac=1e-3):
+    """max |y - ref| / (|ref| + atol) over all elements, atol = atol_frac *
+    rms(ref): the per-element relative error, kept finite where an output
+    crosses zero."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    atol = atol_frac * float(np.sqrt(np.mean(ref * ref)))
+    if atol <= 0:
+        atol = 1.0
+    return float(np.max(np.abs(y - ref) / (np.abs(ref) + atol)))

@@ -17,6 +17,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -175,7 +176,17 @@ int find_kernel(Ctx* c, const char* name, hipFunction_t* out) {
   return fail(c, "smith: kernel '%s' not found in any loaded code object", name);
 }
 
+// The smith_prep_next hint and the prepared f16 operand it leads to belong to
+// the one call that follows: gemm() and the prefill attention read them
+// before their first launch and set them after their last, so every other
+// launch and every copy into device memory drops them here.
+void drop_hints(Ctx* c) {
+  c->next_pending = false;
+  c->a16_src = nullptr;
+}
+
 int launch(Ctx* c, const char* name, dim3 grid, dim3 block, void** args, unsigned shmem = 0) {
+  drop_hints(c);
   hipFunction_t f;
   if (find_kernel(c, name, &f)) return -1;
   hipEvent_t ea = nullptr, eb = nullptr;
@@ -210,6 +221,7 @@ int ensure(Ctx* c, void** p, size_t* have, size_t need) {
   size_t sz = (need + 0xFFFFF) & ~(size_t)0xFFFFF;
   HIPCHK(c, hipMalloc(p, sz));
   *have = sz;
+  c->allocated += sz;  // the device's allocated size counts the op scratch too
   return 0;
 }
 
@@ -239,6 +251,7 @@ int ensure_counters(Ctx* c, size_t n) {
   c->counters_n = 0;
   size_t cap = std::max<size_t>(n, 4096);
   HIPCHK(c, hipMalloc((void**)&c->counters, cap * sizeof(uint32_t)));
+  c->allocated += cap * sizeof(uint32_t);
   // counters start at zero once; the kernel's last workgroup resets its own
   HIPCHK(c, hipMemset(c->counters, 0, cap * sizeof(uint32_t)));
   c->counters_n = cap;
@@ -249,6 +262,7 @@ int ensure_amx(Ctx* c) {
   if (c->amx) return 0;
   if (c->capturing) return fail(c, "smith: greedy LM head state needed while capturing a graph; run the op once first");
   HIPCHK(c, hipMalloc((void**)&c->amx, 2 * sizeof(uint64_t)));
+  c->allocated += 2 * sizeof(uint64_t);
   HIPCHK(c, hipMemset(c->amx, 0, 2 * sizeof(uint64_t)));
   return 0;
 }
@@ -683,6 +697,10 @@ constexpr size_t NOALLOC_PREP_BYTES = 4u << 20;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 constexpr int NOALLOC_MAX_DEVICES = 64;
 static void* g_scratch_dev[NOALLOC_MAX_DEVICES];
+// set while a host thread enqueues work on that device's static scratch: a
+// second thread's call fails instead of sharing the counters (work of two
+// streams that overlaps on the GPU after enqueueing is not detected)
+static std::atomic<bool> g_scratch_busy[NOALLOC_MAX_DEVICES];
 
 // Once per device, with that device current: the device address of its copy
 // of `scratch`, and its counter region cleared (outside any capture).
@@ -882,6 +900,7 @@ int64_t smith_test_release_after_use(void* ctx) {
 int smith_copy_h2d(void* ctx, void* dst, uint64_t off, const void* src, uint64_t bytes) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
+  drop_hints(c);
   if (set_device(c)) return -1;
   if (!bytes) return 0;
   HIPCHK(c, hipMemcpyAsync((char*)dst + off, src, bytes, hipMemcpyHostToDevice, c->stream));
@@ -903,6 +922,7 @@ int smith_copy_d2h(void* ctx, void* dst, const void* src, uint64_t off, uint64_t
 int smith_copy_d2d(void* ctx, void* dst, uint64_t doff, const void* src, uint64_t soff, uint64_t bytes) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;
+  drop_hints(c);
   if (set_device(c)) return -1;
   if (!bytes) return 0;
   HIPCHK(c, hipMemcpyAsync((char*)dst + doff, (const char*)src + soff, bytes, hipMemcpyDeviceToDevice, c->stream));
@@ -915,6 +935,7 @@ int smith_copy_2d(void* ctx, void* dst, uint64_t dpitch, const void* src, uint64
   if (!c) return -1;
   if (!rows || !width) return 0;
   if (!dst || !src || width > dpitch || width > spitch) return fail(c, "smith_copy_2d: bad pitches or buffers");
+  drop_hints(c);
   if (set_device(c)) return -1;
   HIPCHK(c, hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDeviceToDevice, c->stream));
   return 0;
@@ -1122,6 +1143,7 @@ void smith_dispatch(SmithEncoder* enc, uint64_t gx, uint64_t gy, uint64_t gz, ui
     enc->submit_s = now_s();
     if (hipEventCreate(&enc->ev0) == hipSuccess) (void)hipEventRecord(enc->ev0, c->stream);
   }
+  drop_hints(c);
   hipError_t e = hipModuleLaunchKernel(enc->pipe->fn, (unsigned)((gx + bx - 1) / bx), (unsigned)((gy + by - 1) / by),
                                        (unsigned)((gz + bz - 1) / bz), (unsigned)bx, (unsigned)by, (unsigned)bz,
                                        (unsigned)enc->shmem, c->stream, nullptr, extra);
@@ -1281,9 +1303,16 @@ int smith_matmul_q4_noalloc(void* ctx, const float* a, const void* wq, float* ou
   c->prep_bytes = c->a16_bytes = NOALLOC_PREP_BYTES;
   c->ws = (float*)(base + NOALLOC_CNT_BYTES + NOALLOC_PREP_BYTES);
   c->ws_bytes = NOALLOC_BYTES - NOALLOC_CNT_BYTES - NOALLOC_PREP_BYTES;
+  if (g_scratch_busy[c->device].exchange(true))
+    return fail(c, "smith_matmul_q4_noalloc: another call is enqueueing on device %d's static scratch", c->device);
+  // the context's prepared-operand hint names its own f16 buffer, not the
+  // static region: dropped before and after
+  drop_hints(c);
   c->no_alloc = "smith_matmul_q4_noalloc";
   const int rc = qmatmul(c, FQ4S, a, wq, nullptr, out, M, N, K, groups);
   c->no_alloc = nullptr;
+  drop_hints(c);
+  g_scratch_busy[c->device].store(false);
   c->prep = sv.prep, c->prep_bytes = sv.prep_bytes, c->a16 = sv.a16, c->a16_bytes = sv.a16_bytes;
   c->ws = sv.ws, c->ws_bytes = sv.ws_bytes, c->counters = sv.counters, c->counters_n = sv.counters_n;
   return rc;
@@ -1610,6 +1639,7 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
     c->att_cnt_n = 0;
     size_t cap = std::max<size_t>(slots, 4096);
     HIPCHK(c, hipMalloc((void**)&c->att_cnt, cap * sizeof(uint32_t)));
+    c->allocated += cap * sizeof(uint32_t);
     HIPCHK(c, hipMemset(c->att_cnt, 0, cap * sizeof(uint32_t)));
     c->att_cnt_n = cap;
   }

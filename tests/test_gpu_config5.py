@@ -9,11 +9,23 @@ whole teacher-forced sequence (prompt + the first 127 generated tokens) as
 one causal forward, decoding one layer of weights at a time, which gives the
 logits of all 128 steps at once.  Bars:
   * every step's GPU logits (prefill, then host-driven forwardDecode along
-    the same tokens) within 1e-2 normwise of the oracle's;
+    the same tokens) within 1e-2 normwise of the oracle's: the M = 128
+    prompt GEMMs take f16 activations and f16 weights on MFMA (the north
+    star's GEMM bar), and their error stays in the KV cache every later
+    step reads (observed ~2-4e-3 at every step);
+  * the same 255 tokens fed through the decode kernels alone, one per step
+    from position 0 (exact weights, hi/lo activations, no f16 GEMM in any
+    cache): every position's logits within 1e-3 normwise, so a regression of
+    the decode kernels shows even under the prompt's error;
+  * the first eight generated tokens equal the committed fixture
+    tests/golden/cfg5_first_tokens.json (the tokens of an oracle-checked
+    run; bench.py checks its own run against the same file);
   * every generated token equal to the oracle's argmax at that step, except
     where the oracle's top two logits are closer than twice the step's
     largest logit error (then either may win within the tolerance).
 """
+import json
+import os
 import sys
 import time
 
@@ -28,8 +40,10 @@ from smith_amd.synthetic_gguf import CONFIG5, build_llama_gguf
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-2
+TOL_PREFILL = 1e-2  # any step after the f16-operand prompt GEMMs
+TOL_DECODE = 1e-3  # the decode kernels alone
 PROMPT, NEW = 128, 128
+FIRST_TOKENS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cfg5_first_tokens.json")
 
 
 def _progress(msg):
@@ -54,6 +68,11 @@ def test_config5_full_workload(tmp_path_factory, mix):
     gpu = [m.forwardPrefill(prompt, caches)["logits"][-1]]
     for i in range(NEW - 1):
         gpu.append(m.forwardDecode(gen[i], PROMPT + i, caches)["logits"][0])
+    # the same 255 tokens through the decode kernels alone, from position 0
+    # (the prompt too, one token per step): no f16 prompt GEMM in any cache
+    seq = prompt + gen[:NEW - 1]
+    caches = m.createCache()
+    dec_only = [m.forwardDecode(t, i, caches)["logits"][0] for i, t in enumerate(seq)]
     del m, caches
     _progress("%s: GPU generate + %d host-driven steps in %.1f s; %d distinct tokens"
               % (mix, NEW, time.time() - t0, len(set(gen))))
@@ -61,14 +80,21 @@ def test_config5_full_workload(tmp_path_factory, mix):
     t0 = time.time()
     ref = LO.LlamaOracle(path)
     assert ref.lazy
-    ref_logits = ref.forward(prompt + gen[:NEW - 1], 0)[PROMPT - 1:]
+    ref_all = ref.forward(seq, 0)
+    ref_logits = ref_all[PROMPT - 1:]
     _progress("%s: oracle forward of %d tokens in %.1f s" % (mix, PROMPT + NEW - 1, time.time() - t0))
     assert ref_logits.shape == (NEW, c["vocab"])
 
     errs = [normwise_rel_err(g, r) for g, r in zip(gpu, ref_logits)]
-    _progress("%s: logits error max %.2e (step %d), median %.2e, last %.2e"
-              % (mix, max(errs), int(np.argmax(errs)), float(np.median(errs)), errs[-1]))
-    assert max(errs) <= TOL, (mix, int(np.argmax(errs)), max(errs))
+    _progress("%s: logits error after the prompt GEMMs: prefill %.2e; decode steps max %.2e (step %d), "
+              "median %.2e" % (mix, errs[0], max(errs[1:]), 1 + int(np.argmax(errs[1:])), float(np.median(errs[1:]))))
+    assert max(errs) <= TOL_PREFILL, (mix, int(np.argmax(errs)), max(errs))
+    derrs = [normwise_rel_err(g, r) for g, r in zip(dec_only, ref_all)]
+    _progress("%s: logits error of the decode kernels alone (255 positions): max %.2e (position %d), median %.2e"
+              % (mix, max(derrs), int(np.argmax(derrs)), float(np.median(derrs))))
+    assert max(derrs) <= TOL_DECODE, (mix, int(np.argmax(derrs)), max(derrs))
+    with open(FIRST_TOKENS) as f:
+        assert gen[:8] == json.load(f)[mix], (mix, gen[:8])
     flips = 0
     for i, (t, g, r) in enumerate(zip(gen, gpu, ref_logits)):
         # the graph path's token is the argmax of the host-driven path's

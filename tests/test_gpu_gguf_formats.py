@@ -407,3 +407,49 @@ def test_prep_next_chain_matches_unhinted(t):
     r4 = np.stack([_rms(r, g1) for r in r3]) @ wd[3].T
     for got, ref in zip(fused, (r1, h, r3, r4)):
         assert normwise_rel_err(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("between", ["act_gemv", "fill_zero", "copy"])
+def test_prep_next_hint_dropped_by_other_calls(between):
+    """A smith_prep_next hint followed by any other launch or copy is gone by
+    the time the next K-split GEMM runs: that GEMM ends in the plain reduce
+    (no smith_gemm_reduce_prep reading the hinted gamma), and its output
+    equals the unhinted call's bit for bit."""
+    t = O.GGML_Q4_0
+    M, D = 128, 1024
+    ctx = device.ops_ctx()
+    blocks, _ = _weights(t, D, D, 91)
+    pl = _planes(t, blocks, D, D)[0]
+    xb, rb = _buf(prng.randn((M, D), 92)), _buf(prng.randn((M, D), 93))
+    gb = _buf(1 + prng.randn((D,), 94, std=0.1))
+    scratch = device.alloc(4096)
+
+    def run(hint):
+        y = device.alloc(M * D * 4)
+        if hint:
+            device.check(device.lib.smith_prep_next(ctx, gb, EPS))
+            if between == "fill_zero":
+                device.check(device.lib.smith_fill_zero(ctx, scratch, 4096))
+            elif between == "copy":
+                device.check(device.lib.smith_copy_d2d(ctx, scratch, 0, xb, 0, 4096))
+            else:  # a decode act GEMV (row 0 of x through the embedding's act output)
+                tok, row = _buf(np.zeros(1, np.int32)), device.alloc(D * 4)
+                act = device.alloc(D * 4 + D // 8 * 12)
+                device.check(device.lib.smith_embed(ctx, xb, tok, row, 1, D, act, None))
+                device.check(device.lib.smith_prep_next(ctx, gb, EPS))  # the embed dropped the first hint
+                device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act, 0, 0.0, pl, row, D, D,
+                                                                     None, 0, None, None))
+        device.profile_kernels(True)
+        device.check(device.lib.smith_linear_gguf_tiles(ctx, t, xb, pl, y, M, D, D, None, 0.0, rb, 1))
+        _, n_fused = device.profile_read("smith_gemm_reduce_prep")
+        _, n_plain = device.profile_read("smith_gemm_reduce")
+        device.profile_read("")
+        device.profile_kernels(False)
+        out = _get(y, M * D)
+        device.release_buffer(y)
+        return out, n_fused, n_plain
+
+    want, f0, p0 = run(False)
+    got, f1, p1 = run(True)
+    assert (f0, p0) == (0, 1) and (f1, p1) == (0, 1), (f0, p0, f1, p1)
+    assert np.array_equal(got, want)

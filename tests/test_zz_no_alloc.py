@@ -14,13 +14,102 @@ from smith_amd import device, prng
 pytestmark = pytest.mark.gpu
 
 
-def _run(fn, a_buf, q_buf, M, N, K):
-    out = device.alloc(M * N * 4)
-    rc = fn(device.ops_ctx(), a_buf, q_buf, out, M, N, K, (K + 31) // 32)
+def _run(fn, a_buf, q_buf, M, N, K, out=None, ctx=None):
+    own = out is None
+    if own:
+        out = device.alloc(M * N * 4)
+    rc = fn(ctx or device.ops_ctx(), a_buf, q_buf, out, M, N, K, (K + 31) // 32)
     device.check(rc, fn.__name__)
+    if ctx:
+        assert device.lib.smith_sync(ctx) == 0
+    else:
+        device.sync()
     y = device.download(out, M * N * 4, np.float32).reshape(M, N)
-    device.release_buffer(out)
+    if own:
+        device.release_buffer(out)
     return y
+
+
+def _fresh_ctx():
+    """A second context with the code objects loaded and no op scratch yet."""
+    lib = device.lib
+    c = lib.smith_init()
+    assert c
+    for path in (device.CODE_OBJECT_PATH, device.LLAMA_CODE_OBJECT_PATH, device.GEMM_CODE_OBJECT_PATH):
+        assert lib.smith_load_library(c, path.encode()), lib.smith_last_error(c)
+    return c
+
+
+def test_noalloc_first_call_on_fresh_context():
+    """On a context that has never run an op (no scratch of its own), the
+    no-alloc entry point works for shapes that use every region, its
+    allocated size stays zero, and a following allocating call agrees."""
+    lib = device.lib
+    c = _fresh_ctx()
+    try:
+        assert lib.smith_allocated_size(c) == 0
+        for (M, N, K) in ((1, 4096, 14336), (32, 4096, 4096), (64, 1024, 4096)):
+            print("noalloc fresh ctx", M, N, K, flush=True)
+            w = prng.randn((K, N), 960 + M, std=0.02)
+            a = prng.randn((M, K), 970 + M)
+            q = O.quantize_q4s(w)
+            bq, ba, bo = device.alloc(q.nbytes), device.alloc(a.nbytes), device.alloc(M * N * 4)
+            device.upload(bq, q)
+            device.upload(ba, a)
+            got = _run(lib.smith_matmul_q4_noalloc, ba, bq, M, N, K, bo, ctx=c)
+            assert lib.smith_sync(c) == 0
+            assert lib.smith_allocated_size(c) == 0
+            want = _run(lib.smith_matmul_q4, ba, bq, M, N, K, bo, ctx=c)
+            assert lib.smith_sync(c) == 0
+            assert lib.smith_allocated_size(c) > 0  # the allocating entry grew its scratch
+            assert np.array_equal(got, want), (M, N, K)
+            for b in (bq, ba, bo):
+                device.release_buffer(b)
+            lib.smith_destroy(c)
+            c = _fresh_ctx()
+    finally:
+        lib.smith_destroy(c)
+
+
+def test_noalloc_ignores_prepared_operand_hint():
+    """A hinted K-split GEMM (smith_prep_next) leaves its output rows prepared
+    as f16 in the context's own buffer; a no-alloc call on those rows right
+    after must prepare its operand in the static array itself, and equals
+    smith_matmul_q4 on the same rows."""
+    lib = device.lib
+    ctx = device.ops_ctx()
+    M, D = 128, 1024
+    x = prng.randn((M, D), 981)
+    res = prng.randn((M, D), 982)
+    wt = prng.randn((D, D), 983, std=0.02)  # GGUF listing [out, in]
+    xb, rb = device.alloc(x.nbytes), device.alloc(res.nbytes)
+    device.upload(xb, x)
+    device.upload(rb, res)
+    wtb = device.alloc(wt.nbytes)
+    device.upload(wtb, wt)
+    G = D // 32
+    blocks, nib, dsc = device.alloc(D * G * 18), device.alloc(D * G * 16), device.alloc(D * G * 2)
+    device.check(lib.smith_quantize_q4_0(ctx, wtb, blocks, D, D))
+    device.check(lib.smith_repack_q4_0_t_into(ctx, blocks, nib, dsc, D, D, 0, 1, D))
+    w2 = prng.randn((D, 512), 984, std=0.02)
+    q2 = O.quantize_q4s(w2)
+    bq = device.alloc(q2.nbytes)
+    device.upload(bq, q2)
+    y1 = device.alloc(M * D * 4)
+
+    def hinted_linear():
+        device.check(lib.smith_prep_next(ctx, None, 0.0))
+        device.check(lib.smith_linear_q4_0_t(ctx, xb, nib, dsc, y1, M, D, D, None, 0.0, rb, 1))
+
+    hinted_linear()
+    got = _run(lib.smith_matmul_q4_noalloc, y1, bq, M, 512, D)
+    hinted_linear()
+    want = _run(lib.smith_matmul_q4, y1, bq, M, 512, D)
+    assert np.array_equal(got, want)
+    y1h = device.download(y1, M * D * 4, np.float32).reshape(M, D)
+    assert O.normwise_rel_err(got, O.matmul_q4s(y1h, q2, D, 512)) <= 1e-2
+    for b in (xb, rb, wtb, blocks, nib, dsc, bq, y1):
+        device.release_buffer(b)
 
 
 # (M, N, K): M=1 with a cross-block K split (partials + counters), M=4 / 8
@@ -41,11 +130,15 @@ def test_noalloc_matches_allocating_entry(first, second):
         bq, ba = device.alloc(q.nbytes), device.alloc(a.nbytes)
         device.upload(bq, q)
         device.upload(ba, a)
-        want = _run(lib.smith_matmul_q4, ba, bq, M, N, K)
+        # the allocating entry point's scratch counts in the allocated size,
+        # so an allocation inside the no-alloc calls would show here
+        out = device.alloc(M * N * 4)
         before = lib.smith_allocated_size(device.ctx())
-        got = _run(lib.smith_matmul_q4_noalloc, ba, bq, M, N, K)
-        got2 = _run(lib.smith_matmul_q4_noalloc, ba, bq, M, N, K)  # counters left at zero by the first
+        got = _run(lib.smith_matmul_q4_noalloc, ba, bq, M, N, K, out)
+        got2 = _run(lib.smith_matmul_q4_noalloc, ba, bq, M, N, K, out)  # counters left at zero by the first
         assert lib.smith_allocated_size(device.ctx()) == before
+        device.release_buffer(out)
+        want = _run(lib.smith_matmul_q4, ba, bq, M, N, K)
         assert np.array_equal(got, want) and np.array_equal(got2, want), (M, N, K)
         assert O.normwise_rel_err(got, O.matmul_q4s(a, q, K, N)) <= 1e-3
         device.release_buffer(bq)
