@@ -86,13 +86,6 @@ int smith_fill_zero(void* ctx, void* buffer, uint64_t bytes); /* enqueued fill k
  * device memory. */
 int smith_prep_next(void* ctx, const float* gamma, float eps);
 
-/* Platform calibration, no counterpart in the reference (for benchmarks that
- * put a kernel beside the floor of its bytes): kind 0 = an empty launch,
- * 1 = a plain 16-byte streaming read of `bytes` (contiguous 12 KB per
- * 128-thread workgroup), 2 = the config-1 Q4S GEMV's
- * weight reads alone (K = 4096 records of N columns, bytes = 128 * N * 24).
- * `out`: a 4-byte device buffer the kernels never write in practice. */
-int smith_calib_read(void* ctx, uint32_t kind, const void* buffer, uint64_t bytes, uint32_t N, void* out);
 int smith_sync(void* ctx);
 void smith_free(void* p); /* strings and SmithTiming returned by this library */
 const char* smith_last_error(void* ctx);

@@ -963,33 +963,6 @@ int smith_prep_next(void* ctx, const float* gamma, float eps) {
   return 0;
 }
 
-int smith_calib_read(void* ctx, uint32_t kind, const void* buffer, uint64_t bytes, uint32_t N, void* out) {
-  Ctx* c = (Ctx*)ctx;
-  if (!c) return -1;
-  if (set_device(c)) return -1;
-  if (!out) return fail(c, "smith_calib_read: needs a 4-byte output buffer");
-  const void* pb = buffer;
-  void* po = out;
-  if (kind == 0 || kind == 1) {
-    if (bytes % 16) return fail(c, "smith_calib_read: byte count %llu is not a multiple of 16", (unsigned long long)bytes);
-    uint64_t n16 = bytes / 16;
-    void* args[] = {&pb, &n16, &po};
-    if (kind == 0) return launch(c, "smith_calib_empty", dim3(1024), dim3(256), args);
-    // contiguous 12 KB per 128-thread workgroup, six 16-byte loads per thread
-    const uint64_t blocks = (n16 + 767) / 768;
-    if (blocks > 0x7FFFFFFFu) return fail(c, "smith_calib_read: %llu bytes is too large", (unsigned long long)bytes);
-    return launch(c, "smith_calib_block_read", dim3((unsigned)blocks), dim3(128), args);
-  }
-  if (kind == 2) {
-    if (N == 0 || N % 16 || bytes != (uint64_t)128 * N * 24)
-      return fail(c, "smith_calib_read: Q4S record read needs K = 4096 records of N %% 16 == 0 columns");
-    uint32_t pN = N;
-    void* args[] = {&pb, &pN, &po};
-    return launch(c, "smith_calib_q4s_record_read", dim3(N / 16), dim3(512), args);
-  }
-  return fail(c, "smith_calib_read: unknown kind %u", kind);
-}
-
 int smith_sync(void* ctx) {
   Ctx* c = (Ctx*)ctx;
   if (!c) return -1;

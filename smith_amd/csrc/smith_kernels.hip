@@ -2275,68 +2275,3 @@ extern "C" __global__ void smith_zero_u32(uint32_t* __restrict__ p, uint64_t n) 
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = 0u;
 }
-
-// Platform calibration (bench.py --calibrate): a plain 128-bit streaming read
-// with U loads in flight per thread, and an empty kernel.  They bound what
-// any kernel reading the same bytes can achieve on this GPU.
-extern "C" __global__ void smith_calib_stream_read(const uint4* __restrict__ p, uint64_t n16, uint32_t* out) {
-  constexpr int U = 4;
-  uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (uint64_t)gridDim.x * blockDim.x;
-  uint32_t acc = 0;
-  for (uint64_t base = tid; base < n16; base += stride * U) {
-    uint4 v[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      uint64_t i = base + u * stride;
-      v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  }
-  if (acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads alive
-}
-
-// Streaming read in per-workgroup contiguous chunks: 128 threads x 6
-// 16-byte loads, all in flight (the fastest shape of a grid sweep over
-// 64-1024 threads and 1-12 loads per thread on 12.6 MB)
-extern "C" __global__ __launch_bounds__(128) void smith_calib_block_read(const uint4* __restrict__ p, uint64_t n16,
-                                                                       uint32_t* out) {
-  const uint64_t base = (uint64_t)blockIdx.x * 128 * 6 + threadIdx.x;
-  uint4 v[6];
-#pragma unroll
-  for (int u = 0; u < 6; u++) {
-    const uint64_t i = base + 128 * u;
-    v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
-  }
-  uint32_t acc = 0;
-#pragma unroll
-  for (int u = 0; u < 6; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  if (acc == 0x9e3779b9u) out[0] = acc;
-}
-
-// The config-1 GEMV's weight reads alone: the grid, workgroup shape and
-// per-lane record loads of smith_qgemv1_*_m1_k128 on Q4S records (N / 16
-// workgroups of 8 waves; lane (c, j) of wave w reads the 16 + 8 bytes of
-// record (group 16w + 4s + j, column 16 * block + c) for s = 0..3), no math.
-// K = 4096 (128 groups), N % 16 == 0.
-extern "C" __global__ __launch_bounds__(512) void smith_calib_q4s_record_read(const uint8_t* __restrict__ B,
-                                                                            uint32_t N, uint32_t* out) {
-  const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 15, j = lane >> 4;
-  const uint32_t n = blockIdx.x * 16 + c;
-  u32x4 q[4];
-  uint2 sz[4];
-#pragma unroll
-  for (int s = 0; s < 4; s++) {
-    const uint8_t* p = B + ((size_t)(16 * w + 4 * s + j) * N + n) * 24;
-    q[s] = *(const u32x4*)p;
-    sz[s] = *(const uint2*)(p + 16);
-  }
-  uint32_t acc = 0;
-#pragma unroll
-  for (int s = 0; s < 4; s++) acc ^= q[s].x ^ q[s].y ^ q[s].z ^ q[s].w ^ sz[s].x ^ sz[s].y;
-  if (acc == 0x9e3779b9u) out[0] = acc;
-}
-
-extern "C" __global__ void smith_calib_empty(const uint4* p, uint64_t n16, uint32_t* out) {
-  if (n16 == 0x12345u) out[0] = (uint32_t)(size_t)p;
-}

@@ -51,7 +51,6 @@ SYMBOLS = {
     "smith_copy_d2h": (_INT, [_P, _P, _P, _U64, _U64]),
     "smith_copy_d2d": (_INT, [_P, _P, _U64, _P, _U64, _U64]),
     "smith_fill_zero": (_INT, [_P, _P, _U64]),
-    "smith_calib_read": (_INT, [_P, _U32, _P, _U64, _U32, _P]),
     "smith_prep_next": (_INT, [_P, _P, ctypes.c_float]),
     "smith_sync": (_INT, [_P]),
     "smith_free": (None, [_P]),

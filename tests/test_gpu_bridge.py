@@ -156,25 +156,3 @@ def test_dispatch_sync_one_shot():
 def test_compile_source_error_is_reported():
     with pytest.raises(RuntimeError, match="shader compilation failed"):
         device.compile_source('extern "C" __global__ void broken(float* o) { o[0] = undefined_name; }')
-
-
-def test_calib_read_kinds_and_argument_errors():
-    """smith_calib_read (bench floor kernels): the empty launch, the block
-    streaming read of a ragged size and the Q4S record read run and leave
-    the output untouched; a record read of the wrong size and an unknown
-    kind fail with an error instead of launching."""
-    ctx = device.ops_ctx()
-    N = 64
-    nbytes = 128 * N * 24
-    buf = device.alloc(nbytes)
-    device.check(device.lib.smith_fill_zero(ctx, buf, nbytes))
-    out = device.alloc(256)
-    device.check(device.lib.smith_fill_zero(ctx, out, 256))
-    for kind, size in ((0, nbytes), (1, nbytes - 48), (2, nbytes)):
-        device.check(device.lib.smith_calib_read(ctx, kind, buf, size, N, out))
-    device.check(device.lib.smith_sync(ctx))
-    assert not device.download(out, 256, np.uint8).any()
-    assert device.lib.smith_calib_read(ctx, 2, buf, nbytes - 24, N, out) != 0
-    assert device.lib.smith_calib_read(ctx, 7, buf, nbytes, N, out) != 0
-    device.release_buffer(buf)
-    device.release_buffer(out)

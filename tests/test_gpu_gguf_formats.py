@@ -453,3 +453,38 @@ def test_prep_next_hint_dropped_by_other_calls(between):
     got, f1, p1 = run(True)
     assert (f0, p0) == (0, 1) and (f1, p1) == (0, 1), (f0, p0, f1, p1)
     assert np.array_equal(got, want)
+
+
+def test_q4_k_gate_up_two_tiles_per_wave_at_config5_width():
+    """The Q4_K gate|up act GEMV at the config-5 width (N = 2 x 9216
+    interleaved gate/up columns = 1152 column tiles, K = 3072) runs two
+    column tiles per wave (the _c2 variant); with the RMSNorm scale, the
+    SwiGLU epilogue and the act of h emitted for the down projection, which
+    then consumes that act: both outputs against the float64 products of
+    the oracle's weights."""
+    t = O.GGML_Q4_K
+    D, F = 3072, 9216
+    ctx = device.ops_ctx()
+    b_gu, wgu = _weights(t, 2 * F, D, 41)
+    b_dn, wdn = _weights(t, D, F, 42)
+    p_gu, _ = _planes(t, b_gu, 2 * F, D)
+    p_dn, _ = _planes(t, b_dn, D, F)
+    wgu, wdn = wgu.astype(np.float64), wdn.astype(np.float64)
+    x = prng.randn((D,), 43).astype(np.float64)
+    g = 1 + prng.randn((D,), 44, std=0.1).astype(np.float64)
+    act_x = _act_of(x, g)
+    hb, act_h = device.alloc(F * 4), device.alloc(F * 4 + F // 8 * 12)
+    device.profile_kernels(True)
+    device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act_x, 1, EPS, p_gu, hb, 2 * F, D, None, 2, act_h,
+                                                        None))
+    _, n_c2 = device.profile_read("smith_agemv_q4kt_k96_c2")
+    device.profile_read("")
+    device.profile_kernels(False)
+    assert n_c2 == 1
+    h = _get(hb, F).astype(np.float64)
+    assert normwise_rel_err(h, _silu_mul(wgu @ _rms(x, g))) <= TOL_SWIGLU
+    outb = device.alloc(D * 4)
+    device.check(device.lib.smith_linear_gguf_tiles_act(ctx, t, act_h, 0, 0.0, p_dn, outb, D, F, None, 0, None, None))
+    assert normwise_rel_err(_get(outb, D), wdn @ h) <= TOL
+    for b in (p_gu, p_dn, hb, act_h, outb):
+        device.release_buffer(b)
