@@ -281,9 +281,10 @@ def cpu_baseline(K, N, budget_s):
     w = prng.randn((K, N), 1, std=0.02)
     a = prng.randn((1, K), 0)
     q = O.quantize_q4s(w)
+    wd = np.empty((K, N), np.float32)  # reused: the timed loop pays no page faults
     reps, t0 = 0, time.perf_counter()
     while True:
-        O.matmul_f32(a, O.dequant_q4s(q, K, N))
+        O.matmul_f32(a, O.dequant_q4s(q, K, N, wd))
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s and reps >= 2:
@@ -295,18 +296,65 @@ def cpu_baseline(K, N, budget_s):
                       "%.1f ms/call; host has %d cpus" % (reps, el, per * 1e3, os.cpu_count() or 0)}
 
 
-def cpu_baseline_e2e(reps=2):
-    """Config-5 decode on the CPU, the reference's path (weights dequantized to
-    f32 at load, gguf_loader.js:236; f32 GEMVs per token), 1 thread: one
-    layer's seven projections and the LM head timed with the oracle's f32
-    matmul, extrapolated to 32 layers (attention, norms and the sampler are
-    left out: < 1% of the work)."""
+def cpu_baseline_q8(K, N, budget_s):
+    """Config 2 on the CPU: the oracle's Q8 dequantize + f32 matmul (the
+    reference's CPU semantics), 1 thread."""
     from oracle import oracle as O
     from smith_amd import prng
-    c = dict(dim=3072, kv=1024, ffn=9216, vocab=32000, layers=32)
+    w = prng.randn((K, N), 1, std=0.02)
+    a = prng.randn((1, K), 0)
+    q = O.quantize_q8(w)
+    del w
+    wd = np.empty((K, N), np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.matmul_f32(a, O.dequant_q8(q, K, N, wd))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and reps >= 2:
+            break
+    per = el / reps
+    return {"value": round(alg_bytes(q8_bytes(K, N), 1, K, N) / per / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": "%d x [oracle_dequant_q8 + oracle_matmul_f32] on config 2 (M=1, K=4096, N=14336), %.1f s, "
+                      "%.1f ms/call" % (reps, el, per * 1e3)}
+
+
+def cpu_baseline_gemm(K, N, rows=8):
+    """Config 4 on the CPU: the oracle's Q4S dequantize + f32 matmul of a
+    sample of `rows` activation rows (the f32 loop is linear in M, so the
+    rate holds for M = 512 / 2048), 1 thread."""
+    from oracle import oracle as O
+    from smith_amd import prng
+    w = prng.randn((K, N), 3, std=0.02)
+    q = O.quantize_q4s(w)
+    del w
+    a = prng.randn((rows, K), 20)
+    wd = np.empty((K, N), np.float32)
+    wd.fill(0.0)  # pages touched before the timed call
+    t0 = time.perf_counter()
+    O.matmul_f32(a, O.dequant_q4s(q, K, N, wd))
+    el = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * K * N / el / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": "oracle_dequant_q4s + oracle_matmul_f32 of %d rows of config 4 (K=%d, N=%d) in %.1f s, "
+                      "rate taken as the M = 512 / 2048 rate" % (rows, K, N, el)}
+
+
+def cpu_baseline_e2e(reps=2, pos=192):
+    """Config-5 decode on the CPU, the reference's path (weights dequantized
+    to f32 at load, gguf_loader.js:236; f32 GEMVs per token), 1 thread: one
+    layer timed piece by piece -- the seven projections with the oracle's
+    f32 matmul, the two RMSNorms, the whole-row RoPE of q and k, 24 heads
+    of attention over `pos` cached keys (the middle of the 128 generated
+    tokens), SwiGLU and the residuals (oracle/llama_oracle.py) -- times 32,
+    plus the LM head; extrapolated from that one layer."""
+    from oracle import llama_oracle as LO
+    from oracle import oracle as O
+    from smith_amd import prng
+    c = dict(dim=3072, kv=1024, ffn=9216, vocab=32000, layers=32, heads=24, kvh=8, hd=128)
     shapes = [(c["dim"], c["dim"]), (c["dim"], c["kv"]), (c["dim"], c["kv"]), (c["dim"], c["dim"]),
               (c["dim"], c["ffn"]), (c["dim"], c["ffn"]), (c["ffn"], c["dim"])]
-    t_layer = 0.0
+    t_proj = 0.0
     for i, (K, N) in enumerate(shapes):
         w = prng.randn((K, N), 100 + i, std=0.02)
         a = prng.randn((1, K), 0)
@@ -316,17 +364,47 @@ def cpu_baseline_e2e(reps=2):
             O.matmul_f32(a, w)
             el = time.perf_counter() - t0
             best = el if best is None else min(best, el)
-        t_layer += best
+        t_proj += best
         del w
+    # the rest of a layer at position pos, on float64 host vectors
+    x = prng.randn((1, c["dim"]), 1).astype(np.float64)
+    g = np.ones(c["dim"])
+    # whole-row RoPE reads table entry pos * (dim / 2) + i
+    cos, sin = LO.precompute_rope(c["hd"], (pos + 1) * c["dim"] // c["hd"] + 1, 10000.0)
+    Kc = prng.randn((c["kvh"], pos, c["hd"]), 2).astype(np.float64)
+    Vc = prng.randn((c["kvh"], pos, c["hd"]), 3).astype(np.float64)
+    q = prng.randn((1, c["dim"]), 4).astype(np.float64)
+    k = prng.randn((1, c["kv"]), 5).astype(np.float64)
+    gu = prng.randn((2, c["ffn"]), 6).astype(np.float64)
+    best = None
+    for _ in range(max(reps, 3)):
+        t0 = time.perf_counter()
+        n1 = LO.rmsnorm(x, g, 1e-5)
+        LO.rope_rows(q, pos, cos, sin)
+        LO.rope_rows(k, pos, cos, sin)
+        att = np.empty(c["dim"])
+        for h in range(c["heads"]):
+            kv = h // (c["heads"] // c["kvh"])
+            att[h * c["hd"]:(h + 1) * c["hd"]] = LO.attend(q[0, h * c["hd"]:(h + 1) * c["hd"]], Kc[kv], Vc[kv],
+                                                           1.0 / np.sqrt(c["hd"]))
+        x2 = x + n1
+        LO.rmsnorm(x2, g, 1e-5)
+        h_ = LO.swiglu(gu[0], gu[1])
+        x2 + h_[:c["dim"]]
+        el = time.perf_counter() - t0
+        best = el if best is None else min(best, el)
+    t_rest = best
     w = prng.randn((c["dim"], c["vocab"]), 200, std=0.02)
     t0 = time.perf_counter()
     O.matmul_f32(prng.randn((1, c["dim"]), 0), w)
     t_head = time.perf_counter() - t0
     del w
-    per_token = c["layers"] * t_layer + t_head
+    per_token = c["layers"] * (t_proj + t_rest) + t_head
     return {"value": round(1.0 / per_token, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": "oracle f32 GEMVs of one config-5 layer (%.1f ms) x 32 + LM head (%.1f ms), best of %d; "
-                      "extrapolated, attention/norms omitted" % (t_layer * 1e3, t_head * 1e3, reps)}
+            "sample": "one config-5 layer on the CPU: oracle f32 GEMVs of its seven projections (%.1f ms, best of "
+                      "%d) + RMSNorms, whole-row RoPE, 24-head attention over %d cached keys, SwiGLU, residuals "
+                      "(%.2f ms), x 32 layers, + the LM head (%.1f ms); extrapolated from one layer"
+                      % (t_proj * 1e3, reps, pos, t_rest * 1e3, t_head * 1e3)}
 
 
 _FLOOR_LIB = None
@@ -635,6 +713,10 @@ def main():
     if not args.quick:
         cpu = cpu_baseline(K, N, args.cpu_seconds)
         log("cpu baseline:", cpu)
+        configs["cfg2_q8_gemv_M1_K4096_N14336"]["cpu_baseline"] = cpu_baseline_q8(4096, 14336, args.cpu_seconds / 2)
+        log("cfg2 cpu baseline:", configs["cfg2_q8_gemv_M1_K4096_N14336"]["cpu_baseline"])
+        configs["cfg4_q4s_prefill"]["cpu_baseline"] = cpu_baseline_gemm(4096, 14336)
+        log("cfg4 cpu baseline:", configs["cfg4_q4s_prefill"]["cpu_baseline"])
         e2e = bench_e2e(D, args.gguf)
         e2e["cpu_baseline"] = cpu_baseline_e2e()
         e2e["bound_tok_s_at_hbm_peak"] = round(HBM_PEAK_GBS * 1e9 / (1981808640 + 55296000), 1)

@@ -94,6 +94,14 @@ def f32_to_f16_rne(x):
     return lib().oracle_f32_to_f16_rne(float(x))
 
 
+def _out_f32(out, K, N):
+    if out is None:
+        return np.empty((K, N), dtype=np.float32)
+    if out.dtype != np.float32 or out.shape != (K, N) or not out.flags.c_contiguous:
+        raise ValueError("out must be a C-contiguous float32 [%d, %d] array" % (K, N))
+    return out
+
+
 def quantize_q4s(w):
     """quantizeQ4, src/ops/quantize.js:14-68 -> Q4S bytes."""
     w = _f32(w)
@@ -104,10 +112,11 @@ def quantize_q4s(w):
     return out
 
 
-def dequant_q4s(q, K, N):
-    """dequant_q4, shaders/matmul_q4.metal:24-28 -> f32 [K,N]."""
+def dequant_q4s(q, K, N, out=None):
+    """dequant_q4, shaders/matmul_q4.metal:24-28 -> f32 [K,N] (into `out`
+    when given: a reused C-contiguous f32 [K,N] array)."""
     q = np.ascontiguousarray(q, dtype=np.uint8)
-    w = np.empty((K, N), dtype=np.float32)
+    w = _out_f32(out, K, N)
     lib().oracle_dequant_q4s(_p(q), K, N, _p(w))
     return w
 
@@ -122,10 +131,10 @@ def quantize_q8(w):
     return out
 
 
-def dequant_q8(q, K, N):
-    """shaders/matmul_q8.metal:44-52 -> f32 [K,N]."""
+def dequant_q8(q, K, N, out=None):
+    """shaders/matmul_q8.metal:44-52 -> f32 [K,N] (into `out` when given)."""
     q = np.ascontiguousarray(q, dtype=np.uint8)
-    w = np.empty((K, N), dtype=np.float32)
+    w = _out_f32(out, K, N)
     lib().oracle_dequant_q8(_p(q), K, N, _p(w))
     return w
 

@@ -214,16 +214,18 @@ void oracle_quantize_q8(const float* w, int64_t K, int64_t N, uint8_t* out) {
 /* matmul_q8 dequant, shaders/matmul_q8.metal:44-52: float(half scale) *
  * float(int8), in f32. */
 void oracle_dequant_q8(const uint8_t* q, int64_t K, int64_t N, float* w) {
-  for (int64_t k = 0; k < K; k++) {
-    int64_t g = k / 32, kk = k % 32;
-    for (int64_t col = 0; col < N; col++) {
+  const int64_t G = (K + 31) / 32;
+  float* sc = (float*)malloc((size_t)N * sizeof(float));
+  for (int64_t g = 0; g < G; g++) {
+    for (int64_t col = 0; col < N; col++) { /* each block's scale once */
       const uint8_t* blk = q + (g * N + col) * Q8_BYTES;
-      uint16_t h = (uint16_t)(blk[0] | (blk[1] << 8));
-      float s = (float)oracle_from_f16(h);
-      int8_t v = (int8_t)blk[2 + kk];
-      w[k * N + col] = s * (float)v;
+      sc[col] = (float)oracle_from_f16((uint16_t)(blk[0] | (blk[1] << 8)));
     }
+    for (int64_t kk = 0; kk < 32 && g * 32 + kk < K; kk++)
+      for (int64_t col = 0; col < N; col++)
+        w[(g * 32 + kk) * N + col] = sc[col] * (float)(int8_t)q[(g * N + col) * Q8_BYTES + 2 + kk];
   }
+  free(sc);
 }
 
 /* ---------- GGUF Q4_0 / Q8_0 blocks ---------- */
