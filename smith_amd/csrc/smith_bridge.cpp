@@ -204,6 +204,17 @@ int launch(Ctx* c, const char* name, dim3 grid, dim3 block, void** args, unsigne
   return 0;
 }
 
+// Zero fresh device memory on the context's stream and wait for it.  A plain
+// hipMemset runs on the null stream, which the context's non-blocking stream
+// is not ordered after: a kernel enqueued next could read the counters
+// before they are zero, and a counter that never reaches its "last arrival"
+// value is never reset by the kernels, so every later call would go wrong.
+int zero_now(Ctx* c, void* p, size_t bytes) {
+  HIPCHK(c, hipMemsetAsync(p, 0, bytes, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return 0;
+}
+
 // Grow-only device scratch owned by the context.  Growing waits for the
 // stream so no enqueued kernel still uses the old allocation.
 int ensure(Ctx* c, void** p, size_t* have, size_t need) {
@@ -253,7 +264,7 @@ int ensure_counters(Ctx* c, size_t n) {
   HIPCHK(c, hipMalloc((void**)&c->counters, cap * sizeof(uint32_t)));
   c->allocated += cap * sizeof(uint32_t);
   // counters start at zero once; the kernel's last workgroup resets its own
-  HIPCHK(c, hipMemset(c->counters, 0, cap * sizeof(uint32_t)));
+  if (zero_now(c, c->counters, cap * sizeof(uint32_t))) return -1;
   c->counters_n = cap;
   return 0;
 }
@@ -263,7 +274,7 @@ int ensure_amx(Ctx* c) {
   if (c->capturing) return fail(c, "smith: greedy LM head state needed while capturing a graph; run the op once first");
   HIPCHK(c, hipMalloc((void**)&c->amx, 2 * sizeof(uint64_t)));
   c->allocated += 2 * sizeof(uint64_t);
-  HIPCHK(c, hipMemset(c->amx, 0, 2 * sizeof(uint64_t)));
+  if (zero_now(c, c->amx, 2 * sizeof(uint64_t))) return -1;
   return 0;
 }
 
@@ -1613,7 +1624,7 @@ int smith_attention(void* ctx, const float* qkv, uint32_t ld, const int32_t* pos
     size_t cap = std::max<size_t>(slots, 4096);
     HIPCHK(c, hipMalloc((void**)&c->att_cnt, cap * sizeof(uint32_t)));
     c->allocated += cap * sizeof(uint32_t);
-    HIPCHK(c, hipMemset(c->att_cnt, 0, cap * sizeof(uint32_t)));
+    if (zero_now(c, c->att_cnt, cap * sizeof(uint32_t))) return -1;
     c->att_cnt_n = cap;
   }
   void* pws = c->att_ws;

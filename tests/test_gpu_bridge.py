@@ -156,3 +156,62 @@ def test_dispatch_sync_one_shot():
 def test_compile_source_error_is_reported():
     with pytest.raises(RuntimeError, match="shader compilation failed"):
         device.compile_source('extern "C" __global__ void broken(float* o) { o[0] = undefined_name; }')
+
+
+def _fresh_ctx():
+    c = device.lib.smith_init()
+    assert c
+    for path in (device.CODE_OBJECT_PATH, device.LLAMA_CODE_OBJECT_PATH, device.GEMM_CODE_OBJECT_PATH):
+        assert device.lib.smith_load_library(c, path.encode()), device.lib.smith_last_error(c)
+    return c
+
+
+def test_first_split_k_calls_on_a_fresh_context():
+    """The split-K counters a context allocates on first use are zeroed on
+    its own stream before the first kernel reads them (zeroed on the null
+    stream, which the context's stream is not ordered after, the first
+    Q6_K LM head of a fresh process returned garbage, and the counters it
+    left behind broke every later call).  On a new context the very first
+    split-K launches -- a Q6_K LM head (12 K splits) on one context, a
+    single-row GEMV split across blocks (K = 14336) on another -- match the
+    oracle."""
+    from oracle import oracle as O
+    lib = device.lib
+    K, N = 3072, 4096
+    w = prng.randn((K, N), 71, std=0.02)
+    x = prng.randn((K,), 72)
+    c = _fresh_ctx()
+    try:
+        blocks = O.quantize_rows(O.GGML_Q6_K, w)
+        wd = O.dequantize_tensor(O.GGML_Q6_K, blocks, K * N).reshape(K, N).astype(np.float64)
+        src = device.alloc(blocks.nbytes)
+        device.upload(src, blocks)
+        planes = device.alloc(int(lib.smith_lmhead_q6_k_bytes(K, N)))
+        xb, yb = device.alloc(K * 4), device.alloc(N * 4)
+        device.upload(xb, x.astype(np.float32))
+        assert lib.smith_repack_lmhead_q6_k(c, src, planes, K, N) == 0
+        assert lib.smith_lmhead_q6_k_nb(c, xb, None, 0.0, planes, yb, K, N) == 0
+        assert lib.smith_sync(c) == 0
+        y = device.download(yb, N * 4, np.float32)
+        assert O.normwise_rel_err(y, x.astype(np.float64) @ wd) <= 2e-6
+        for b in (src, planes, xb, yb):
+            device.release_buffer(b)
+    finally:
+        lib.smith_destroy(c)
+    c = _fresh_ctx()
+    try:
+        Kg, Ng = 14336, 4096
+        wg = prng.randn((Kg, Ng), 73, std=0.02)
+        a = prng.randn((1, Kg), 74)
+        q = O.quantize_q4s(wg)
+        qb, ab, ob = device.alloc(q.nbytes), device.alloc(a.nbytes), device.alloc(Ng * 4)
+        device.upload(qb, q)
+        device.upload(ab, a)
+        assert lib.smith_matmul_q4(c, ab, qb, ob, 1, Ng, Kg, Kg // 32) == 0
+        assert lib.smith_sync(c) == 0
+        y = device.download(ob, Ng * 4, np.float32)
+        assert O.normwise_rel_err(y, O.matmul_q4s(a, q, Kg, Ng)) <= 2e-5
+        for b in (qb, ab, ob):
+            device.release_buffer(b)
+    finally:
+        lib.smith_destroy(c)
