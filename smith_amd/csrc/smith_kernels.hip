@@ -1859,14 +1859,13 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
     // partials made up 40 % of the block's load data: the workgroup's loads
     // return at ~155 GB/s, which bounds this kernel)
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void*)parts, 0, 0x7FFFFFFF, RSRC_WORD3);
-    {  // (m, l) of head h0 + threadIdx.x; splits past nsplit were not written
-       // for this position and are not read (out-of-range offsets)
+    {  // (m, l) of head h0 + threadIdx.x (all splits: offsets that waited for the
+       // position's split count would put a memory round trip before these loads)
       const bool live = h0 + threadIdx.x < hend;
 #pragma unroll
       for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
-        const uint32_t off = live && (uint32_t)zz < nsplit
-                                 ? (uint32_t)((((h0 + threadIdx.x) * ATTP_MAXSPLIT + zz) * ATTP_STRIDE) * 4)
-                                 : 0x80000000u;
+        const uint32_t off =
+            live ? (uint32_t)((((h0 + threadIdx.x) * ATTP_MAXSPLIT + zz) * ATTP_STRIDE) * 4) : 0x80000000u;
         const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(prs, off, 0, 0));
         mlv[2 * zz] = ml.x;
         mlv[2 * zz + 1] = ml.y;
@@ -1879,9 +1878,7 @@ __device__ __forceinline__ void agemv_body(const uint8_t* __restrict__ act, cons
       const uint32_t e0 = 8 * pi, hh = e0 / hd, d0 = e0 % hd;
 #pragma unroll
       for (int zz = 0; zz < ATTP_MAXSPLIT; zz++) {
-        const uint32_t off = live && (uint32_t)zz < nsplit
-                                 ? (uint32_t)(((hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE + 4 + d0) * 4)
-                                 : 0x80000000u;
+        const uint32_t off = live ? (uint32_t)(((hh * ATTP_MAXSPLIT + zz) * ATTP_STRIDE + 4 + d0) * 4) : 0x80000000u;
         oa[q][zz] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 0));
         ob[q][zz] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, 0));
       }
