@@ -488,32 +488,62 @@ def read_floor(D, S, prng, K, N, steps):
     return {k: round(v, 3) for k, v in res.items()}
 
 
+def stream_floor_us(D, nbytes, steps=100):
+    """Per-launch us of a plain 16-byte streaming read of `nbytes` (the
+    fastest grid shape found, floor_block_read), graph-replayed over copies
+    rotated past the MALL: what any kernel reading that many weight bytes
+    takes on this GPU, whatever its grid."""
+    out = D.alloc(256)
+    D.check(D.lib.smith_fill_zero(D.ctx(), out, 256))
+    nbytes = -(-nbytes // 16) * 16
+    bufs = [D.alloc(nbytes) for _ in range(max(2, -(-ROTATE_BYTES // nbytes)))]
+    for b in bufs:
+        D.check(D.lib.smith_fill_zero(D.ctx(), b, nbytes))
+    D.sync()
+    n16 = nbytes // 16
+    us = floor_us("floor_block_read", bufs, n16, out, (n16 + 767) // 768, 128, steps)
+    D.sync()
+    for b in bufs:
+        D.release_buffer(b)
+    D.release_buffer(out)
+    return round(us, 3)
+
+
+def _sweep_point(ms, nbytes, launches, floor):
+    us = ms * 1e3
+    return {"GBps": round(nbytes / ms / 1e6, 1), "pct_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 2),
+            "us_step": round(us, 2), "kernels_per_step": launches, "stream_read_us": floor,
+            "over_stream_read": round(us / floor, 3) if floor == floor else None}
+
+
 def bench_sweeps(D, S, prng):
     """Config 2 and the config-3 sweeps (Q4S records and GGUF Q4_0 blocks),
-    each point graph-replayed."""
+    each point graph-replayed, with the streaming-read floor of its weight
+    bytes (stream_read_us; over_stream_read = step / floor)."""
+    eager = os.environ.get("SMITH_BENCH_EAGER") == "1"  # traced runs: no floor graphs
+    floor = (lambda nbytes: float("nan")) if eager else (lambda nbytes: stream_floor_us(D, nbytes))
     configs = {}
     sub = 100  # sweep points: enough graph-replayed steps to amortise the graph launch
     ms8, kt8, b8 = bench_q8(D, S, prng, 1, 4096, 14336, sub, 5, graph=True)
-    configs["cfg2_q8_gemv_M1_K4096_N14336"] = {
-        "GBps": round(b8 / ms8 / 1e6, 1), "pct_hbm_peak": round(b8 / ms8 / 1e6 / HBM_PEAK_GBS * 100, 2),
-        "us_step": round(ms8 * 1e3, 2), "kernels_per_step": kt8["launches_per_step"]}
+    configs["cfg2_q8_gemv_M1_K4096_N14336"] = _sweep_point(ms8, b8, kt8["launches_per_step"],
+                                                           floor(q8_bytes(4096, 14336)))
     log("cfg2:", configs["cfg2_q8_gemv_M1_K4096_N14336"])
     sweep = {}
     for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
         for M in (1, 4, 8, 16, 32):
+            if M == 1:
+                fl = floor(q4s_bytes(Kk, Nn))
             msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, sub, 5, graph=True)
-            sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = {
-                "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
-                "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
+            sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = _sweep_point(msx, bx, ktx["launches_per_step"], fl)
     configs["cfg3_q4s_batched_decode"] = sweep
     log("cfg3:", json.dumps(sweep))
     sweep40 = {}  # the same sweep on GGUF Q4_0 blocks (18 B per 32 weights, tile-major planes)
     for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
         for M in (1, 4, 8, 16, 32):
+            if M == 1:
+                fl = floor(q40_bytes(Kk, Nn))
             msx, ktx, bx = bench_q40(D, S, prng, M, Kk, Nn, sub, 5, graph=True)
-            sweep40["M%d_N%d_K%d" % (M, Nn, Kk)] = {
-                "GBps": round(bx / msx / 1e6, 1), "pct_hbm_peak": round(bx / msx / 1e6 / HBM_PEAK_GBS * 100, 2),
-                "us_step": round(msx * 1e3, 2), "kernels_per_step": ktx["launches_per_step"]}
+            sweep40["M%d_N%d_K%d" % (M, Nn, Kk)] = _sweep_point(msx, bx, ktx["launches_per_step"], fl)
     configs["cfg3_q4_0_batched_decode"] = sweep40
     log("cfg3 q4_0:", json.dumps(sweep40))
     return configs

@@ -653,13 +653,12 @@ int qmatmul(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, float
       const char* e = getenv("SMITH_QGEMV");
       return e ? atoi(e) : 0;
     }();
-    // the one-launch kernels read the activations in 32-element groups.
-    // Past 16 rows every workgroup of the one-launch kernel converts 32
-    // activation rows of its K range: worth it while one round of
-    // workgroups covers the matrix, else the activations are prepared once
-    // (smith_qprep_*) for smith_qgemv3_*
-    const uint64_t rounds32 = (uint64_t)((N + 15) / 16 < 128 ? (N + 15) / 16 : (N + 63) / 64) * ((G + 31) / 32);
-    const bool v3 = K % 32 != 0 || vq == 3 || (vq == 0 && mc > 16 && rounds32 > 256);
+    // the one-launch kernels read the activations in 32-element groups
+    // (K % 32 != 0 prepares them once, smith_qprep_*, for smith_qgemv3_*).
+    // At 32 rows the one-launch kernel also wins on the wide shapes once its
+    // 64-column blocks fit two per CU (14336 x 4096 Q4S: 27.0 us for prep +
+    // qgemv3 -> 23.8 us; 4096 x 14336: 29.4 -> 27.4 us)
+    const bool v3 = K % 32 != 0 || vq == 3;
     const bool v5 = !v3 && vq != 4;
     int rc = mc <= 2 ? qgemv1_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)
                      : (v3 ? qgemv3_chunk(c, fmt, am, B, D, om, mc, N, K, G, e)

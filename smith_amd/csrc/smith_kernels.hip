@@ -1513,10 +1513,14 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   constexpr int IPT = (NITEM + 63) / 64;
   __shared__ u32x4 fragL[KB][4][VR];
   // when the fragments and a separate reduction array would not fit the
-  // LDS (16 waves x 32 rows), the reduction reuses the fragments after a
-  // block barrier
-  constexpr bool ALIAS = sizeof(fragL) + sizeof(float) * WK * 16 * RB * BC > 150 * 1024;
-  static_assert(!ALIAS || sizeof(fragL) >= sizeof(float) * WK * 16 * RB * BC, "reduction fits the fragments");
+  // LDS (16 waves x 32 rows), or would keep a second workgroup off the CU
+  // while the fragments alone leave room for it (8 waves x 32 rows: 80 /
+  // 128 -> 64 KB at 16 / 64 columns), the reduction reuses the fragments
+  // after a block barrier
+  constexpr size_t RED_BYTES = sizeof(float) * WK * 16 * RB * BC;
+  constexpr bool ALIAS = sizeof(fragL) + RED_BYTES > 150 * 1024 ||
+                         (sizeof(fragL) + RED_BYTES >= 80 * 1024 && sizeof(fragL) <= 72 * 1024);
+  static_assert(!ALIAS || sizeof(fragL) >= RED_BYTES, "reduction fits the fragments");
   __shared__ float red_own[ALIAS ? 1 : WK][ALIAS ? 1 : 16 * RB][BC];
   float(*red)[16 * RB][BC] = ALIAS ? (float(*)[16 * RB][BC])(void*)fragL : (float(*)[16 * RB][BC])red_own;
   __shared__ int s_last;
