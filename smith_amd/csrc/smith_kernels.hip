@@ -1483,16 +1483,16 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
 //   fragL[group][kslice][vrow], vrow = m (hi or plain) or MR + m (lo).
 // The record operands have their exponent-bias offsets subtracted in f16
 // (exact), so the MFMA yields sum(a * q); the per-(group, row) sums S =
-// sum(a) for the zero term come from one more MFMA per group against a
-// constant B operand (column 0 ones), read by every lane with a row
-// broadcast (DPP row_newbcast).  The conversion is only the f16 rounding
-// (v_cvt_pk_f16_f32, and one fused multiply-add per element for the lo
-// half).
+// sum(a) of the f16 operand values for the zero term: for the hi/lo rows
+// (M <= 8) formed during the conversion (v_dot2_f32_f16 against ones over a
+// lane's 8 values, then the lane quad of the row's four K slices by DPP) and
+// kept in LDS, where each lane reads the four of its output rows with one
+// broadcast load; for plain rows from one more MFMA per group against a
+// ones column, read by every lane with a DPP row broadcast.  The conversion
+// is the f16 rounding (v_cvt_pk_f16_f32, and one fused multiply-add per
+// element for the lo half) and those sums.
 // Grid: x = column blocks of 16*CT, y = K splits of 4*S*WK groups.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float row_bcast0(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150, 0xF, 0xF, false));
-}
 
 template <int FMT, int MR, bool HILO, int CT, int S, int WK>
 __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const uint8_t* __restrict__ B,
@@ -1509,9 +1509,18 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   static_assert(!HILO || RB == 1, "hi/lo rows fit one row block");
   static_assert(RB <= 2, "at most two row blocks");
   constexpr int VR = HILO ? 2 * MR : MR;   // live virtual rows
+  constexpr bool NEED_S = FMT != FMT_Q8;  // Q4S: - zero * S, Q4_0: - 8 * S
+  // hi/lo rows: S formed during the conversion and kept in LDS; plain rows:
+  // S from one more MFMA per group against a ones column (same-box A/B: the
+  // LDS sums took M = 4 from 6.31 to 5.99 us at 4096 x 4096, but made the
+  // plain M = 16 / 32 buckets, with 2-4x the conversion work, 2-6 % slower)
+  constexpr bool SUM_LDS = NEED_S && HILO;
   constexpr int NITEM = GPW * MR * 4;      // prep items of a wave (group, row, kslice), kslice fastest
   constexpr int IPT = (NITEM + 63) / 64;
   __shared__ u32x4 fragL[KB][4][VR];
+  // per (group, MFMA row) sum of the f16 operand values of that row (the S of
+  // the zero term, hi/lo buckets): hi row m at m, lo row m at 8 + m
+  __shared__ __attribute__((aligned(16))) float sL[HILO ? KB : 1][16 * RB];
   // when the fragments and a separate reduction array would not fit the
   // LDS (16 waves x 32 rows), or would keep a second workgroup off the CU
   // while the fragments alone leave room for it (8 waves x 32 rows: 80 /
@@ -1575,6 +1584,8 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
       const uint32_t item = lane + it * 64;
       const uint32_t kq = item & 3, m = (item >> 2) % MR, gl = wk * GPW + (item >> 2) / MR;
       u32x4 hp, lp;
+      const half2_t one2 = {(_Float16)1, (_Float16)1};
+      float sh = 0.f, sl = 0.f;  // sums of the f16 values (v_dot2_f32_f16 against ones)
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int e0 = FMT == FMT_Q8 ? perm_q8[2 * q] : perm_q4[2 * q];
@@ -1582,15 +1593,26 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
         const float a0 = alive[it] ? av[it][e0] : 0.f, a1 = alive[it] ? av[it][e1] : 0.f;
         const half2_t h = __builtin_convertvector((float2_t){a0, a1}, half2_t);
         hp[q] = __builtin_bit_cast(uint32_t, h);
+        sh = __builtin_amdgcn_fdot2(h, one2, sh, false);
         if (HILO) {
           const float l0 = __builtin_fmaf((float)h[0], -2048.0f, a0 * 2048.0f);
           const float l1 = __builtin_fmaf((float)h[1], -2048.0f, a1 * 2048.0f);
-          lp[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){l0, l1}, half2_t));
+          const half2_t lh = __builtin_convertvector((float2_t){l0, l1}, half2_t);
+          lp[q] = __builtin_bit_cast(uint32_t, lh);
+          sl = __builtin_amdgcn_fdot2(lh, one2, sl, false);
         }
+      }
+      if (SUM_LDS) {  // the four K slices of (group, row) sit in one lane quad
+        sh = add_xor2(add_xor1(sh));
+        if (HILO) sl = add_xor2(add_xor1(sl));
       }
       if (item < (uint32_t)NITEM) {
         fragL[gl][kq][m] = hp;
         if (HILO) fragL[gl][kq][MR + m] = lp;
+        if (SUM_LDS && kq == 0) {
+          sL[gl][m] = sh;
+          if (HILO) sL[gl][8 + m] = sl;
+        }
       }
     }
   }
@@ -1611,22 +1633,16 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
     a_live[rb] = 16 * rb + rm < (uint32_t)MR;
     avr[rb] = HILO && r >= 8 ? MR + rm : 16 * rb + rm;
   }
-  // B operand of the sums MFMA: column 0 ones (-> S per group and row), the
-  // other columns zero.  The record operands get their exponent-bias offset
-  // (1024 / 64 per nibble slot, 1152 per int8) subtracted in f16 -- exact --
-  // so the MFMA sums a * q itself instead of a * (offset + q) with the
-  // offset part taken off afterwards in f32, which cancelled ~1e-5 of the
-  // result at K = 512
-  half8 bx, boff;
+  // The record operands get their exponent-bias offset (1024 / 64 per
+  // nibble slot, 1152 per int8) subtracted in f16 -- exact -- so the MFMA
+  // sums a * q itself instead of a * (offset + q) with the offset part taken
+  // off afterwards in f32, which cancelled ~1e-5 of the result at K = 512
+  half8 boff;
   {
     const _Float16 off_q4[8] = {1024, 1024, 64, 64, 1024, 1024, 64, 64};
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      bx[e] = c == 0 ? (_Float16)1 : (_Float16)0;
-      boff[e] = FMT == FMT_Q8 ? (_Float16)1152 : off_q4[e];
-    }
+    for (int e = 0; e < 8; e++) boff[e] = FMT == FMT_Q8 ? (_Float16)1152 : off_q4[e];
   }
-  constexpr bool NEED_S = FMT != FMT_Q8;  // Q4S: - zero * S, Q4_0: - 8 * S
   f32x4 acc[CT][RB];
 #pragma unroll
   for (int ct = 0; ct < CT; ct++)
@@ -1644,10 +1660,20 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
         u32x4 f = (u32x4){0u, 0u, 0u, 0u};
         if (a_live[rb]) f = fragL[gl0 + t][j][avr[rb]];
         af[t][rb] = __builtin_bit_cast(half8, f);
-        if (NEED_S) {
+        if (SUM_LDS) {  // S of the lane's output rows 4j .. 4j+3 (same-address reads broadcast)
+          const float4 s4 = *(const float4*)&sL[gl0 + t][16 * rb + 4 * j];
+          sv4[t][rb][0] = s4.x;
+          sv4[t][rb][1] = s4.y;
+          sv4[t][rb][2] = s4.z;
+          sv4[t][rb][3] = s4.w;
+        } else if (NEED_S) {
+          half8 bx;
+#pragma unroll
+          for (int e = 0; e < 8; e++) bx[e] = c == 0 ? (_Float16)1 : (_Float16)0;
           const f32x4 pe = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bx, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; i++) sv4[t][rb][i] = row_bcast0(pe[i]);
+          for (int i = 0; i < 4; i++)
+            sv4[t][rb][i] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(pe[i]), 0x150, 0xF, 0xF, false));
         }
       }
 #pragma unroll
