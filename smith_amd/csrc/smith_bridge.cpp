@@ -301,8 +301,8 @@ const char* fmt_tag(Fmt f) {
   return tags[f];
 }
 
-// M > 2: prepare the activations once (smith_qprep_*), then the 16-row
-// MFMA GEMV (smith_qgemv3_*).  Buckets must match DEF_QGEMV3_FMT.
+// M > 2 with K % 32 != 0: prepare the activations once (smith_qprep_*), then
+// the 16-row MFMA GEMV (smith_qgemv3_*).  Buckets must match DEF_QGEMV3_FMT.
 struct Epi {
   const float* gamma = nullptr;  // RMSNorm of the activation rows first
   float eps = 0.f;

@@ -29,7 +29,7 @@
 //   smith_qgemv1_*  M <= 2: activation prep fused (LDS), one kernel per call
 //   smith_qgemv5_*  2 < M <= 32: per-wave activation prep, one launch
 //   smith_qgemv3_*  2 < M <= 32: activations prepared once by smith_qprep_*
-//                   (M > 16 on the widest shapes, K % 32 != 0)
+//                   (K % 32 != 0)
 //   smith_qgemv4_*  2 < M <= 32: workgroup-shared prep (comparison path)
 //   smith_agemv_*   M == 1 on an act (act_frag.h) its producer wrote
 // Q4_0 weights for the decode path use tile-major planes (FMT_Q40T): the 16
