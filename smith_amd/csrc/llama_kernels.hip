@@ -634,7 +634,7 @@ DEF_ATT_PREFILL(8)
 struct AttPShared {
   float qr[128] __attribute__((aligned(16)));
   float Kt[ATTP_ROWS][132] __attribute__((aligned(16)));  // 16-byte rows: 4-float reads
-  float Vt[ATTP_ROWS][128] __attribute__((aligned(16)));
+  float Vt[ATTP_ROWS][132] __attribute__((aligned(16)));  // padded: rows 2rr, 2rr+1 of a column in other banks
   float sc[ATTP_ROWS] __attribute__((aligned(16)));
 };
 
@@ -645,8 +645,6 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t maxSeq, float* __restrict__ parts,
     uint32_t rope_len, uint32_t* __restrict__ err) {
   __shared__ AttPShared sh;
-  __shared__ float kn[128], vn[128];
-  __shared__ float ored[2][128];
   const uint32_t rep = nH / nKV;
   const uint32_t kvh = blockIdx.x % nKV, h = kvh * rep + blockIdx.x / nKV, z = blockIdx.y;
   const uint32_t tid = threadIdx.x, c4n = hd / 4;
@@ -695,11 +693,11 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     ck = cosT[(size_t)p0 * hk + pk];
     sk = sinT[(size_t)p0 * hk + pk];
   }
+  // this token's roped key element tid and value element tid stay in
+  // registers: their threads write them into tile row p0 themselves
+  const float kr = ik < hk ? k0 * ck - k1 * sk : k0 * sk + k1 * ck;
   if (tid < hd) {
     sh.qr[tid] = iq < hq ? q0 * cq - q1 * sq : q0 * sq + q1 * cq;
-    const float kr = ik < hk ? k0 * ck - k1 * sk : k0 * sk + k1 * ck;
-    kn[tid] = kr;
-    vn[tid] = vnew;
     if (h % rep == 0 && z == 0) {
       const size_t oo = ((size_t)kvh * maxSeq + p0) * hd + tid;
       kcache[oo] = kr;
@@ -707,10 +705,10 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     }
   }
 
-  // 3. the split's tiles
-  const uint32_t ee = tid % 128, part = tid / 128;
+  // 3. the split's tiles.  P.V lanes: column ee, rows of parity `part`;
+  //    the two parities of a column sit in adjacent lanes
+  const uint32_t ee = tid >> 1, part = tid & 1;
   float m = -__builtin_inff(), l = 0.f, o = 0.f;
-  __syncthreads();  // qr, kn, vn visible
   for (uint32_t tau = z; tau < ntile; tau += ATTP_MAXSPLIT) {
     const uint32_t tb = ATTP_ROWS * tau;
 #pragma unroll
@@ -720,15 +718,17 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
         const uint32_t t = tb + r;
         float4 kv = kreg[i], vv = vreg[i];
         if (t > p0) kv = vv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t == p0) {
-          kv = make_float4(kn[4 * c4], kn[4 * c4 + 1], kn[4 * c4 + 2], kn[4 * c4 + 3]);
-          vv = make_float4(vn[4 * c4], vn[4 * c4 + 1], vn[4 * c4 + 2], vn[4 * c4 + 3]);
+        if (t != p0) {  // row p0: written below by the threads holding its elements
+          *(float4*)&sh.Kt[r][4 * c4] = kv;
+          *(float4*)&sh.Vt[r][4 * c4] = vv;
         }
-        *(float4*)&sh.Kt[r][4 * c4] = kv;
-        *(float4*)&sh.Vt[r][4 * c4] = vv;
       }
     }
-    __syncthreads();
+    if (tid < hd && p0 >= tb && p0 < tb + ATTP_ROWS) {
+      sh.Kt[p0 - tb][tid] = kr;
+      sh.Vt[p0 - tb][tid] = vnew;
+    }
+    __syncthreads();  // the tile (and, first time, qr) visible
     if (tau + ATTP_MAXSPLIT < ntile) {  // the split's next tile in flight during this one
       const uint32_t tn = tb + ATTP_ROWS * ATTP_MAXSPLIT;
 #pragma unroll
@@ -744,6 +744,8 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
       // score of row r: lanes (r, sub) take elements 16 sub .. 16 sub + 15
       // (four 16-byte reads of q and of the key row, all issued together)
       const uint32_t r = tid / 8, sub = tid % 8, c0 = 16 * sub;
+      // (one wave per SIMD here, so instruction latency is exposed: four
+      // independent chains of four FMAs instead of one of sixteen)
       float d = 0.f;
       if (c0 < hd) {
         float4 qv[4], kv[4];
@@ -752,14 +754,18 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
           qv[i] = *(const float4*)&sh.qr[c0 + 4 * i];
           kv[i] = *(const float4*)&sh.Kt[r][c0 + 4 * i];
         }
+        float di[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 4; i++) {
+          di[i] = 0.f;
           if (c0 + 4 * i < hd) {  // hd % 4 == 0
-            d = __builtin_fmaf(qv[i].x, kv[i].x, d);
-            d = __builtin_fmaf(qv[i].y, kv[i].y, d);
-            d = __builtin_fmaf(qv[i].z, kv[i].z, d);
-            d = __builtin_fmaf(qv[i].w, kv[i].w, d);
+            di[i] = qv[i].x * kv[i].x;
+            di[i] = __builtin_fmaf(qv[i].y, kv[i].y, di[i]);
+            di[i] = __builtin_fmaf(qv[i].z, kv[i].z, di[i]);
+            di[i] = __builtin_fmaf(qv[i].w, kv[i].w, di[i]);
           }
+        }
+        d = (di[0] + di[1]) + (di[2] + di[3]);
       }
       d = sum8_lanes(d);
       if (sub == 0) sh.sc[r] = tb + r <= p0 ? d * scale : -__builtin_inff();
@@ -780,28 +786,50 @@ extern "C" __global__ __launch_bounds__(256) void smith_attention_part(
     float vv[ATTP_ROWS / 2];
 #pragma unroll
     for (int rr = 0; rr < ATTP_ROWS / 2; rr++) vv[rr] = sh.Vt[2 * rr + part][ec];
-    float tm = sv[0];
+    // the tile's max as a tree (exact in any order)
+    float mx[ATTP_ROWS / 2];
 #pragma unroll
-    for (int i = 1; i < ATTP_ROWS; i++) tm = sv[i] > tm ? sv[i] : tm;
+    for (int i = 0; i < ATTP_ROWS / 2; i++) mx[i] = sv[2 * i + 1] > sv[2 * i] ? sv[2 * i + 1] : sv[2 * i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) mx[i] = mx[i + 8] > mx[i] ? mx[i + 8] : mx[i];
+#pragma unroll
+    for (int i = 0; i < 4; i++) mx[i] = mx[i + 4] > mx[i] ? mx[i + 4] : mx[i];
+#pragma unroll
+    for (int i = 0; i < 2; i++) mx[i] = mx[i + 2] > mx[i] ? mx[i + 2] : mx[i];
+    const float tm = mx[1] > mx[0] ? mx[1] : mx[0];
     const float mn = tm > m ? tm : m;
     const float alpha = __expf(m - mn);  // first tile: m = -inf -> 0
-    float ps = 0.f, acc = 0.f;
+    // weights of this lane's parity only; the other parity's sum comes from
+    // lane ^ 1.  Two interleaved accumulation chains each.
+    // (the parity select on the bits: as `part ? a : b` the compiler turned
+    // it into a dynamically indexed read of the score array, in scratch)
+    const uint32_t pm = 0u - part;
+    float pe[ATTP_ROWS / 2];
 #pragma unroll
     for (int rr = 0; rr < ATTP_ROWS / 2; rr++) {
-      const float p0e = __expf(sv[2 * rr] - mn), p1e = __expf(sv[2 * rr + 1] - mn);  // masked rows: 0
-      ps += p0e;
-      ps += p1e;
-      acc = __builtin_fmaf(part ? p1e : p0e, vv[rr], acc);
+      const uint32_t bits = (__float_as_uint(sv[2 * rr]) & ~pm) | (__float_as_uint(sv[2 * rr + 1]) & pm);
+      pe[rr] = __expf(__uint_as_float(bits) - mn);  // masked rows: 0
     }
+    float psa = 0.f, psb = 0.f, acca = 0.f, accb = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < ATTP_ROWS / 2; rr += 2) {
+      psa += pe[rr];
+      psb += pe[rr + 1];
+      acca = __builtin_fmaf(pe[rr], vv[rr], acca);
+      accb = __builtin_fmaf(pe[rr + 1], vv[rr + 1], accb);
+    }
+    const float ps_own = psa + psb, acc = acca + accb;
+    const float ps_other = dpp_f32<0xB1>(ps_own);  // every lane active: no DPP under a branch
+    const float ps = part ? ps_other + ps_own : ps_own + ps_other;  // even + odd rows
     l = l * alpha + ps;
     o = o * alpha + acc;
     m = mn;
-    __syncthreads();
+    if (tau + ATTP_MAXSPLIT < ntile) __syncthreads();  // every lane done with the tile before the next
   }
-  if (ee < hd) ored[part][ee] = o;
-  __syncthreads();
+  // the even-row sum plus the odd-row sum of column ee (lane ^ 1)
+  const float o_odd = dpp_f32<0xB1>(o);
   float* pp = parts + ((size_t)h * ATTP_MAXSPLIT + z) * ATTP_STRIDE;
-  if (tid < hd) pp[4 + tid] = ored[0][tid] + ored[1][tid];
+  if (part == 0 && ee < hd) pp[4 + ee] = o + o_odd;
   if (tid == 0) {
     pp[0] = m;
     pp[1] = l;
