@@ -407,3 +407,50 @@ def test_decode_shapes_random_sweep():
             y = (S.matmulQ4 if name == "q4" else S.matmulQ8)(S.tensor(a), q).data
             e = err(y, a.astype(np.float64) @ dq.astype(np.float64))
             assert e <= tol_for(M, K), (case, name, M, K, N, e)
+
+
+def test_hilo_buckets_random_sweep():
+    """The 3 <= M <= 8 buckets of the one-launch batched GEMV (hi/lo
+    activations, the zero term's row sums formed during the conversion and
+    read from LDS) on seeded random shapes that reach each block variant
+    (whole-K 16-column blocks, 32-group K ranges over 16 or 64 columns,
+    ragged N, K % 32 == 0), on Q4S records and GGUF Q4_0 tile planes, with
+    activation rows of mixed magnitude and one all-zero row (its sums are
+    zero).  Bars as for configs 1-3 (normwise 2e-5, elementwise 1e-3)."""
+    rng = np.random.default_rng(2027)
+    ctx = device.ops_ctx()
+    for case in range(10):
+        M = int(rng.integers(3, 9))
+        K = int(rng.choice([32, 64, 96, 256, 1024, 4096]))
+        N = int(rng.choice([int(rng.integers(17, 700)), int(rng.integers(2000, 2600)), int(rng.integers(5200, 6000))]))
+        a = prng.randn((M, K), 3000 + case)
+        a[1] *= 64.0  # a row far from the others' magnitude
+        a[M - 1] = 0.0
+        # Q4S records, ragged N
+        w = prng.randn((K, N), 3100 + case, std=0.02)
+        q = S.quantizeQ4(w)
+        y = S.matmulQ4(S.tensor(a), q).data
+        ref = a.astype(np.float64) @ O.dequant_q4s(dev_bytes(q), K, N).astype(np.float64)
+        what = "hilo q4s case %d M=%d K=%d N=%d" % (case, M, K, N)
+        assert err(y, ref) <= TOL_HILO, what
+        assert elem(y, ref, what) <= ELEM_HILO, what
+        assert not y[M - 1].any(), what
+        # GGUF Q4_0 tile planes (the decode path's layout), N a multiple of 16
+        N16 = max(16, N // 16 * 16)
+        wq = prng.randn((N16, K), 3200 + case, std=0.02)  # GGUF listing [out, in]
+        blocks = O.quantize_rows(O.GGML_Q4_0, wq)
+        G = K // 32
+        src, nib, dsc = device.alloc(blocks.size), device.alloc(N16 * G * 16), device.alloc(N16 * G * 2)
+        device.upload(src, blocks)
+        device.check(device.lib.smith_repack_q4_0_t_into(ctx, src, nib, dsc, N16, K, 0, 1, N16))
+        at = S.tensor(a)
+        out = S.create([M, N16])
+        device.check(device.lib.smith_linear_q4_0_t(ctx, at.buffer, nib, dsc, out.buffer, M, N16, K, None, 0.0,
+                                                    None, 0))
+        wd = O.dequantize_tensor(O.GGML_Q4_0, blocks, N16 * K).reshape(N16, K).astype(np.float64)
+        ref = a.astype(np.float64) @ wd.T
+        what = "hilo q4_0 tiles case %d M=%d K=%d N=%d" % (case, M, K, N16)
+        assert err(out.data, ref) <= TOL_HILO, what
+        assert elem(out.data, ref, what) <= ELEM_HILO, what
+        for b in (src, nib, dsc):
+            device.release_buffer(b)
