@@ -507,19 +507,46 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
                        seg_count<NW>(P::PRY, wave) + seg_count<NW>(P::SUY, wave);
 
   // one padded segment: per 16-column tile a run of TPB bytes at plane +
-  // tile_off(tg); lanes past the segment load the last word again (into the pad)
-  auto segment = [&](uint8_t* dst, int bytes, int TPB, auto src_of) {
-    const uint32_t ni = (uint32_t)bytes / 256;
-    for (uint32_t j = wave; j < ni; j += NW) {
-      uint32_t off = j * 256 + lane * 4;
+  // tile_off(tg); lanes past the segment load the last word again (into the
+  // pad).  Each lane's source of its j-th instruction is formed once, for
+  // stage 0; a stage adds the plane's stride (per-stage address arithmetic
+  // was ~11 VALU per instruction in a VALU-bound loop)
+  constexpr uint32_t SEGJ = (uint32_t)(P::NIB / 256 + NW - 1) / NW;  // most instructions of any segment per wave
+  static_assert((uint32_t)(P::HBY / 256 + NW - 1) / NW <= SEGJ && (uint32_t)(P::PRY / 256 + NW - 1) / NW <= SEGJ &&
+                    (uint32_t)(P::SUY / 256 + NW - 1) / NW <= SEGJ,
+                "the nibble segment is the longest");
+  auto seg_src = [&](const uint8_t* (&src)[SEGJ], int bytes, int TPB, auto src_of) {
+#pragma unroll
+    for (uint32_t jj = 0; jj < SEGJ; jj++) {
+      uint32_t off = (wave + jj * NW) * 256 + lane * 4;
       const uint32_t real = (uint32_t)(BN / 16) * TPB;
       off = off < real ? off : real - 4;
       const uint32_t tt = off / TPB, w = off % TPB;
       uint32_t tg = n0 / 16 + tt;
       tg = tg < NT16 ? tg : NT16 - 1;
-      dma<4>(src_of(tg) + w, (lds_ptr_t)(dst + j * 256));
+      src[jj] = src_of(tg) + w;
+      (void)bytes;
     }
   };
+  auto segment = [&](uint8_t* dst, int bytes, const uint8_t* const (&src)[SEGJ], size_t stage_off) {
+    const uint32_t ni = (uint32_t)bytes / 256;
+#pragma unroll
+    for (uint32_t jj = 0; jj < SEGJ; jj++) {
+      const uint32_t j = wave + jj * NW;
+      if (j < ni) dma<4>(src[jj] + stage_off, (lds_ptr_t)(dst + j * 256));
+    }
+  };
+  const uint8_t* srcN[SEGJ];
+  const uint8_t* srcH[SEGJ];
+  const uint8_t* srcP[SEGJ];
+  const uint8_t* srcS[SEGJ];
+  if constexpr (FMT != WF_Q4S) {
+    seg_src(srcN, P::NIB, 512, [&](uint32_t tg) { return B + ((size_t)tg * G * 16) * 16; });
+    if (GF::HB) seg_src(srcH, P::HBY, 32 * GF::HB, [&](uint32_t tg) { return hbp + ((size_t)tg * G * 16) * GF::HB; });
+    seg_src(srcP, P::PRY, 32 * GF::PRM, [&](uint32_t tg) { return prp + ((size_t)tg * G * 16) * GF::PRM; });
+    if (GF::SUP)
+      seg_src(srcS, P::SUY, 16 * GF::SUP, [&](uint32_t tg) { return sup + ((size_t)tg * (G / 8) * 16) * GF::SUP; });
+  }
 
   // DMA of stage s (absolute) into buffers (as, bs)
   auto issue = [&](uint32_t s, uint8_t* as, uint8_t* bs) {
@@ -543,16 +570,11 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
         dma<4>(B + (a < lim ? a : lim), (lds_ptr_t)(bs + j * 256));
       }
     } else {
-      const size_t g0 = 2 * s;
-      segment(bs, P::NIB, 512, [&](uint32_t tg) { return B + (((size_t)tg * G + g0) * 16) * 16; });
-      if (GF::HB)
-        segment(bs + P::NIB, P::HBY, 32 * GF::HB,
-                [&](uint32_t tg) { return hbp + (((size_t)tg * G + g0) * 16) * GF::HB; });
-      segment(bs + P::NIB + P::HBY, P::PRY, 32 * GF::PRM,
-              [&](uint32_t tg) { return prp + (((size_t)tg * G + g0) * 16) * GF::PRM; });
-      if (GF::SUP)
-        segment(bs + P::NIB + P::HBY + P::PRY, P::SUY, 16 * GF::SUP,
-                [&](uint32_t tg) { return sup + (((size_t)tg * (G / 8) + g0 / 8) * 16) * GF::SUP; });
+      const size_t g0 = 2 * s;  // a stage is two 32-row groups
+      segment(bs, P::NIB, srcN, g0 * 16 * 16);
+      if (GF::HB) segment(bs + P::NIB, P::HBY, srcH, g0 * 16 * GF::HB);
+      segment(bs + P::NIB + P::HBY, P::PRY, srcP, g0 * 16 * GF::PRM);
+      if (GF::SUP) segment(bs + P::NIB + P::HBY + P::PRY, P::SUY, srcS, (g0 / 8) * 16 * GF::SUP);
     }
   };
 
