@@ -393,15 +393,16 @@ DEF_GEMM_FMT(q6kt, GT_Q6K)
 // the weights kept in LDS as their raw records -- dequantized in registers
 // right before the MFMAs.  Per stage of 64 K: A rows (f16, 16-byte chunks
 // XOR-swizzled by row through the choice of each lane's source), weight
-// records of the tile's BN columns for 2 groups (Q4S 24 B, Q4_0 tiles 16 B
-// nibbles + 2 B d).  The A operand's 8-element chunks are in the slot order
+// planes of the tile's BN columns for 2 groups (Q4_0 tiles: 16 B of
+// nibbles + 2 B d per record; the other tile formats add their high-bit and
+// parameter planes).  The A operand's 8-element chunks are in the slot order
 // {0,4,1,5,2,6,3,7} (smith_gemm_prep_a_perm), the order in which a nibble
 // dword converts to f16 with 4 bit-inserts (exponent bias 1024 + q for low
 // nibbles, 64 + q for high): both operands permuted alike leave the dot
 // product unchanged.  Q4_0: w = (h - bias - 8) * d in packed f16 (q - 8
-// exact, one rounding); Q4S: w = fma(h, s, c) in f32 with c = -s*(z + bias),
-// one f16 rounding.  The loop is unrolled by the ring size so every LDS
-// access names its stage buffer at compile time (precise vmcnt waits).
+// exact, one rounding).  The loop is unrolled by the ring size so every LDS
+// access names its stage buffer at compile time.  (Q4S records take the
+// register-staged kernel above: converted per wave here they were slower.)
 // ---------------------------------------------------------------------------
 template <int BYTES_PER_WAVE>
 struct DmaUnit {  // dwordx4 or dword loads splitting a wave's bytes evenly (LDS slot = lane * size)
@@ -439,7 +440,7 @@ struct G2 {
   using GF = GtFmt<FMT>;
   static constexpr int NW = (BM / WM) * (BN / WN);
   static constexpr int A_BYTES = BM * 128;
-  static constexpr int NIB = FMT == WF_Q4S ? BN * 48 : BN * 32;  // Q4S: whole 24 B records
+  static constexpr int NIB = BN * 32;  // nibbles of 2 groups
   static constexpr int HBY = pad256(BN * 2 * GF::HB);
   static constexpr int PRY = GF::TILES ? pad256(BN * 2 * GF::PRM) : 0;
   static constexpr int SUY = pad256(BN * GF::SUP);
@@ -477,6 +478,7 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
                                           float* __restrict__ ws, uint32_t sps) {
   using P = G2<FMT, BM, BN, WM, WN>;
   using GF = GtFmt<FMT>;
+  static_assert(GF::TILES, "tile-plane formats only");
   constexpr int NW = P::NW, WAVES_N = BN / WN;
   constexpr int TM = WM / 16, TN = WN / 16;
   __shared__ __attribute__((aligned(1024))) uint8_t As0[P::A_BYTES], As1[P::A_BYTES], As2[P::A_BYTES];
@@ -540,7 +542,7 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
   const uint8_t* srcH[SEGJ];
   const uint8_t* srcP[SEGJ];
   const uint8_t* srcS[SEGJ];
-  if constexpr (FMT != WF_Q4S) {
+  {
     seg_src(srcN, P::NIB, 512, [&](uint32_t tg) { return B + ((size_t)tg * G * 16) * 16; });
     if (GF::HB) seg_src(srcH, P::HBY, 32 * GF::HB, [&](uint32_t tg) { return hbp + ((size_t)tg * G * 16) * GF::HB; });
     seg_src(srcP, P::PRY, 32 * GF::PRM, [&](uint32_t tg) { return prp + ((size_t)tg * G * 16) * GF::PRM; });
@@ -560,22 +562,11 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
       const uint32_t m = m0 + row < M ? m0 + row : M - 1;
       dma<P::UA::U>(A16 + (size_t)m * K + k0 + 8 * c + ci, (lds_ptr_t)(as + (wave * P::UA::N + q) * 64 * P::UA::U));
     }
-    if constexpr (FMT == WF_Q4S) {
-      const uint32_t ni = P::NIB / 256;
-      for (uint32_t j = wave; j < ni; j += NW) {
-        const uint32_t off = j * 256 + lane * 4;
-        const uint32_t g2 = off / (BN * 24), w = off % (BN * 24);
-        size_t a = ((size_t)(2 * s + g2) * N + n0) * 24 + w;
-        const size_t lim = (size_t)G * N * 24 - 4;
-        dma<4>(B + (a < lim ? a : lim), (lds_ptr_t)(bs + j * 256));
-      }
-    } else {
-      const size_t g0 = 2 * s;  // a stage is two 32-row groups
-      segment(bs, P::NIB, srcN, g0 * 16 * 16);
-      if (GF::HB) segment(bs + P::NIB, P::HBY, srcH, g0 * 16 * GF::HB);
-      segment(bs + P::NIB + P::HBY, P::PRY, srcP, g0 * 16 * GF::PRM);
-      if (GF::SUP) segment(bs + P::NIB + P::HBY + P::PRY, P::SUY, srcS, (g0 / 8) * 16 * GF::SUP);
-    }
+    const size_t g0 = 2 * s;  // a stage is two 32-row groups
+    segment(bs, P::NIB, srcN, g0 * 16 * 16);
+    if (GF::HB) segment(bs + P::NIB, P::HBY, srcH, g0 * 16 * GF::HB);
+    segment(bs + P::NIB + P::HBY, P::PRY, srcP, g0 * 16 * GF::PRM);
+    if (GF::SUP) segment(bs + P::NIB + P::HBY + P::PRY, P::SUY, srcS, (g0 / 8) * 16 * GF::SUP);
   };
 
   f32x4 acc[TM][TN];
@@ -599,21 +590,7 @@ __device__ __forceinline__ void gemm2_body(const _Float16* __restrict__ A16, con
       for (int j = 0; j < TN; j++) {
         const uint32_t col = wn * WN + j * 16 + r16;
         u32x4 u;
-        if constexpr (FMT == WF_Q4S) {
-          const uint8_t* rec = bs + (kk * BN + col) * 24;
-          const uint32_t x = *(const uint32_t*)(rec + 4 * kq);
-          const float2 sz = *(const float2*)(rec + 16);
-          const uint32_t y = x >> 8;
-          const uint32_t h[4] = {(x & 0x000F000Fu) | 0x64006400u, (x & 0x00F000F0u) | 0x54005400u,
-                                 (y & 0x000F000Fu) | 0x64006400u, (y & 0x00F000F0u) | 0x54005400u};
-          const float clo = -sz.x * (sz.y + 1024.0f), chi = -sz.x * (sz.y + 64.0f);
-#pragma unroll
-          for (int d = 0; d < 4; d++) {
-            const h2 hv = __builtin_bit_cast(h2, h[d]);
-            const float c = (d & 1) ? chi : clo;
-            u[d] = pack_h2(__builtin_fmaf((float)hv.x, sz.x, c), __builtin_fmaf((float)hv.y, sz.x, c));
-          }
-        } else {
+        {
           const uint32_t tt = col / 16, cc = col % 16;
           const uint32_t ri = (tt * 2 + kk) * 16 + cc;  // record within the stage, tile order
           const uint32_t x = *(const uint32_t*)(bs + ri * 16 + 4 * kq);
