@@ -86,7 +86,7 @@ class Weights:
         D.sync()
 
 
-def time_steps(D, step, steps, warmup, rotation=1, graph=False):
+def time_steps(D, step, steps, warmup, rotation=1, graph=False, probe=()):
     """ms per step over exactly `steps` calls, HIP events on the library
     stream around the timed region, and the number of kernel launches one
     step makes (counted in a separate, untimed pass).  graph=True: the
@@ -123,9 +123,18 @@ def time_steps(D, step, steps, warmup, rotation=1, graph=False):
         D.lib.smith_graph_destroy(g)
     D.profile_kernels(True)
     step(0)
-    _, launches = D.profile_read("")
+    # which of the `probe` kernel names (longest first: prefixes) one step launched
+    kernel, launches = None, 0
+    for name in probe:
+        _, k = D.profile_read(name)
+        if k:
+            kernel = kernel or name
+            launches += k
+    _, rest = D.profile_read("")
+    launches += rest
     D.profile_kernels(False)
-    return ms / steps, {"launches_per_step": launches, "steps_timed": steps, "graph": g is not None}
+    return ms / steps, {"launches_per_step": launches, "steps_timed": steps, "graph": g is not None,
+                        "kernel": kernel}
 
 
 _Q4S_CACHE = {}
@@ -138,7 +147,7 @@ def q4s_weights(D, S, prng, K, N):
     return _Q4S_CACHE[(K, N)]
 
 
-def bench_q4s(D, S, prng, M, K, N, steps, warmup, graph=False):
+def bench_q4s(D, S, prng, M, K, N, steps, warmup, graph=False, probe=()):
     W = q4s_weights(D, S, prng, K, N)
     a = S.tensor(prng.randn((M, K), 0))
     out = S.create([M, N])
@@ -149,7 +158,7 @@ def bench_q4s(D, S, prng, M, K, N, steps, warmup, graph=False):
     def step(i):
         D.lib.smith_matmul_q4(ctx, a.buffer, bufs[i % len(bufs)], out.buffer, M, N, K, G)
 
-    ms, kt = time_steps(D, step, steps, warmup, rotation=len(bufs), graph=graph)
+    ms, kt = time_steps(D, step, steps, warmup, rotation=len(bufs), graph=graph, probe=probe)
     return ms, kt, alg_bytes(q4s_bytes(K, N), M, K, N)
 
 
@@ -171,7 +180,7 @@ def bench_q8(D, S, prng, M, K, N, steps, warmup, graph=False):
     return ms, kt, alg_bytes(q8_bytes(K, N), M, K, N)
 
 
-def bench_q40(D, S, prng, M, K, N, steps, warmup, graph=False):
+def bench_q40(D, S, prng, M, K, N, steps, warmup, graph=False, probe=()):
     """GGUF Q4_0 blocks as the GGUF decode path holds them: nibble and scale
     planes in 16-column tile-major order (smith_repack_q4_0_t_into), through
     smith_linear_q4_0_t (the same GEMV kernels as matmulQ4 for M <= 32)."""
@@ -191,7 +200,7 @@ def bench_q40(D, S, prng, M, K, N, steps, warmup, graph=False):
         j = i % len(W.bufs)
         D.lib.smith_linear_q4_0_t(ctx, a.buffer, W.bufs[j], W.extra[j][0], out.buffer, M, N, K, None, 0.0, None, 0)
 
-    ms, kt = time_steps(D, step, steps, warmup, rotation=len(W.bufs), graph=graph)
+    ms, kt = time_steps(D, step, steps, warmup, rotation=len(W.bufs), graph=graph, probe=probe)
     for b in W.bufs[1:]:
         D.release_buffer(b)
     for eb, _ in W.extra[1:]:
@@ -509,6 +518,63 @@ def stream_floor_us(D, nbytes, steps=100):
     return round(us, 3)
 
 
+# The decode GEMV variants of configs 1-3: (name suffix, record-read floor
+# kernel, threads, grid (N, G) -> (GX, GY)); names longest first (probe
+# prefixes), as the bridge names its launches
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+GEMV_VARIANTS = [
+    ("qgemv1_%s_m1_k128_c2", "c2s4w8", 512, lambda N, G: (_cdiv(N, 32), _cdiv(G, 128))),
+    ("qgemv1_%s_m1_k128", "c1s4w8", 512, lambda N, G: (_cdiv(N, 16), _cdiv(G, 128))),
+    ("qgemv5_%s_m%d_k32c4", "c4s1w8", 512, lambda N, G: (_cdiv(N, 64), _cdiv(G, 32))),
+    ("qgemv5_%s_m%d_k64c2", "c2s1w16", 1024, lambda N, G: (_cdiv(N, 32), _cdiv(G, 64))),
+    ("qgemv5_%s_m%d_k32", "c1s1w8", 512, lambda N, G: (_cdiv(N, 16), _cdiv(G, 32))),
+    ("qgemv5_%s_m%d_w16", "c1s2w16", 1024, lambda N, G: (_cdiv(N, 16), 1)),
+]
+
+
+def gemv_probe(tag, M):
+    """Kernel names one config-3 step may launch (prefixes, longest first)."""
+    return [_variant_name(fmt, tag, M) for fmt, _, _, _ in GEMV_VARIANTS
+            if (M == 1) == fmt.startswith("qgemv1")]
+
+
+def _bucket(M):
+    return 4 if M <= 4 else 8 if M <= 8 else 16 if M <= 16 else 32
+
+
+def _variant_name(fmt, tag, M):
+    return "smith_" + (fmt % tag if fmt.startswith("qgemv1") else fmt % (tag, _bucket(M)))
+
+
+def record_floor_us(D, bufs, tag, kernel, M, K, N, steps=100):
+    """Per-launch us of the launched GEMV's record loads alone (its grid,
+    lanes and records; no math, no split-K finish), graph-replayed over the
+    rotated zero buffers `bufs`."""
+    G = K // 32
+    for fmt, suffix, threads, grid in GEMV_VARIANTS:
+        if _variant_name(fmt, tag, M) == kernel:
+            gx, gy = grid(N, G)
+            out = D.alloc(256)
+            D.check(D.lib.smith_fill_zero(D.ctx(), out, 256))
+            n = N | (G << 20) | (gx << 40)
+            us = floor_us("floor_rec_%s_%s" % (tag, suffix), bufs, n, out, gx * gy, threads, steps)
+            D.release_buffer(out)
+            return round(us, 3)
+    raise RuntimeError("no record floor for %s" % kernel)
+
+
+def _rotated_zeros(D, nbytes):
+    nbytes = -(-nbytes // 16) * 16
+    bufs = [D.alloc(nbytes) for _ in range(max(2, -(-ROTATE_BYTES // nbytes)))]
+    for b in bufs:
+        D.check(D.lib.smith_fill_zero(D.ctx(), b, nbytes))
+    D.sync()
+    return bufs
+
+
 def _sweep_point(ms, nbytes, launches, floor):
     us = ms * 1e3
     return {"GBps": round(nbytes / ms / 1e6, 1), "pct_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 2),
@@ -519,7 +585,9 @@ def _sweep_point(ms, nbytes, launches, floor):
 def bench_sweeps(D, S, prng):
     """Config 2 and the config-3 sweeps (Q4S records and GGUF Q4_0 blocks),
     each point graph-replayed, with the streaming-read floor of its weight
-    bytes (stream_read_us; over_stream_read = step / floor)."""
+    bytes (stream_read_us; over_stream_read = step / floor) and the
+    launched kernel's record loads alone with its grid (record_read_us,
+    over_record_read)."""
     eager = os.environ.get("SMITH_BENCH_EAGER") == "1"  # traced runs: no floor graphs
     floor = (lambda nbytes: float("nan")) if eager else (lambda nbytes: stream_floor_us(D, nbytes))
     configs = {}
@@ -528,24 +596,28 @@ def bench_sweeps(D, S, prng):
     configs["cfg2_q8_gemv_M1_K4096_N14336"] = _sweep_point(ms8, b8, kt8["launches_per_step"],
                                                            floor(q8_bytes(4096, 14336)))
     log("cfg2:", configs["cfg2_q8_gemv_M1_K4096_N14336"])
-    sweep = {}
-    for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
-        for M in (1, 4, 8, 16, 32):
-            if M == 1:
-                fl = floor(q4s_bytes(Kk, Nn))
-            msx, ktx, bx = bench_q4s(D, S, prng, M, Kk, Nn, sub, 5, graph=True)
-            sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = _sweep_point(msx, bx, ktx["launches_per_step"], fl)
-    configs["cfg3_q4s_batched_decode"] = sweep
-    log("cfg3:", json.dumps(sweep))
-    sweep40 = {}  # the same sweep on GGUF Q4_0 blocks (18 B per 32 weights, tile-major planes)
-    for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
-        for M in (1, 4, 8, 16, 32):
-            if M == 1:
-                fl = floor(q40_bytes(Kk, Nn))
-            msx, ktx, bx = bench_q40(D, S, prng, M, Kk, Nn, sub, 5, graph=True)
-            sweep40["M%d_N%d_K%d" % (M, Nn, Kk)] = _sweep_point(msx, bx, ktx["launches_per_step"], fl)
-    configs["cfg3_q4_0_batched_decode"] = sweep40
-    log("cfg3 q4_0:", json.dumps(sweep40))
+    for tag, bench_fn, nbytes_fn, key in (("q4s", bench_q4s, q4s_bytes, "cfg3_q4s_batched_decode"),
+                                          ("q40t", bench_q40, q40_bytes, "cfg3_q4_0_batched_decode")):
+        # (the same sweep on GGUF Q4_0 blocks: 18 B per 32 weights, tile-major planes)
+        sweep = {}
+        for (Nn, Kk) in [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]:
+            fl = floor(nbytes_fn(Kk, Nn))
+            # the record floors read zeros laid out as the kernel's weight (Q4_0:
+            # nibble plane then scale plane)
+            rbufs = None if eager else _rotated_zeros(D, nbytes_fn(Kk, Nn))
+            for M in (1, 4, 8, 16, 32):
+                msx, ktx, bx = bench_fn(D, S, prng, M, Kk, Nn, sub, 5, graph=True, probe=gemv_probe(tag, M))
+                pt = _sweep_point(msx, bx, ktx["launches_per_step"], fl)
+                pt["kernel"] = ktx["kernel"]
+                if rbufs is not None and ktx["kernel"]:
+                    rr = record_floor_us(D, rbufs, tag, ktx["kernel"], M, Kk, Nn)
+                    pt["record_read_us"] = rr
+                    pt["over_record_read"] = round(msx * 1e3 / rr, 3)
+                sweep["M%d_N%d_K%d" % (M, Nn, Kk)] = pt
+            for b in rbufs or ():
+                D.release_buffer(b)
+        configs[key] = sweep
+        log(key + ":", json.dumps(sweep))
     return configs
 
 

@@ -95,3 +95,62 @@ extern "C" __global__ __launch_bounds__(512) void floor_q40t_record_read(const u
   for (int s = 0; s < 4; s++) acc ^= q[s].x ^ q[s].y ^ q[s].z ^ q[s].w ^ sb[s];
   if (acc == 0x9e3779b9u) out[0] = acc;
 }
+
+// The record loads alone of the batched and single-row GEMVs, with the
+// kernel's grid and lanes: workgroup (bx, by) of GX x GY (launched as one
+// dimension, b = by * GX + bx), wave wk, lane (c, j) loads the record of
+// column bx * 16 CT + 16 ct + c in group by * KB + wk * 4S + 4 st + j for
+// every step st < S and column tile ct < CT (clamped into range), as
+// smith_qgemv1 / smith_qgemv5 do.  n packs N (bits 0-19), the group count G
+// (20-39) and GX (40-59).
+template <int CT, int S, int WK, bool Q40T>
+__device__ __forceinline__ void rec_read(const uint8_t* __restrict__ B, uint64_t n, uint32_t* out) {
+  const uint32_t N = (uint32_t)(n & 0xFFFFF), G = (uint32_t)((n >> 20) & 0xFFFFF), GX = (uint32_t)(n >> 40);
+  const uint32_t bx = blockIdx.x % GX, by = blockIdx.x / GX;
+  const uint32_t lane = threadIdx.x & 63, wk = threadIdx.x >> 6, c = lane & 15, j = lane >> 4;
+  constexpr uint32_t KB = 4 * S * WK, BC = 16 * CT;
+  const uint16_t* D = (const uint16_t*)(B + (size_t)N * G * 16);  // Q4_0 tile planes: nibbles, then scales
+  u32x4 q[S][CT];
+  uint32_t t[S][CT];
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+      uint32_t g = by * KB + wk * 4 * S + 4 * st + j, col = bx * BC + ct * 16 + c;
+      g = g < G ? g : G - 1;
+      col = col < N ? col : N - 1;
+      if (Q40T) {
+        const size_t rec = ((size_t)(col / 16) * G + g) * 16 + col % 16;
+        q[st][ct] = *(const u32x4*)(B + rec * 16);
+        t[st][ct] = D[rec];
+      } else {
+        const uint8_t* p = B + ((size_t)g * N + col) * 24;
+        q[st][ct] = *(const u32x4*)p;
+        const uint2 sz = *(const uint2*)(p + 16);
+        t[st][ct] = sz.x ^ sz.y;
+      }
+    }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int st = 0; st < S; st++)
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) acc ^= q[st][ct].x ^ q[st][ct].y ^ q[st][ct].z ^ q[st][ct].w ^ t[st][ct];
+  if (acc == 0x9e3779b9u) out[0] = acc;
+}
+
+#define DEF_REC_READ(NAME, CT, S, WK)                                                                    \
+  extern "C" __global__ __launch_bounds__(64 * WK) void floor_rec_q4s_##NAME(const uint8_t* __restrict__ B, \
+                                                                           uint64_t n, uint32_t* out) {    \
+    rec_read<CT, S, WK, false>(B, n, out);                                                               \
+  }                                                                                                      \
+  extern "C" __global__ __launch_bounds__(64 * WK) void floor_rec_q40t_##NAME(const uint8_t* __restrict__ B, \
+                                                                            uint64_t n, uint32_t* out) {   \
+    rec_read<CT, S, WK, true>(B, n, out);                                                                \
+  }
+// qgemv1 k128 (one / two column tiles per wave), qgemv5 w16 / k32 / k32c4 / k64c2
+DEF_REC_READ(c1s4w8, 1, 4, 8)
+DEF_REC_READ(c2s4w8, 2, 4, 8)
+DEF_REC_READ(c1s2w16, 1, 2, 16)
+DEF_REC_READ(c1s1w8, 1, 1, 8)
+DEF_REC_READ(c4s1w8, 4, 1, 8)
+DEF_REC_READ(c2s1w16, 2, 1, 16)

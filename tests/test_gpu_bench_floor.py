@@ -31,3 +31,28 @@ def test_floor_kernels_run_and_write_nothing():
         bench.floor_us("no_such_kernel", bufs, 16, out, 1, 64, 1)
     for b in bufs + [out]:
         device.release_buffer(b)
+
+
+def test_same_grid_record_floors_stay_in_range():
+    """The record-read floors of every batched / single-row GEMV variant
+    (bench.GEMV_VARIANTS: the kernel's grid, lanes and clamped records) on a
+    small weight of each layout: positive times, nothing written."""
+    K, N = 1024, 136  # 32 groups; N not a multiple of the 64-column blocks
+    G = K // 32
+    out = device.alloc(256)
+    device.check(device.lib.smith_fill_zero(device.ops_ctx(), out, 256))
+    for tag, nbytes in (("q4s", bench.q4s_bytes(K, N)), ("q40t", N // 16 * 16 * G * 18)):
+        n_cols = N if tag == "q4s" else N // 16 * 16
+        bufs = [device.alloc(nbytes) for _ in range(2)]
+        for b in bufs:
+            device.check(device.lib.smith_fill_zero(device.ops_ctx(), b, nbytes))
+        device.sync()
+        for fmt, suffix, threads, grid in bench.GEMV_VARIANTS:
+            gx, gy = grid(n_cols, G)
+            n = n_cols | (G << 20) | (gx << 40)
+            us = bench.floor_us("floor_rec_%s_%s" % (tag, suffix), bufs, n, out, gx * gy, threads, 4)
+            assert us > 0, (tag, suffix)
+        for b in bufs:
+            device.release_buffer(b)
+    assert not device.download(out, 256, np.uint8).any()
+    device.release_buffer(out)
