@@ -1482,8 +1482,9 @@ __device__ __forceinline__ void qgemv4_body(const float* __restrict__ A, const u
 // from registers; LDS holds only the MR live rows:
 //   fragL[group][kslice][vrow], vrow = m (hi or plain) or MR + m (lo).
 // The record operands have their exponent-bias offsets subtracted in f16
-// (exact), so the MFMA yields sum(a * q); the per-(group, row) sums S =
-// sum(a) of the f16 operand values for the zero term: for the hi/lo rows
+// (exact; for Q4_0 its zero point 8 too), so the MFMA yields sum(a * q)
+// (Q4_0: sum(a * (q - 8))); Q4S needs the per-(group, row) sums S =
+// sum(a) of the f16 operand values for its zero term: for the hi/lo rows
 // (M <= 8) formed during the conversion (v_dot2_f32_f16 against ones over a
 // lane's 8 values, then the lane quad of the row's four K slices by DPP) and
 // kept in LDS, where each lane reads the four of its output rows with one
@@ -1509,7 +1510,9 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   static_assert(!HILO || RB == 1, "hi/lo rows fit one row block");
   static_assert(RB <= 2, "at most two row blocks");
   constexpr int VR = HILO ? 2 * MR : MR;   // live virtual rows
-  constexpr bool NEED_S = FMT != FMT_Q8;  // Q4S: - zero * S, Q4_0: - 8 * S
+  // Q4S: - zero * S; Q4_0's zero point 8 comes off with the f16 offsets
+  // (exact), so only Q4S needs the sums
+  constexpr bool NEED_S = FMT == FMT_Q4S;
   // hi/lo rows: S formed during the conversion and kept in LDS; plain rows:
   // S from one more MFMA per group against a ones column (same-box A/B: the
   // LDS sums took M = 4 from 6.31 to 5.99 us at 4096 x 4096, but made the
@@ -1520,7 +1523,7 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   __shared__ u32x4 fragL[KB][4][VR];
   // per (group, MFMA row) sum of the f16 operand values of that row (the S of
   // the zero term, hi/lo buckets): hi row m at m, lo row m at 8 + m
-  __shared__ __attribute__((aligned(16))) float sL[HILO ? KB : 1][16 * RB];
+  __shared__ __attribute__((aligned(16))) float sL[SUM_LDS ? KB : 1][16 * RB];
   // when the fragments and a separate reduction array would not fit the
   // LDS (16 waves x 32 rows), or would keep a second workgroup off the CU
   // while the fragments alone leave room for it (8 waves x 32 rows: 80 /
@@ -1641,7 +1644,7 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   {
     const _Float16 off_q4[8] = {1024, 1024, 64, 64, 1024, 1024, 64, 64};
 #pragma unroll
-    for (int e = 0; e < 8; e++) boff[e] = FMT == FMT_Q8 ? (_Float16)1152 : off_q4[e];
+    for (int e = 0; e < 8; e++) boff[e] = FMT == FMT_Q8 ? (_Float16)1152 : off_q4[e] + (is_q40(FMT) ? 8 : 0);
   }
   f32x4 acc[CT][RB];
 #pragma unroll
@@ -1683,8 +1686,8 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
       rec_kslices<FMT>(wr[st][ct], bf, sv, zv);
 #pragma unroll
       for (int t = 0; t < 4; t++) {
-        const float s = __uint_as_float(sv[t]), z = is_q40(FMT) ? 8.0f : __uint_as_float(zv[t]);
-        const half8 bq = bf[t] - boff;  // the integers q themselves
+        const float s = __uint_as_float(sv[t]), z = __uint_as_float(zv[t]);
+        const half8 bq = bf[t] - boff;  // the integers q (Q4_0: q - 8) themselves
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
           const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t][rb], bq, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
