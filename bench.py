@@ -526,6 +526,7 @@ def _cdiv(a, b):
 
 
 GEMV_VARIANTS = [
+    ("qgemv1_%s_m1_k448w16_pl", "c1s7w16", 1024, lambda N, G: (_cdiv(N, 16), 1)),
     ("qgemv1_%s_m1_k128_c2", "c2s4w8", 512, lambda N, G: (_cdiv(N, 32), _cdiv(G, 128))),
     ("qgemv1_%s_m1_k128", "c1s4w8", 512, lambda N, G: (_cdiv(N, 16), _cdiv(G, 128))),
     ("qgemv5_%s_m%d_k32c4", "c4s1w8", 512, lambda N, G: (_cdiv(N, 64), _cdiv(G, 32))),

@@ -147,8 +147,10 @@ __device__ __forceinline__ void rec_read(const uint8_t* __restrict__ B, uint64_t
                                                                             uint64_t n, uint32_t* out) {   \
     rec_read<CT, S, WK, true>(B, n, out);                                                                \
   }
-// qgemv1 k128 (one / two column tiles per wave), qgemv5 w16 / k32 / k32c4 / k64c2
+// qgemv1 k128 (one / two column tiles per wave) and k448w16, qgemv5 w16 /
+// k32 / k32c4 / k64c2
 DEF_REC_READ(c1s4w8, 1, 4, 8)
+DEF_REC_READ(c1s7w16, 1, 7, 16)
 DEF_REC_READ(c2s4w8, 2, 4, 8)
 DEF_REC_READ(c1s2w16, 1, 2, 16)
 DEF_REC_READ(c1s1w8, 1, 1, 8)

@@ -1122,7 +1122,8 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 
 // Fused M <= 2 variants, named by the groups one block covers: k64 = 4 waves
 // x 4 steps, k96 / k128 / k288 = 8 waves x 3 / 4 / 9 steps (K = 3072, 4096,
-// 9216 in one block); _c2: two 16-column tiles per wave (wide N); _pl:
+// 9216 in one block), k448w16 = 16 waves x 7 steps (K = 14336 in one block,
+// plain single-row matmuls only); _c2: two 16-column tiles per wave (wide N); _pl:
 // plain matmuls; the _c2 and _pls variants read each step's A operands
 // right before its MFMAs (fewer VGPRs: more workgroups per CU, for wide N).
 #define DEF_QGEMV1_FMT(TAG, FMT)                                          \
@@ -1132,6 +1133,7 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64_pl, FMT, 1, 1, 4, 1, 4, true)    \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_pl, FMT, 1, 1, 8, 1, 3, true)    \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k288_pl, FMT, 1, 1, 8, 1, 9, true)   \
+  DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k448w16_pl, FMT, 1, 1, 16, 1, 7, true, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k96_c2_pl, FMT, 1, 2, 8, 1, 3, true, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k128_c2_pl, FMT, 1, 2, 8, 1, 4, true, true) \
   DEF_QGEMV1(smith_qgemv1_##TAG##_m1_k64, FMT, 1, 1, 4, 1, 4)             \

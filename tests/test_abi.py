@@ -54,6 +54,7 @@ def test_code_object_has_kernels():
         need += ["smith_qgemv3_%s_m%d" % (fmt, m) for m in (4, 8, 16, 32)]
         need += ["smith_qgemv1_%s_m%d_k%d" % (fmt, m, k) for m in (1, 2) for k in (64, 96, 128, 288)]
         need += ["smith_qgemv1_%s_m1_k%d_c2" % (fmt, k) for k in (96, 128)]
+        need += ["smith_qgemv1_%s_m1_k448w16_pl" % fmt]
         # every variant qgemv5_chunk can name (bucket x shape)
         need += ["smith_qgemv5_%s_m%d_%s" % (fmt, m, v) for m in (4, 8, 16, 32) for v in ("w16", "k32", "k32c4")
                  if not (m == 32 and v == "w16")]

@@ -252,6 +252,39 @@ def test_config1_q4_0_tile_planes_gemv(M):
         device.release_buffer(b)
 
 
+@pytest.mark.parametrize("N,K", [(4096, 14336), (4004, 9248), (3600, 12288)])
+def test_single_row_long_k_one_block(N, K):
+    """M = 1 with 288 < K/32 <= 448 and 225-320 column tiles: one 16-wave
+    block covers all of K (no split-K finish); ragged N and a K whose last
+    waves hold no groups, Q4S records and Q4_0 tile planes against the
+    float64 product of the decoded weights."""
+    w = prng.randn((K, N), 71, std=0.02)
+    q = S.quantizeQ4(w)
+    dq = O.dequant_q4s(dev_bytes(q), K, N).astype(np.float64)
+    a = prng.randn((1, K), 72)
+    y = S.matmulQ4(S.tensor(a), q).data
+    ref = a.astype(np.float64) @ dq
+    assert err(y, ref) <= TOL_HILO
+    assert elem(y, ref, "q4s M=1 N=%d K=%d" % (N, K)) <= ELEM_M2
+    if N % 16 == 0:
+        wt = prng.randn((N, K), 73, std=0.02)
+        blocks = O.quantize_rows(O.GGML_Q4_0, wt)
+        G = K // 32
+        ctx = device.ops_ctx()
+        src, nib, dsc = device.alloc(blocks.size), device.alloc(N * G * 16), device.alloc(N * G * 2)
+        device.upload(src, blocks)
+        device.check(device.lib.smith_repack_q4_0_t_into(ctx, src, nib, dsc, N, K, 0, 1, N))
+        wd = O.dequantize_tensor(O.GGML_Q4_0, blocks, N * K).reshape(N, K).astype(np.float64)
+        at = S.tensor(a)
+        out = S.create([1, N])
+        device.check(device.lib.smith_linear_q4_0_t(ctx, at.buffer, nib, dsc, out.buffer, 1, N, K, None, 0.0, None, 0))
+        ref = a.astype(np.float64) @ wd.T
+        assert err(out.data, ref) <= TOL_HILO
+        assert elem(out.data, ref, "q4_0 tiles M=1 N=%d K=%d" % (N, K)) <= ELEM_M2
+        for b in (src, nib, dsc):
+            device.release_buffer(b)
+
+
 @pytest.mark.parametrize("N", [1024, 1040])
 def test_q8_chunked_and_window_reads_agree(N):
     """Single-row Q8 matmuls read whole 16-column record runs as 16-byte
