@@ -48,7 +48,8 @@ def test_noalloc_first_call_on_fresh_context():
     c = _fresh_ctx()
     try:
         assert lib.smith_allocated_size(c) == 0
-        for (M, N, K) in ((1, 4096, 14336), (32, 4096, 4096), (64, 1024, 4096)):
+        # (1, 2048, 14336): a 4-way K split (a 4096-column output covers K in one block)
+        for (M, N, K) in ((1, 2048, 14336), (32, 4096, 4096), (64, 1024, 4096)):
             print("noalloc fresh ctx", M, N, K, flush=True)
             w = prng.randn((K, N), 960 + M, std=0.02)
             a = prng.randn((M, K), 970 + M)
