@@ -547,6 +547,29 @@ __device__ __forceinline__ Rec<FMT> load_rec(const uint8_t* __restrict__ B, cons
   return r;
 }
 
+// Weight k of record (g, n) in f32, read byte by byte (0 outside the
+// weight): nibble k in byte k / 2, low nibble first, for Q4S
+// scale * (nibble - zero) (shaders/matmul_q4.metal:21-26) and Q4_0
+// d * (nibble - 8) (src/gguf.js:187-197); Q8_0 d * int8 k.  Only the f32
+// fallback of the GEMVs uses it (few registers, slow), not their MFMA path.
+template <int FMT>
+__device__ __forceinline__ float weight_at(const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
+                                           uint32_t N, uint32_t G, uint32_t g, uint32_t n, uint32_t k) {
+  if (g >= G || n >= N) return 0.f;
+  if (FMT == FMT_Q8) {
+    const uint8_t* p = B + ((size_t)g * N + n) * 34;
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(p[0] | (p[1] << 8)));
+    return d * (float)(int8_t)p[2 + k];
+  }
+  size_t rec = (size_t)g * N + n;
+  if (FMT == FMT_Q40T) rec = ((size_t)(n >> 4) * G + g) * 16 + (n & 15);
+  const uint8_t* p = B + rec * (FMT == FMT_Q4S ? 24 : 16);
+  const uint32_t byte = p[k >> 1];
+  const float nib = (float)((k & 1) ? byte >> 4 : byte & 15u);
+  if (FMT == FMT_Q4S) return *(const float*)(p + 16) * (nib - *(const float*)(p + 20));
+  return (float)__builtin_bit_cast(_Float16, D[rec]) * (nib - 8.0f);
+}
+
 // (x & mask) | (base & ~mask).  Plain C on purpose: the compiler's hazard
 // recognizer does not see VALU work inside inline asm, and a v_bfi_b32
 // written by asm into a dead lane of an in-flight MFMA's result was
@@ -862,6 +885,43 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
         if (FMT == FMT_Q4S) t = __builtin_fmaf(-z, cv[m].y, t);
         acc[ct][m] = __builtin_fmaf(s, t, acc[ct][m]);
       }
+    }
+  }
+
+  // rare: a non-finite partial sum -- an activation beyond the f16 range
+  // (|a| >= 65520) or an infinite / NaN one.  The lane recomputes its
+  // partial sums in f32 from the activations (normalised as above) and the
+  // dequantized records, group by group in K order, as the reference
+  // multiplies; the usual case pays one sum per lane and a branch not taken.
+  {
+    float tot = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+      for (int m = 0; m < MR; m++) tot += acc[ct][m];
+    if (__builtin_amdgcn_ballot_w64(!(__builtin_fabsf(tot) < __builtin_inff())) != 0) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[ct][m] = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+          if ((uint32_t)m >= M) continue;
+          float d = 0.f;
+#pragma unroll 1
+          for (int st = 0; st < S; st++) {
+            const uint32_t g = gw + 4 * st + j;
+#pragma unroll 1
+            for (uint32_t k = g * 32; k < g * 32 + 32 && k < K; k++) {
+              float x = A[(size_t)m * K + k];
+              if (gamma) x = x * rms[m] * gamma[k];
+              d = __builtin_fmaf(x, weight_at<FMT>(B, D, N, G, g, n0 + ct * 16 + c, k % 32), d);
+            }
+          }
+          acc[ct][m] = d;
+        }
     }
   }
 
@@ -1700,6 +1760,43 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
           }
         }
       }
+    }
+  }
+
+  // rare: a non-finite partial sum -- an activation beyond the f16 range
+  // (|a| >= 65520) or an infinite / NaN one.  The wave recomputes its partial
+  // sums in f32 from the activations and the dequantized records, group by
+  // group in K order, as the reference multiplies (one max-free sum per
+  // lane decides; the usual case pays only that and a branch not taken).
+  {
+    float tot = 0.f;
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) tot += acc[ct][rb][i];
+    if (__builtin_amdgcn_ballot_w64(!(__builtin_fabsf(tot) < __builtin_inff())) != 0) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            // MFMA row vr: an activation row (hi/lo: rows 8-15, the lo halves, stay 0)
+            const uint32_t vr = 16 * rb + 4 * j + i;
+            if (vr < (uint32_t)(HILO ? 8 : 16 * RB) && vr < (uint32_t)MR && vr < M) {
+              float d = 0.f;
+#pragma unroll 1
+              for (uint32_t k = gw * 32; k < (gw + 4 * S) * 32 && k < K; k++)
+                d = __builtin_fmaf(A[(size_t)vr * K + k], weight_at<FMT>(B, D, N, G, k / 32, n0 + ct * 16 + c, k % 32), d);
+              acc[ct][rb][i] = d;
+            }
+          }
     }
   }
 

@@ -285,6 +285,71 @@ def test_single_row_long_k_one_block(N, K):
             device.release_buffer(b)
 
 
+def test_gemv_activations_beyond_f16_range():
+    """The GEMVs (M <= 32, K % 32 == 0) feed f16 operands to the MFMAs but
+    keep the reference's f32 range: rows with entries up to 1e6 / 3e30 next
+    to rows of ordinary size (every row bucket, Q4S, Q8 and Q4_0 tile
+    planes) match the float64 product of the decoded weights row by row at
+    the usual bars (a wave whose f16 sums overflow recomputes its part in
+    f32)."""
+    N, K = 512, 1024
+    w = prng.randn((K, N), 81, std=0.02)
+    q4, q8 = S.quantizeQ4(w), S.quantizeQ8(w)
+    dq4 = O.dequant_q4s(dev_bytes(q4), K, N).astype(np.float64)
+    dq8 = O.dequant_q8(dev_bytes(q8), K, N).astype(np.float64)
+    wt = prng.randn((N, K), 82, std=0.02)
+    blocks = O.quantize_rows(O.GGML_Q4_0, wt)
+    G = K // 32
+    ctx = device.ops_ctx()
+    src, nib, dsc = device.alloc(blocks.size), device.alloc(N * G * 16), device.alloc(N * G * 2)
+    device.upload(src, blocks)
+    device.check(device.lib.smith_repack_q4_0_t_into(ctx, src, nib, dsc, N, K, 0, 1, N))
+    wd = O.dequantize_tensor(O.GGML_Q4_0, blocks, N * K).reshape(N, K).astype(np.float64)
+    for M in (1, 2, 4, 8, 16, 32):
+        a = prng.randn((M, K), 83 + M)
+        a[0, 5] = 1.0e6                  # one huge entry, the rest ordinary
+        if M > 1:
+            a[1] *= 3.0e4                # a whole row near the f16 limit
+            a[M - 1, 700:710] = -3.0e30  # far beyond it, beside ordinary rows
+        at = S.tensor(a)
+        out = S.create([M, N])
+        device.check(device.lib.smith_linear_q4_0_t(ctx, at.buffer, nib, dsc, out.buffer, M, N, K, None, 0.0, None, 0))
+        bar = TOL_HILO if M <= 8 else TOL
+        for name, y, ref in (("q4s", S.matmulQ4(at, q4).data, a.astype(np.float64) @ dq4),
+                             ("q8", S.matmulQ8(at, q8).data, a.astype(np.float64) @ dq8),
+                             ("q4_0 tiles", out.data, a.astype(np.float64) @ wd.T)):
+            assert np.isfinite(y).all(), (name, M)
+            for m in range(M):
+                e = err(y[m], ref[m])
+                assert e <= bar, (name, M, m, e)
+    for b in (src, nib, dsc):
+        device.release_buffer(b)
+
+
+def test_gemv_infinite_and_nan_activations():
+    """An infinite or NaN activation gives the reference's non-finite
+    outputs (f32: inf * w is +-inf, or NaN where w = 0; NaN spreads) in its
+    row only, for M = 1 / 4 / 16 / 32; the other rows stay at the usual
+    bars."""
+    N, K = 256, 512
+    w = prng.randn((K, N), 91, std=0.02)
+    q4 = S.quantizeQ4(w)
+    dq4 = O.dequant_q4s(dev_bytes(q4), K, N).astype(np.float64)
+    for M in (1, 4, 16, 32):
+        a = prng.randn((M, K), 92 + M)
+        a[0, 33] = np.inf
+        if M > 1:
+            a[M - 1, 400] = np.nan
+        y = S.matmulQ4(S.tensor(a), q4).data
+        with np.errstate(invalid="ignore", over="ignore"):
+            ref = a.astype(np.float64) @ dq4
+        assert np.array_equal(np.isnan(y), np.isnan(ref)), M
+        assert np.array_equal(np.isposinf(y), np.isposinf(ref)), M
+        assert np.array_equal(np.isneginf(y), np.isneginf(ref)), M
+        for m in range(1, M - 1):
+            assert err(y[m], ref[m]) <= (TOL_HILO if M <= 8 else TOL), (M, m)
+
+
 @pytest.mark.parametrize("N", [1024, 1040])
 def test_q8_chunked_and_window_reads_agree(N):
     """Single-row Q8 matmuls read whole 16-column record runs as 16-byte
