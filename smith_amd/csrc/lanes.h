@@ -34,14 +34,6 @@ __device__ __forceinline__ float max16_lanes(float v) {
   v = max_dpp<0x141>(v);
   return max_dpp<0x140>(v);
 }
-// maximum over the whole wave (64 lanes), in every lane
-__device__ __forceinline__ float max64_lanes(float v) {
-  v = max16_lanes(v);
-  auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-  p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-}
 // v + v of lane ^ 16 / lane ^ 32 (the two rows / halves swapped whole)
 __device__ __forceinline__ float add_xor16(float v) {
   const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
