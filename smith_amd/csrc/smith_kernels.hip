@@ -570,6 +570,29 @@ __device__ __forceinline__ float weight_at(const uint8_t* __restrict__ B, const 
   return (float)__builtin_bit_cast(_Float16, D[rec]) * (nib - 8.0f);
 }
 
+__device__ __forceinline__ bool finite_f32(float v) { return __builtin_fabsf(v) < __builtin_inff(); }
+
+// f32 fallback of the GEMVs: sum over k of the groups [g0, g1) (within K)
+// of a[m][k] (times rms * gamma[k] with an RMSNorm) * weight k of column n,
+// in K order as the reference multiplies.  Taken only for a block sum that
+// came out non-finite from the f16 operands (an activation beyond the f16
+// range, or an infinite / NaN one); slow and small in registers.
+template <int FMT>
+__device__ __forceinline__ float f32_block_sum(const float* __restrict__ A, const uint8_t* __restrict__ B,
+                                               const uint16_t* __restrict__ D, uint32_t N, uint32_t G, uint32_t K,
+                                               uint32_t m, uint32_t n, uint32_t g0, uint32_t g1,
+                                               const float* __restrict__ gamma, float rms) {
+  const uint32_t k1 = g1 * 32 < K ? g1 * 32 : K;
+  float d = 0.f;
+#pragma unroll 1
+  for (uint32_t k = g0 * 32; k < k1; k++) {
+    float x = A[(size_t)m * K + k];
+    if (gamma) x = x * rms * gamma[k];
+    d = __builtin_fmaf(x, weight_at<FMT>(B, D, N, G, k / 32, n, k % 32), d);
+  }
+  return d;
+}
+
 // (x & mask) | (base & ~mask).  Plain C on purpose: the compiler's hazard
 // recognizer does not see VALU work inside inline asm, and a v_bfi_b32
 // written by asm into a dead lane of an in-flight MFMA's result was
@@ -736,6 +759,8 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 
   // 4. activations -> f16 hi/lo fragments + (C1, S) in LDS
   float rms[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) rms[m] = 1.0f;
   if (gamma) {
 #pragma unroll
     for (int m = 0; m < MR; m++) {
@@ -888,43 +913,6 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
     }
   }
 
-  // rare: a non-finite partial sum -- an activation beyond the f16 range
-  // (|a| >= 65520) or an infinite / NaN one.  The lane recomputes its
-  // partial sums in f32 from the activations (normalised as above) and the
-  // dequantized records, group by group in K order, as the reference
-  // multiplies; the usual case pays one sum per lane and a branch not taken.
-  {
-    float tot = 0.f;
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-      for (int m = 0; m < MR; m++) tot += acc[ct][m];
-    if (__builtin_amdgcn_ballot_w64(!(__builtin_fabsf(tot) < __builtin_inff())) != 0) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-        for (int m = 0; m < MR; m++) acc[ct][m] = 0.f;
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-          if ((uint32_t)m >= M) continue;
-          float d = 0.f;
-#pragma unroll 1
-          for (int st = 0; st < S; st++) {
-            const uint32_t g = gw + 4 * st + j;
-#pragma unroll 1
-            for (uint32_t k = g * 32; k < g * 32 + 32 && k < K; k++) {
-              float x = A[(size_t)m * K + k];
-              if (gamma) x = x * rms[m] * gamma[k];
-              d = __builtin_fmaf(x, weight_at<FMT>(B, D, N, G, g, n0 + ct * 16 + c, k % 32), d);
-            }
-          }
-          acc[ct][m] = d;
-        }
-    }
-  }
-
   // 6. sum the four lane groups (different K groups, same column), then the
   //    WK waves of the block in fixed order
 #pragma unroll
@@ -938,6 +926,15 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
   __syncthreads();
   const uint32_t nb = blockIdx.x * BC;
   const uint32_t mrows = M < (uint32_t)MR ? M : MR;
+  // a non-finite block sum (an activation beyond the f16 range, |a| >=
+  // 65520, or an infinite / NaN one) is recomputed in f32 over the block's
+  // K range and stored again over the first store
+  auto f32_sum = [&](uint32_t m, uint32_t n) {
+    float r = 0.f;
+#pragma unroll
+    for (int q = 0; q < MR; q++) r = (uint32_t)q == m ? rms[q] : r;
+    return f32_block_sum<FMT>(A, B, D, N, G, K, m, n, gb, gb + KB, gamma, r);
+  };
   if (ksplit == 1) {
     if (epi == EPI_SWIGLU) {
       for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
@@ -948,7 +945,9 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
           g += red[w][m][cc];
           u += red[w][m][cc + 1];
         }
-        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(g, u);
+        if (n >= N) continue;
+        C[(size_t)m * (N / 2) + n / 2] = silu_mul(g, u);
+        if (!finite_f32(g) || !finite_f32(u)) C[(size_t)m * (N / 2) + n / 2] = silu_mul(f32_sum(m, n), f32_sum(m, n + 1));
       }
     } else {
       for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
@@ -958,6 +957,10 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
         for (int w = 0; w < WK; w++) v += red[w][m][cc];
         if (n >= N) continue;
         C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+        if (!finite_f32(v)) {
+          v = f32_sum(m, n);
+          C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+        }
       }
     }
     return;
@@ -968,6 +971,7 @@ __device__ __forceinline__ void qgemv1_body(const float* __restrict__ A, const u
 #pragma unroll
     for (int w = 0; w < WK; w++) v += red[w][m][cc];
     if (n >= N) continue;
+    if (!finite_f32(v)) v = f32_sum(m, n);
     __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -1763,43 +1767,6 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
     }
   }
 
-  // rare: a non-finite partial sum -- an activation beyond the f16 range
-  // (|a| >= 65520) or an infinite / NaN one.  The wave recomputes its partial
-  // sums in f32 from the activations and the dequantized records, group by
-  // group in K order, as the reference multiplies (one max-free sum per
-  // lane decides; the usual case pays only that and a branch not taken).
-  {
-    float tot = 0.f;
-#pragma unroll
-    for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-      for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) tot += acc[ct][rb][i];
-    if (__builtin_amdgcn_ballot_w64(!(__builtin_fabsf(tot) < __builtin_inff())) != 0) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++) acc[ct][rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ct = 0; ct < CT; ct++)
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            // MFMA row vr: an activation row (hi/lo: rows 8-15, the lo halves, stay 0)
-            const uint32_t vr = 16 * rb + 4 * j + i;
-            if (vr < (uint32_t)(HILO ? 8 : 16 * RB) && vr < (uint32_t)MR && vr < M) {
-              float d = 0.f;
-#pragma unroll 1
-              for (uint32_t k = gw * 32; k < (gw + 4 * S) * 32 && k < K; k++)
-                d = __builtin_fmaf(A[(size_t)vr * K + k], weight_at<FMT>(B, D, N, G, k / 32, n0 + ct * 16 + c, k % 32), d);
-              acc[ct][rb][i] = d;
-            }
-          }
-    }
-  }
-
   // 5. the WK waves of the block in fixed order, then the epilogue or the
   //    cross-block split
   if (ALIAS) __syncthreads();  // every wave is done with the fragments
@@ -1821,18 +1788,31 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
     }
     return v;
   };
+  // a non-finite block sum (an activation beyond the f16 range, |a| >=
+  // 65520, or an infinite / NaN one) is recomputed in f32 over the block's
+  // K range and stored again over the first store
+  auto f32_sum = [&](uint32_t m, uint32_t n) {
+    return f32_block_sum<FMT>(A, B, D, N, G, K, m, n, gb, gb + KB, nullptr, 1.0f);
+  };
   if (ksplit == 1) {
     if (epi == EPI_SWIGLU) {
       for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
         const uint32_t m = e / (BC / 2), cc = 2 * (e % (BC / 2)), n = nb + cc;
-        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(colsum(m, cc), colsum(m, cc + 1));
+        if (n >= N) continue;
+        const float g = colsum(m, cc), u = colsum(m, cc + 1);
+        C[(size_t)m * (N / 2) + n / 2] = silu_mul(g, u);
+        if (!finite_f32(g) || !finite_f32(u)) C[(size_t)m * (N / 2) + n / 2] = silu_mul(f32_sum(m, n), f32_sum(m, n + 1));
       }
     } else {
       for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
         const uint32_t m = e / BC, cc = e % BC, n = nb + cc;
         if (n >= N) continue;
-        const float v = colsum(m, cc);
+        float v = colsum(m, cc);
         C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+        if (!finite_f32(v)) {
+          v = f32_sum(m, n);
+          C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+        }
       }
     }
     return;
@@ -1840,7 +1820,9 @@ __device__ __forceinline__ void qgemv5_body(const float* __restrict__ A, const u
   for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
     const uint32_t m = e / BC, cc = e % BC, n = nb + cc;
     if (n >= N) continue;
-    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(colsum(m, cc)),
+    float v = colsum(m, cc);
+    if (!finite_f32(v)) v = f32_sum(m, n);
+    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
