@@ -38,8 +38,8 @@ ROTATE_BYTES = 400 << 20
 # this kernel (FETCH_SIZE, then WRITE_SIZE, per dispatch), FETCH_SIZE scaled
 # by the factor a plain device copy of known size gives; the profile named in
 # TRAFFIC_SOURCE holds the commands and the figures.
-TRAFFIC_CFG1 = 12766844
-TRAFFIC_CFG1_Q40 = 9631803
+TRAFFIC_CFG1 = 12771509
+TRAFFIC_CFG1_Q40 = 9626116
 TRAFFIC_SOURCE = "profiles/qgemv1_q4s_m1_cfg1_hbm_traffic.md"
 # kernel trace (rocprofv3 --kernel-trace --stats) of the config-1 launches
 KERNEL_TRACE = "profiles/qgemv1_cfg1_kernel_trace.md"
