@@ -363,7 +363,9 @@ int qgemv3_chunk(Ctx* c, Fmt fmt, const float* a, const void* B, const void* D, 
   uint32_t pM = M, pN = N, pG = G;
   const float* pR = ep.resid;
   uint32_t pepi = ep.mode;
-  void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG, &pR, &pepi};
+  const float* pA = a;  // the rows the prep read (normalised when ep.gamma): the f32 fallback's input
+  uint32_t pK = K;
+  void* args[] = {&frag, &cst, &pB, &pD, &pC, &pws, &pcnt, &pM, &pN, &pG, &pR, &pepi, &pA, &pK};
   return launch(c, name, dim3(gx, ksplit), dim3(nthreads), args);
 }
 

@@ -1019,7 +1019,8 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
                                             const uint8_t* __restrict__ B, const uint16_t* __restrict__ D,
                                             float* __restrict__ C, float* __restrict__ ws,
                                             uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
-                                            uint32_t G, const float* __restrict__ R, uint32_t epi) {
+                                            uint32_t G, const float* __restrict__ R, uint32_t epi,
+                                            const float* __restrict__ A, uint32_t K) {
   constexpr int GPW = 4 * S;
   constexpr int BC = 16 * CT * WN;
   constexpr int NT = 64 * WK * WN;
@@ -1152,11 +1153,21 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
     }
     return v;
   };
+  // a non-finite block sum (an activation beyond the f16 range, |a| >=
+  // 65520, or an infinite / NaN one) is recomputed in f32 over the block's
+  // K range from the activations the prep read, and stored again
+  const uint32_t gb = blockIdx.y * WK * GPW;
+  auto f32_sum = [&](uint32_t m, uint32_t n) {
+    return f32_block_sum<FMT>(A, B, D, N, G, K, m, n, gb, gb + WK * GPW, nullptr, 1.0f);
+  };
   if (ksplit == 1) {
     if (epi == EPI_SWIGLU) {
       for (uint32_t e = threadIdx.x; e < mrows * BC / 2; e += NT) {
         uint32_t m = e / (BC / 2), cc = 2 * (e % (BC / 2)), n = nb + cc;
-        if (n < N) C[(size_t)m * (N / 2) + n / 2] = silu_mul(colsum(m, cc), colsum(m, cc + 1));
+        if (n >= N) continue;
+        const float g = colsum(m, cc), u = colsum(m, cc + 1);
+        C[(size_t)m * (N / 2) + n / 2] = silu_mul(g, u);
+        if (!finite_f32(g) || !finite_f32(u)) C[(size_t)m * (N / 2) + n / 2] = silu_mul(f32_sum(m, n), f32_sum(m, n + 1));
       }
     } else {
       for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
@@ -1164,6 +1175,10 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
         if (n >= N) continue;
         float v = colsum(m, cc);
         C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+        if (!finite_f32(v)) {
+          v = f32_sum(m, n);
+          C[(size_t)m * N + n] = epi == EPI_RESID ? R[(size_t)m * N + n] + v : v;
+        }
       }
     }
     return;
@@ -1171,7 +1186,9 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
   for (uint32_t e = threadIdx.x; e < mrows * BC; e += NT) {
     uint32_t m = e / BC, cc = e % BC, n = nb + cc;
     if (n >= N) continue;
-    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(colsum(m, cc)),
+    float v = colsum(m, cc);
+    if (!finite_f32(v)) v = f32_sum(m, n);
+    __hip_atomic_exchange((uint32_t*)ws + ((size_t)blockIdx.y * M + m) * N + n, __float_as_uint(v),
                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   splitk_finish(ws, counters, C, R, epi, M, N, mrows, nb, BC, NT, ksplit, &s_last);
@@ -1180,8 +1197,9 @@ __device__ __forceinline__ void qgemv3_body(const u32x4* __restrict__ frag, cons
 #define DEF_QGEMV3(NAME, FMT, RB, HILO, VPL, CT, S, WK, WN)                                             \
   extern "C" __global__ __launch_bounds__(WK * WN * 64) void NAME(                                       \
       const u32x4* frag, const float2* cst, const uint8_t* B, const uint16_t* D, float* C, float* ws,    \
-      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G, const float* R, uint32_t epi) {            \
-    qgemv3_body<FMT, RB, HILO, VPL, CT, S, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G, R, epi);   \
+      uint32_t* counters, uint32_t M, uint32_t N, uint32_t G, const float* R, uint32_t epi, const float* A, \
+      uint32_t K) {                                                                                      \
+    qgemv3_body<FMT, RB, HILO, VPL, CT, S, WK, WN>(frag, cst, B, D, C, ws, counters, M, N, G, R, epi, A, K); \
   }
 
 // Fused M <= 2 variants, named by the groups one block covers: k64 = 4 waves

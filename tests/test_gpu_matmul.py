@@ -326,6 +326,28 @@ def test_gemv_activations_beyond_f16_range():
         device.release_buffer(b)
 
 
+def test_gemv_beyond_f16_range_ragged_k():
+    """K % 32 != 0 (the prepared-activation batched GEMV, M > 2, and the
+    fused single-row one) with rows beyond the f16 range: the same f32
+    results as the reference, Q4S and Q8, per row at the usual bars."""
+    N, K = 200, 1000
+    w = prng.randn((K, N), 95, std=0.02)
+    q4, q8 = S.quantizeQ4(w), S.quantizeQ8(w)
+    dq4 = O.dequant_q4s(dev_bytes(q4), K, N).astype(np.float64)
+    dq8 = O.dequant_q8(dev_bytes(q8), K, N).astype(np.float64)
+    for M in (1, 4, 16, 32):
+        a = prng.randn((M, K), 96 + M)
+        a[0, 999] = 2.0e5
+        if M > 1:
+            a[M - 1, :40] = -7.0e4
+        at = S.tensor(a)
+        for name, y, ref in (("q4s", S.matmulQ4(at, q4).data, a.astype(np.float64) @ dq4),
+                             ("q8", S.matmulQ8(at, q8).data, a.astype(np.float64) @ dq8)):
+            assert np.isfinite(y).all(), (name, M)
+            for m in range(M):
+                assert err(y[m], ref[m]) <= (TOL_HILO if M <= 8 else TOL), (name, M, m)
+
+
 def test_gemv_infinite_and_nan_activations():
     """An infinite or NaN activation gives the reference's non-finite
     outputs (f32: inf * w is +-inf, or NaN where w = 0; NaN spreads) in its
