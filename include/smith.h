@@ -135,9 +135,10 @@ int smith_quantize_q4(void* ctx, const float* w, void* out, uint32_t K, uint32_t
 int smith_quantize_q8(void* ctx, const float* w, void* out, uint32_t K, uint32_t N);
 
 /* matmulQ4 (src/ops/quantize.js:71-90): out[M,N] = a[M,K] . deq(wq).
- * M <= 32 runs the decode GEMVs, which keep the reference's f32 range (a
- * sum the f16 operands overflow, or an inf / NaN activation, is redone in
- * f32); M >= 64 runs the f16 MFMA GEMM, which needs |a| < 65504. */
+ * M < 64 (or K % 32 != 0) runs the decode GEMVs on 32-row chunks, which
+ * keep the reference's f32 range (a sum the f16 operands overflow, or an
+ * inf / NaN activation, is redone in f32); M >= 64 with K % 32 == 0 runs
+ * the f16 MFMA GEMM, which needs |a| < 65504. */
 int smith_matmul_q4(void* ctx, const float* a, const void* wq, float* out, uint32_t M, uint32_t N,
                     uint32_t K, uint32_t groups);
 
